@@ -1,0 +1,137 @@
+// kvrt_internal.h — launch argument blocks shared by the host runtime
+// (kvrt_runtime.hip) and the kernels (kvrt_kernels.hip).
+//
+// Every block is passed BY VALUE as the kernel argument (kernarg segment),
+// so a launch captures its own copy of slot lists and page-table edits at
+// enqueue time; nothing the host changes afterwards can race the kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kvrt.h"
+
+namespace kvrt {
+
+constexpr int kMaxItems = KVRT_MAX_ITEMS;
+constexpr int kWaves = 4;            // waves per attention workgroup
+constexpr int kPtUpdates = 128;      // page-table edits carried by one launch
+
+// Where the rows of one layer live. Row (slot, head, pos) starts at element
+//   CONTIG: slot*slot_stride + head*head_stride + pos*row_stride
+//   RING:   slot*slot_stride + head*head_stride + (pos % rows)*row_stride
+//   PAGED:  ((page*kv_heads + head)*rows + pos % rows)*D, page = pt[slot][pos / rows]
+// INT8 scales are indexed by the same row number (element offset / D).
+struct KVView {
+    void *k;
+    void *v;
+    float *ks;
+    float *vs;
+    int64_t slot_stride;
+    int64_t head_stride;
+    int64_t row_stride;
+    int32_t rows;        // CONTIG: capacity, RING: ring rows, PAGED: block size
+    int32_t layout;
+    int32_t kv_heads;
+    int32_t block_shift; // PAGED: log2(block size)
+    int32_t *page_table; // PAGED: [n_slots, pt_stride]
+    int32_t pt_stride;
+    int32_t pool_pages;
+};
+
+struct Lengths {
+    int32_t *lens;   // device lengths; entry = lens[slot*stride + offset]
+    int32_t stride;
+    int32_t offset;
+};
+
+struct AppendArgs {
+    KVView kv;
+    Lengths len;
+    const uint16_t *k_src;  // bf16 [n, kv_heads, rows, D] (strided)
+    const uint16_t *v_src;
+    int64_t src_item_stride;
+    int64_t src_head_stride;
+    int64_t src_row_stride;
+    int32_t n_items;
+    int32_t rows;           // Q (append) or S (import)
+    int32_t import_mode;    // 0: pos0 = device length, length += rows
+                            // 1: pos0 = 0, length = rows
+    int32_t keep_from;      // import: rows below this position are not stored
+    int32_t *err;           // device error flag
+    int32_t n_upd;          // page-table edits applied before the writes
+    int32_t upd_idx[kPtUpdates];
+    int32_t upd_val[kPtUpdates];
+    int32_t slots[kMaxItems];
+};
+
+struct GatherArgs {
+    KVView kv;
+    Lengths len;
+    void *out_k;            // [n, kv_heads, lmax, D] bf16 or fp32
+    void *out_v;
+    int64_t out_item_stride, out_head_stride, out_row_stride;
+    void *mask;             // [n, lmax] or null
+    int64_t mask_item_stride;
+    int32_t mask_dtype;
+    int32_t out_fp32;
+    int32_t n_items;
+    int32_t lmax;
+    int32_t window;         // ring default start rule
+    int32_t has_start;
+    int32_t *err;
+    int32_t start[kMaxItems];
+    int32_t slots[kMaxItems];
+};
+
+struct DecodeArgs {
+    KVView kv;
+    Lengths len;
+    const uint16_t *q;      // [n, Hq, Q, D] contiguous
+    uint16_t *out;          // [n, Hq, Q, D] contiguous
+    const uint16_t *k_new;  // fused append: [n, kv_heads, Q, D] contiguous, else null
+    const uint16_t *v_new;
+    float *part_acc;        // [n, kv_heads, n_split, R, D]
+    float2 *part_ml;        // [n, kv_heads, n_split, R]
+    int32_t *err;
+    int32_t n_items;
+    int32_t group;          // Hq / kv_heads
+    int32_t qn;             // Q
+    int32_t window;
+    int32_t n_split;        // wave splits per (item, kv head) = gridDim.x * kWaves
+    int32_t advance;        // merge kernel adds qn to each item's length
+    float scale_log2;       // softmax scale * log2(e)
+    int32_t slots[kMaxItems];
+};
+
+struct SetLenArgs {
+    int32_t *lens;
+    int32_t n;
+    int32_t idx[kPtUpdates];
+    int32_t val[kPtUpdates];
+};
+
+struct CopyRowsArgs {
+    const uint8_t *src;
+    uint8_t *dst;
+    int64_t d0, d1, rows, row_bytes;          // row_bytes multiple of 4
+    int64_t s0, s1, sr;                       // src strides in bytes
+    int64_t t0, t1, tr;                       // dst strides in bytes
+};
+
+// ---- launchers (kvrt_kernels.hip) ----------------------------------------
+hipError_t launch_append(const AppendArgs &a, int head_dim, int dtype, int grid_x, hipStream_t s);
+hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream_t s);
+// Attention over the view with split-K partials, then the merge kernel.
+hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head,
+                         hipStream_t s);
+hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
+hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,
+                            hipStream_t s);
+hipError_t launch_copy_rows(const CopyRowsArgs &a, hipStream_t s);
+hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s);
+
+// Smallest instantiated row tile >= rows (1, 2, 4, 8, 16); 0 if too large.
+int rows_tile(int rows);
+
+}  // namespace kvrt

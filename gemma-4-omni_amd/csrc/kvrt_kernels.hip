@@ -1,0 +1,629 @@
+// kvrt_kernels.hip — gfx950 kernels of the KV hot path.
+//
+//   append_kernel   per-frame K/V append / prefix import into CONTIG, RING or
+//                   PAGED rows (bf16 copy or int8 quantise-on-write)
+//   gather_kernel   ragged N-stream gather into a zero-padded batch + mask
+//   decode_kernel   GQA split-K decode attention, one wave per key split,
+//                   fp32 online softmax, partial (m, l, acc) per split
+//   merge_kernel    deterministic log-sum-exp merge of the splits -> bf16
+//   set_i32_kernel  length / page-table edits carried in the kernarg block
+//   copy_rows_kernel, zero_kernel
+//
+// Every memory-bound loop moves 16 B per lane with consecutive lanes on
+// consecutive addresses (one 1 KiB transaction per wave instruction).
+#include "kvrt_device.h"
+#include "kvrt_internal.h"
+
+namespace kvrt {
+
+constexpr float kNegBig = -1.0e30f;  // running-max start; exp2(kNegBig - m) == 0
+
+// Element offset of the first element of row (slot, head, pos); -1 if the
+// page is unmapped or out of the pool.
+template <int LAYOUT>
+__device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int head, int pos, int D) {
+    if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
+        return slot * v.slot_stride + head * v.head_stride + (int64_t)pos * v.row_stride;
+    } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
+        return slot * v.slot_stride + head * v.head_stride + (int64_t)(pos % v.rows) * v.row_stride;
+    } else {
+        const int lp = pos >> v.block_shift;
+        if (pos < 0 || lp >= v.pt_stride) return -1;
+        const int page = v.page_table[(int64_t)slot * v.pt_stride + lp];
+        if (page < 0 || page >= v.pool_pages) return -1;
+        return (((int64_t)page * v.kv_heads + head) * v.rows + (pos & (v.rows - 1))) * (int64_t)D;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// append / import
+// ---------------------------------------------------------------------------
+// grid (grid_x, n_items), 256 threads. Thread chunk = 8 elements of one row.
+// Append mode runs with grid_x == 1, so the workgroup that advances an item's
+// length is the only one that reads it.
+template <int D, int KDT, int LAYOUT>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    constexpr int LPR = D / 8;
+    const int item = blockIdx.y;
+    const int slot = a.slots[item];
+    if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+        for (int i = threadIdx.x; i < a.n_upd; i += blockDim.x) {
+            const int idx = a.upd_idx[i];
+            if (idx / a.kv.pt_stride == slot) a.kv.page_table[idx] = a.upd_val[i];
+        }
+        __syncthreads();
+    }
+    int32_t *lp = a.len.lens + (int64_t)slot * a.len.stride + a.len.offset;
+    const int pos0 = a.import_mode ? 0 : *lp;
+    const int64_t chunks = (int64_t)a.kv.kv_heads * a.rows * LPR;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += step) {
+        const int seg = (int)(c % LPR);
+        const int64_t rowid = c / LPR;
+        const int r = (int)(rowid % a.rows);
+        const int h = (int)(rowid / a.rows);
+        const int pos = pos0 + r;
+        if (a.import_mode && pos < a.keep_from) continue;  // uniform over the row group
+        const int64_t src = item * a.src_item_stride + h * a.src_head_stride + r * a.src_row_stride + seg * 8;
+        const uint4 kx = *reinterpret_cast<const uint4 *>(a.k_src + src);
+        const uint4 vx = *reinterpret_cast<const uint4 *>(a.v_src + src);
+        bool ok = true;
+        if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) ok = pos < a.kv.rows;
+        const int64_t dst = ok ? row_offset<LAYOUT>(a.kv, slot, h, pos, D) : -1;
+        if (dst < 0) {
+            if (seg == 0) a.err[0] = 1;
+            continue;
+        }
+        if constexpr (KDT == KVRT_BF16) {
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.k) + dst + seg * 8) = kx;
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.v) + dst + seg * 8) = vx;
+        } else {
+            // Symmetric int8 per (token, head): scale = amax / 127,
+            // q = clamp(rne(x / scale), -127, 127); amax == 0 stores zeros.
+            const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
+            const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
+            float kf[8], vf[8];
+            float ka = 0.f, va = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kf[2 * i] = bf16_lo(kw[i]);
+                kf[2 * i + 1] = bf16_hi(kw[i]);
+                vf[2 * i] = bf16_lo(vw[i]);
+                vf[2 * i + 1] = bf16_hi(vw[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ka = fmaxf(ka, fabsf(kf[i]));
+                va = fmaxf(va, fabsf(vf[i]));
+            }
+            ka = group_max<LPR>(ka);
+            va = group_max<LPR>(va);
+            const float ksc = ka / 127.0f;
+            const float vsc = va / 127.0f;
+            uint32_t kq[2] = {0u, 0u}, vq[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                int qk = 0, qv = 0;
+                if (ka > 0.f) qk = (int)fminf(fmaxf(rintf(kf[i] / ksc), -127.f), 127.f);
+                if (va > 0.f) qv = (int)fminf(fmaxf(rintf(vf[i] / vsc), -127.f), 127.f);
+                kq[i >> 2] |= ((uint32_t)(qk & 0xff)) << (8 * (i & 3));
+                vq[i >> 2] |= ((uint32_t)(qv & 0xff)) << (8 * (i & 3));
+            }
+            *reinterpret_cast<uint2 *>(static_cast<int8_t *>(a.kv.k) + dst + seg * 8) = make_uint2(kq[0], kq[1]);
+            *reinterpret_cast<uint2 *>(static_cast<int8_t *>(a.kv.v) + dst + seg * 8) = make_uint2(vq[0], vq[1]);
+            if (seg == 0) {
+                a.kv.ks[dst / D] = ksc;
+                a.kv.vs[dst / D] = vsc;
+            }
+        }
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x == 0) *lp = a.import_mode ? a.rows : pos0 + a.rows;
+}
+
+// ---------------------------------------------------------------------------
+// gather
+// ---------------------------------------------------------------------------
+// grid (chunks, n_items), 256 threads; thread chunk = 8 elements.
+template <int D, int KDT, int LAYOUT>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+    constexpr int LPR = D / 8;
+    const int item = blockIdx.y;
+    const int slot = a.slots[item];
+    const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    int start;
+    if (a.has_start) start = a.start[item];
+    else if (LAYOUT == KVRT_LAYOUT_RING && a.window > 0) start = max(0, L - (a.window - 1));
+    else start = 0;
+    const int valid = max(0, L - start);
+    const int64_t chunks = (int64_t)a.kv.kv_heads * a.lmax * LPR;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += step) {
+        const int seg = (int)(c % LPR);
+        const int64_t rowid = c / LPR;
+        const int j = (int)(rowid % a.lmax);
+        const int h = (int)(rowid / a.lmax);
+        const int64_t o = item * a.out_item_stride + h * a.out_head_stride + j * a.out_row_stride + seg * 8;
+        float kf[8], vf[8];
+        uint4 kx = make_uint4(0, 0, 0, 0), vx = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[i] = vf[i] = 0.f;
+        if (j < valid) {
+            int64_t src = row_offset<LAYOUT>(a.kv, slot, h, start + j, D);
+            if (LAYOUT == KVRT_LAYOUT_CONTIG && start + j >= a.kv.rows) src = -1;
+            if (src < 0) {
+                if (seg == 0) a.err[0] = 1;
+            } else if constexpr (KDT == KVRT_BF16) {
+                kx = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.k) + src + seg * 8);
+                vx = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.v) + src + seg * 8);
+            } else {
+                const uint2 kq = *reinterpret_cast<const uint2 *>(static_cast<const int8_t *>(a.kv.k) + src + seg * 8);
+                const uint2 vq = *reinterpret_cast<const uint2 *>(static_cast<const int8_t *>(a.kv.v) + src + seg * 8);
+                const float ks = a.kv.ks[src / D], vs = a.kv.vs[src / D];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t kw = i < 4 ? kq.x : kq.y, vw = i < 4 ? vq.x : vq.y;
+                    kf[i] = (float)(int8_t)(kw >> (8 * (i & 3))) * ks;
+                    vf[i] = (float)(int8_t)(vw >> (8 * (i & 3))) * vs;
+                }
+            }
+        }
+        if (a.out_fp32) {
+            if constexpr (KDT == KVRT_BF16) {
+                const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w}, vw[4] = {vx.x, vx.y, vx.z, vx.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kf[2 * i] = bf16_lo(kw[i]); kf[2 * i + 1] = bf16_hi(kw[i]);
+                    vf[2 * i] = bf16_lo(vw[i]); vf[2 * i + 1] = bf16_hi(vw[i]);
+                }
+            }
+            float4 *ko = reinterpret_cast<float4 *>(static_cast<float *>(a.out_k) + o);
+            float4 *vo = reinterpret_cast<float4 *>(static_cast<float *>(a.out_v) + o);
+            ko[0] = make_float4(kf[0], kf[1], kf[2], kf[3]);
+            ko[1] = make_float4(kf[4], kf[5], kf[6], kf[7]);
+            vo[0] = make_float4(vf[0], vf[1], vf[2], vf[3]);
+            vo[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
+        } else {
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_k) + o) = kx;
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_v) + o) = vx;
+        }
+    }
+    if (a.mask != nullptr) {
+        for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < a.lmax; j += (int)step) {
+            const bool ok = j < valid;
+            const int64_t mo = item * a.mask_item_stride + j;
+            if (a.mask_dtype == KVRT_BOOL) static_cast<uint8_t *>(a.mask)[mo] = ok ? 1 : 0;
+            else if (a.mask_dtype == KVRT_FP32) static_cast<float *>(a.mask)[mo] = ok ? 0.f : -3.4028234663852886e38f;
+            else static_cast<uint16_t *>(a.mask)[mo] = ok ? (uint16_t)0 : (uint16_t)0xff7f;  // bf16 finfo.min
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention (split-K)
+// ---------------------------------------------------------------------------
+// grid (n_split / kWaves, kv_heads, n_items), 256 threads = kWaves waves.
+// Wave w of workgroup x owns key split s = x*kWaves + w: a contiguous key
+// range. Inside a wave, LPR = D/VEC lanes share one key row (VEC elements =
+// 16 B each) and KPW = 64/LPR key rows are in flight per load instruction.
+// The R rows of a kv head are its g q heads x Q query positions
+// (row r = j*Q + i for q head kvh*g + j, query i).
+template <int D, int R, int KDT, int LAYOUT>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+    constexpr int VEC = (KDT == KVRT_INT8) ? 16 : 8;
+    constexpr int LPR = D / VEC;
+    constexpr int KPW = 64 / LPR;
+    constexpr int U = (R <= 4) ? 8 : (R == 8 ? 4 : 2);
+    constexpr int QW = VEC / 2;  // packed bf16 pairs of q per lane and row
+    static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad head_dim");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane / LPR;
+    const int seg = lane % LPR;
+    const int item = blockIdx.z;
+    const int kvh = blockIdx.y;
+    const int hkv = gridDim.y;
+    const int split = blockIdx.x * kWaves + wave;
+    const int slot = a.slots[item];
+    const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const bool fused = (KDT == KVRT_BF16) && a.k_new != nullptr;
+    int kend = fused ? len + Qn : len;
+    if (LAYOUT == KVRT_LAYOUT_CONTIG && kend > a.kv.rows) {
+        // a length beyond the rows of the view (caller-provided lengths):
+        // clamp the reads and raise the device flag
+        if (threadIdx.x == 0 && blockIdx.x == 0) a.err[0] = 1;
+        kend = a.kv.rows;
+    }
+    const int p0 = kend - Qn;
+    const int kstart = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int nk = max(0, kend - kstart);
+    int chunk = (nk + a.n_split - 1) / a.n_split;
+    chunk = (chunk + KPW - 1) / KPW * KPW;
+    const int ws = kstart + split * chunk;
+    const int we = min(kend, ws + chunk);
+
+    if constexpr (KDT == KVRT_BF16) {
+        // Fused append: workgroup 0 of every (item, kv head) stores the new
+        // rows. No workgroup of this launch reads those cache rows (they are
+        // taken from k_new below); RING rows overwritten here hold positions
+        // older than the window.
+        if (fused && blockIdx.x == 0) {
+            for (int c = threadIdx.x; c < Qn * (D / 8); c += blockDim.x) {
+                const int r = c / (D / 8), sg = c % (D / 8);
+                const int pos = len + r;
+                bool ok = true;
+                if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) ok = pos < a.kv.rows;
+                const int64_t dst = ok ? row_offset<LAYOUT>(a.kv, slot, kvh, pos, D) : -1;
+                if (dst < 0) {
+                    a.err[0] = 1;
+                    continue;
+                }
+                const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 8;
+                *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.k) + dst + sg * 8) =
+                    *reinterpret_cast<const uint4 *>(a.k_new + src);
+                *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.v) + dst + sg * 8) =
+                    *reinterpret_cast<const uint4 *>(a.v_new + src);
+            }
+        }
+    }
+
+    // q rows of this kv head, packed bf16 pairs.
+    uint32_t qw[R][QW];
+    const int hq = hkv * a.group;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r < rows) {
+            const int j = r / Qn, i = r % Qn;
+            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + seg * VEC;
+#pragma unroll
+            for (int t = 0; t < VEC / 8; ++t) {
+                const uint4 x = *reinterpret_cast<const uint4 *>(qp + t * 8);
+                qw[r][4 * t + 0] = x.x; qw[r][4 * t + 1] = x.y;
+                qw[r][4 * t + 2] = x.z; qw[r][4 * t + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < QW; ++t) qw[r][t] = 0u;
+        }
+    }
+    // Per-row visibility bounds: key in [lo_r, hi_r].
+    int hi[R], lo[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int p = p0 + (r % Qn);
+        hi[r] = r < rows ? p : -1;
+        lo[r] = a.window > 0 ? p - a.window + 1 : 0;
+    }
+
+    float m_run[R], l_run[R], acc[R][VEC];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m_run[r] = kNegBig;
+        l_run[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[r][e] = 0.f;
+    }
+
+    const int64_t new_base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * VEC;
+    for (int base = ws; base < we; base += KPW * U) {
+        uint4 kx[U], vx[U];
+        float ksc[U], vsc[U];
+        int key[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            key[u] = base + u * KPW + sub;
+            kx[u] = make_uint4(0, 0, 0, 0);
+            vx[u] = make_uint4(0, 0, 0, 0);
+            ksc[u] = vsc[u] = 0.f;
+            if (key[u] < we) {
+                if (fused && key[u] >= len) {
+                    const int64_t o = new_base + (int64_t)(key[u] - len) * D;
+                    kx[u] = *reinterpret_cast<const uint4 *>(a.k_new + o);
+                    vx[u] = *reinterpret_cast<const uint4 *>(a.v_new + o);
+                } else {
+                    const int64_t o = row_offset<LAYOUT>(a.kv, slot, kvh, key[u], D);
+                    if (o >= 0) {
+                        if constexpr (KDT == KVRT_BF16) {
+                            kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.k) + o + seg * VEC);
+                            vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.v) + o + seg * VEC);
+                        } else {
+                            kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.k) + o + seg * VEC);
+                            vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.v) + o + seg * VEC);
+                            ksc[u] = a.kv.ks[o / D];
+                            vsc[u] = a.kv.vs[o / D];
+                        }
+                    } else {
+                        key[u] = 0x7fffffff;  // unmapped page: masked out
+                        if (seg == 0) a.err[0] = 1;
+                    }
+                }
+            } else {
+                key[u] = 0x7fffffff;
+            }
+        }
+        // scores (log2 domain)
+        float s[U][R];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kw[4] = {kx[u].x, kx[u].y, kx[u].z, kx[u].w};
+            float kf[16];
+            if constexpr (KDT == KVRT_INT8) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) kf[e] = (float)(int8_t)(kw[e >> 2] >> (8 * (e & 3)));
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float d = 0.f;
+                if constexpr (KDT == KVRT_BF16) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) d = dot2_bf16(qw[r][t], kw[t], d);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        d = fmaf(bf16_lo(qw[r][t]), kf[2 * t], d);
+                        d = fmaf(bf16_hi(qw[r][t]), kf[2 * t + 1], d);
+                    }
+                }
+                d = group_sum<LPR>(d);
+                if constexpr (KDT == KVRT_INT8) d *= ksc[u];
+                const bool vis = key[u] <= hi[r] && key[u] >= lo[r];
+                s[u][r] = vis ? d * a.scale_log2 : -INFINITY;
+            }
+        }
+        // online softmax, one rescale per block of U keys
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float mb = s[0][r];
+#pragma unroll
+            for (int u = 1; u < U; ++u) mb = fmaxf(mb, s[u][r]);
+            const float mn = fmaxf(m_run[r], mb);
+            const float corr = __builtin_amdgcn_exp2f(m_run[r] - mn);
+            m_run[r] = mn;
+            l_run[r] *= corr;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[r][e] *= corr;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t vw[4] = {vx[u].x, vx[u].y, vx[u].z, vx[u].w};
+            float vf[VEC];
+            if constexpr (KDT == KVRT_BF16) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    vf[2 * t] = bf16_lo(vw[t]);
+                    vf[2 * t + 1] = bf16_hi(vw[t]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) vf[e] = (float)(int8_t)(vw[e >> 2] >> (8 * (e & 3)));
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = __builtin_amdgcn_exp2f(s[u][r] - m_run[r]);
+                l_run[r] += p;
+                if constexpr (KDT == KVRT_INT8) p *= vsc[u];
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc[r][e] = fmaf(p, vf[e], acc[r][e]);
+            }
+        }
+    }
+
+    // merge the KPW key sub-groups of the wave (lanes LPR apart)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if constexpr (KPW > 1) {
+            const float M = strided_max<LPR>(m_run[r]);
+            const float w = __builtin_amdgcn_exp2f(m_run[r] - M);
+            l_run[r] = strided_sum<LPR>(l_run[r] * w);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[r][e] = strided_sum<LPR>(acc[r][e] * w);
+            m_run[r] = M;
+        }
+    }
+    if (sub == 0) {
+        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + split) * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < rows) {
+                float4 *dst = reinterpret_cast<float4 *>(a.part_acc + (pbase + r) * D + seg * VEC);
+#pragma unroll
+                for (int t = 0; t < VEC / 4; ++t)
+                    dst[t] = make_float4(acc[r][4 * t], acc[r][4 * t + 1], acc[r][4 * t + 2], acc[r][4 * t + 3]);
+                if (seg == 0) a.part_ml[pbase + r] = make_float2(m_run[r], l_run[r]);
+            }
+        }
+    }
+}
+
+// grid (kv_heads, n_items), 256 threads. Splits are merged in index order, so
+// the result does not depend on workgroup scheduling.
+template <int D, int R>
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+    const int item = blockIdx.y;
+    const int kvh = blockIdx.x;
+    const int hkv = gridDim.x;
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const int hq = hkv * a.group;
+    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;
+    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
+        const int r = idx / D, d = idx % D;
+        float M = kNegBig;
+        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, a.part_ml[pbase + s * R + r].x);
+        float L = 0.f, A = 0.f;
+        for (int s = 0; s < a.n_split; ++s) {
+            const float2 ml = a.part_ml[pbase + s * R + r];
+            const float w = __builtin_amdgcn_exp2f(ml.x - M);
+            L = fmaf(ml.y, w, L);
+            A = fmaf(a.part_acc[(pbase + s * R + r) * D + d], w, A);
+        }
+        const float o = L > 0.f ? A / L : 0.f;
+        const int j = r / Qn, i = r % Qn;
+        a.out[(((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(o);
+    }
+    if (a.advance && kvh == 0 && threadIdx.x == 0) {
+        a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += Qn;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// small control kernels
+// ---------------------------------------------------------------------------
+__global__ void set_i32_kernel(SetLenArgs a) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) a.lens[a.idx[i]] = a.val[i];
+}
+
+__global__ __launch_bounds__(256) void copy_rows_kernel(CopyRowsArgs a) {
+    const int64_t words = a.row_bytes / 4;
+    const int64_t total = a.d0 * a.d1 * a.rows * words;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t w = i % words;
+        int64_t t = i / words;
+        const int64_t r = t % a.rows;
+        t /= a.rows;
+        const int64_t b = t % a.d1;
+        const int64_t c = t / a.d1;
+        const uint32_t x = *reinterpret_cast<const uint32_t *>(a.src + c * a.s0 + b * a.s1 + r * a.sr + 4 * w);
+        *reinterpret_cast<uint32_t *>(a.dst + c * a.t0 + b * a.t1 + r * a.tr + 4 * w) = x;
+    }
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// dispatch
+// ---------------------------------------------------------------------------
+int rows_tile(int rows) {
+    if (rows <= 1) return 1;
+    if (rows <= 2) return 2;
+    if (rows <= 4) return 4;
+    if (rows <= 8) return 8;
+    if (rows <= 16) return 16;
+    return 0;
+}
+
+#define KVRT_DISPATCH_D(D_, ...)                       \
+    switch (D_) {                                      \
+        case 64: { constexpr int HD = 64; __VA_ARGS__; break; }   \
+        case 128: { constexpr int HD = 128; __VA_ARGS__; break; } \
+        case 256: { constexpr int HD = 256; __VA_ARGS__; break; } \
+        case 512: { constexpr int HD = 512; __VA_ARGS__; break; } \
+        default: return hipErrorInvalidValue;          \
+    }
+
+#define KVRT_DISPATCH_LAYOUT(L_, ...)                                             \
+    switch (L_) {                                                                 \
+        case KVRT_LAYOUT_CONTIG: { constexpr int LY = KVRT_LAYOUT_CONTIG; __VA_ARGS__; break; } \
+        case KVRT_LAYOUT_RING: { constexpr int LY = KVRT_LAYOUT_RING; __VA_ARGS__; break; }     \
+        case KVRT_LAYOUT_PAGED: { constexpr int LY = KVRT_LAYOUT_PAGED; __VA_ARGS__; break; }   \
+        default: return hipErrorInvalidValue;                                     \
+    }
+
+hipError_t launch_append(const AppendArgs &a, int head_dim, int dtype, int grid_x, hipStream_t s) {
+    dim3 grid(grid_x, a.n_items), block(256);
+    if (dtype == KVRT_INT8) {
+        if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
+        KVRT_DISPATCH_D(head_dim, hipLaunchKernelGGL((append_kernel<HD, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a));
+    } else {
+        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
+            hipLaunchKernelGGL((append_kernel<HD, KVRT_BF16, LY>), grid, block, 0, s, a)));
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream_t s) {
+    const int64_t chunks = (int64_t)a.kv.kv_heads * a.lmax * (head_dim / 8);
+    int gx = (int)((chunks + 255) / 256);
+    gx = gx < 1 ? 1 : (gx > 4096 ? 4096 : gx);
+    dim3 grid(gx, a.n_items), block(256);
+    if (dtype == KVRT_INT8) {
+        if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
+        KVRT_DISPATCH_D(head_dim, hipLaunchKernelGGL((gather_kernel<HD, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a));
+    } else {
+        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
+            hipLaunchKernelGGL((gather_kernel<HD, KVRT_BF16, LY>), grid, block, 0, s, a)));
+    }
+    return hipGetLastError();
+}
+
+template <int HD, int RT>
+static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s) {
+    dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
+    if (dtype == KVRT_INT8) {
+        if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a);
+    } else {
+        KVRT_DISPATCH_LAYOUT(a.kv.layout,
+            hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, LY>), grid, block, 0, s, a));
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s) {
+    if (a.n_split % kWaves != 0 || a.n_split <= 0) return hipErrorInvalidValue;
+    const int rt = rows_tile(rows_per_head);
+    switch (rt) {
+        case 1: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 1>(a, dtype, s)); break;
+        case 2: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 2>(a, dtype, s)); break;
+        case 4: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 4>(a, dtype, s)); break;
+        case 8: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 8>(a, dtype, s)); break;
+        case 16: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 16>(a, dtype, s)); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(kPtUpdates), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val, hipStream_t s) {
+    for (int off = 0; off < n; off += kPtUpdates) {
+        SetLenArgs a{};
+        a.lens = pt;
+        a.n = (n - off) < kPtUpdates ? (n - off) : kPtUpdates;
+        for (int i = 0; i < a.n; ++i) {
+            a.idx[i] = idx[off + i];
+            a.val[i] = val[off + i];
+        }
+        hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(kPtUpdates), 0, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_copy_rows(const CopyRowsArgs &a, hipStream_t s) {
+    const int64_t total = a.d0 * a.d1 * a.rows * (a.row_bytes / 4);
+    if (total <= 0) return hipSuccess;
+    int64_t g = (total + 255) / 256;
+    if (g > 8192) g = 8192;
+    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)g), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    if ((bytes & 15u) != 0 || (reinterpret_cast<uintptr_t>(p) & 15u) != 0) return hipErrorInvalidValue;
+    const uint64_t n16 = bytes / 16;
+    uint64_t g = (n16 + 255) / 256;
+    if (g > 16384) g = 16384;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)g), dim3(256), 0, s, static_cast<uint4 *>(p), n16);
+    return hipGetLastError();
+}
+
+}  // namespace kvrt

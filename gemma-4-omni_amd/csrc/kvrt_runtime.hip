@@ -1,0 +1,1026 @@
+// kvrt_runtime.hip — host side of the kvrt C ABI (include/kvrt.h).
+//
+// Owns the per-layer KV storage, the host-authoritative lengths and page
+// tables, their device mirrors, and the split-K workspace. Validation happens
+// before any enqueue; a failed enqueue poisons the context (no retry, no
+// fallback), mirroring the fail-closed contract of the reference batch
+// executor (native/gemma4_listener_microbatch/MICROBATCH_DESIGN.md:38-43).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "kvrt_internal.h"
+
+using namespace kvrt;
+
+namespace {
+
+struct Layer {
+    kvrt_layer_spec spec{};
+    int owner = 0;          // layer index whose storage and length this layer uses
+    void *k = nullptr, *v = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+    bool owned = false;
+    uint64_t kv_bytes = 0, scale_bytes = 0;
+};
+
+bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+int ilog2(int x) { int s = 0; while ((1 << s) < x) ++s; return s; }
+
+int elem_size(int dtype) {
+    switch (dtype) {
+        case KVRT_BF16: return 2;
+        case KVRT_INT8: return 1;
+        case KVRT_FP32: return 4;
+        case KVRT_BOOL: return 1;
+        case KVRT_INT32: return 4;
+        default: return 0;
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *s = std::getenv(name);
+    if (!s || !*s) return dflt;
+    const int v = std::atoi(s);
+    return v > 0 ? v : dflt;
+}
+
+}  // namespace
+
+struct kvrt_ctx {
+    kvrt_config cfg{};
+    std::vector<Layer> layers;
+    hipStream_t stream = nullptr;
+    int device = 0;
+    bool poisoned = false;
+    bool inject = false;
+    std::vector<int32_t> len;       // host shadow [slot * n_layers + layer]
+    int32_t *d_len = nullptr;
+    int32_t *d_err = nullptr;
+    bool paged = false;
+    int pt_stride = 0;
+    std::vector<int32_t> pt;        // host page table mirror, -1 unmapped
+    int32_t *d_pt = nullptr;
+    std::vector<int32_t> free_pages;
+    std::vector<int32_t> first_live; // per slot: first mapped logical page
+    float *ws = nullptr;
+    size_t ws_bytes = 0;
+    std::vector<float *> retired_ws;  // kept until destroy: captured graphs may reference them
+    kvrt_counters counters{};
+
+    int len_at(int slot, int layer) const { return len[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
+    int &len_ref(int slot, int layer) { return len[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
+};
+
+namespace {
+
+int poison(kvrt_ctx *c) {
+    c->poisoned = true;
+    return KVRT_EDEVICE;
+}
+
+int device_ok(kvrt_ctx *c, hipError_t e) {
+    if (e != hipSuccess) return poison(c);
+    return KVRT_OK;
+}
+
+// Preamble of every mutating call.
+int begin(kvrt_ctx *c) {
+    if (!c) return KVRT_EINVAL;
+    if (c->poisoned) return KVRT_EPOISONED;
+    if (c->inject) {
+        c->inject = false;
+        return poison(c);
+    }
+    if (hipSetDevice(c->device) != hipSuccess) return poison(c);
+    return KVRT_OK;
+}
+
+KVView make_view(kvrt_ctx *c, int layer) {
+    const Layer &L = c->layers[c->layers[layer].owner];
+    const kvrt_layer_spec &s = L.spec;
+    KVView v{};
+    v.k = L.k;
+    v.v = L.v;
+    v.ks = L.ks;
+    v.vs = L.vs;
+    v.layout = s.layout;
+    v.kv_heads = s.kv_heads;
+    v.row_stride = s.head_dim;
+    if (s.layout == KVRT_LAYOUT_CONTIG) {
+        v.rows = c->cfg.capacity;
+    } else if (s.layout == KVRT_LAYOUT_RING) {
+        v.rows = s.ring_rows;
+    } else {
+        v.rows = c->cfg.block_size;
+        v.block_shift = ilog2(c->cfg.block_size);
+        v.page_table = c->d_pt;
+        v.pt_stride = c->pt_stride;
+        v.pool_pages = c->cfg.pool_pages;
+    }
+    v.head_stride = (int64_t)v.rows * s.head_dim;
+    v.slot_stride = v.head_stride * s.kv_heads;
+    return v;
+}
+
+Lengths make_len(kvrt_ctx *c, int layer) {
+    Lengths l{};
+    l.lens = c->d_len;
+    l.stride = c->cfg.n_layers;
+    l.offset = c->layers[layer].owner;
+    return l;
+}
+
+bool valid_slot(const kvrt_ctx *c, int s) { return s >= 0 && s < c->cfg.n_slots; }
+bool valid_layer(const kvrt_ctx *c, int l) { return l >= 0 && l < c->cfg.n_layers; }
+
+bool distinct_slots(const kvrt_ctx *c, int n, const int32_t *slots) {
+    if (n <= 0 || n > kMaxItems || !slots) return false;
+    for (int i = 0; i < n; ++i) {
+        if (!valid_slot(c, slots[i])) return false;
+        for (int j = 0; j < i; ++j)
+            if (slots[j] == slots[i]) return false;
+    }
+    return true;
+}
+
+// Tensor with the given dtype and rank; last dim contiguous; 16-byte aligned
+// rows. Dims are checked by the callers.
+bool tensor_ok(const kvrt_tensor *t, int dtype, int ndim) {
+    if (!t || !t->data || t->dtype != dtype || t->ndim != ndim) return false;
+    if (t->strides[ndim - 1] != 1) return false;
+    const int es = elem_size(dtype);
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return false;
+    for (int i = 0; i < ndim - 1; ++i) {
+        if (t->dims[i] > 1 && ((t->strides[i] * es) & 15) != 0) return false;
+        if (t->strides[i] < 0) return false;
+    }
+    for (int i = 0; i < ndim; ++i)
+        if (t->dims[i] < 0) return false;
+    return true;
+}
+
+bool is_contiguous(const kvrt_tensor *t) {
+    int64_t expect = 1;
+    for (int i = t->ndim - 1; i >= 0; --i) {
+        if (t->dims[i] != 1 && t->strides[i] != expect) return false;
+        expect *= t->dims[i];
+    }
+    return true;
+}
+
+int ensure_workspace(kvrt_ctx *c, size_t bytes) {
+    if (bytes <= c->ws_bytes) return KVRT_OK;
+    if (c->ws) {
+        c->retired_ws.push_back(c->ws);
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
+    size_t want = std::max(bytes, (size_t)1 << 20);
+    if (hipMalloc(&c->ws, want) != hipSuccess) {
+        c->ws = nullptr;
+        return poison(c);
+    }
+    c->ws_bytes = want;
+    return KVRT_OK;
+}
+
+// Number of wave splits per (item, kv head): enough workgroups to fill the
+// chip, but at least min_keys keys per wave.
+int choose_splits(int n_items, int kv_heads, int64_t max_keys) {
+    static const int target_wgs = env_int("KVRT_TARGET_WGS", 512);
+    static const int min_keys = env_int("KVRT_MIN_KEYS_PER_WAVE", 64);
+    const int per_head = n_items * kv_heads;
+    int wg = (target_wgs + per_head - 1) / per_head;
+    const int64_t cap = std::max<int64_t>(1, (max_keys + (int64_t)kWaves * min_keys - 1) / ((int64_t)kWaves * min_keys));
+    if (wg > cap) wg = (int)cap;
+    if (wg < 1) wg = 1;
+    return wg * kWaves;
+}
+
+int visible_keys(const kvrt_layer_spec &s, int len, int q) {
+    if (s.window > 0) return std::min(len, s.window + q - 1);
+    return len;
+}
+
+// Allocate pages for positions [from, to) of slot; records device edits.
+int map_pages(kvrt_ctx *c, int slot, int from, int to, std::vector<int32_t> &idx,
+              std::vector<int32_t> &val) {
+    const int bs = c->cfg.block_size;
+    if (to <= from) return KVRT_OK;
+    const int p_lo = from / bs, p_hi = (to - 1) / bs;
+    if (p_hi >= c->pt_stride) return KVRT_ESTATE;
+    std::vector<std::pair<int, int>> taken;
+    for (int p = p_lo; p <= p_hi; ++p) {
+        int32_t &e = c->pt[(size_t)slot * c->pt_stride + p];
+        if (e >= 0) continue;
+        if (c->free_pages.empty()) {
+            for (auto &t : taken) {  // roll back this call's allocations
+                c->pt[(size_t)slot * c->pt_stride + t.first] = -1;
+                c->free_pages.push_back(t.second);
+                c->counters.pages_in_use--;
+            }
+            for (size_t i = 0; i < taken.size(); ++i) {
+                idx.pop_back();
+                val.pop_back();
+            }
+            return KVRT_ENOMEM;
+        }
+        const int page = c->free_pages.back();
+        c->free_pages.pop_back();
+        e = page;
+        taken.push_back({p, page});
+        idx.push_back(slot * c->pt_stride + p);
+        val.push_back(page);
+        c->counters.pages_in_use++;
+    }
+    return KVRT_OK;
+}
+
+// Undo page allocations recorded in (idx, val) that were not yet enqueued.
+void unmap_pages(kvrt_ctx *c, const std::vector<int32_t> &idx, const std::vector<int32_t> &val) {
+    for (size_t i = idx.size(); i-- > 0;) {
+        c->pt[idx[i]] = -1;
+        c->free_pages.push_back(val[i]);
+        c->counters.pages_in_use--;
+    }
+}
+
+// Map pages for [L_i, L_i + q) of every item; all-or-nothing.
+int map_items(kvrt_ctx *c, int n, const int32_t *slots, const std::vector<int> &from, int q,
+              std::vector<int32_t> &idx, std::vector<int32_t> &val) {
+    for (int i = 0; i < n; ++i) {
+        const int r = map_pages(c, slots[i], from[i], from[i] + q, idx, val);
+        if (r != KVRT_OK) {
+            unmap_pages(c, idx, val);
+            idx.clear();
+            val.clear();
+            return r;
+        }
+    }
+    return KVRT_OK;
+}
+
+int enqueue_pages(kvrt_ctx *c, const std::vector<int32_t> &idx, const std::vector<int32_t> &val) {
+    if (idx.empty()) return KVRT_OK;
+    c->counters.launches += (idx.size() + kPtUpdates - 1) / kPtUpdates;
+    if (launch_set_pages(c->d_pt, (int)idx.size(), idx.data(), val.data(), c->stream) != hipSuccess)
+        return poison(c);
+    return KVRT_OK;
+}
+
+int set_device_lens(kvrt_ctx *c, const std::vector<int32_t> &idx) {
+    for (size_t off = 0; off < idx.size(); off += kPtUpdates) {
+        SetLenArgs a{};
+        a.lens = c->d_len;
+        a.n = (int)std::min<size_t>(kPtUpdates, idx.size() - off);
+        for (int i = 0; i < a.n; ++i) {
+            a.idx[i] = idx[off + i];
+            a.val[i] = c->len[idx[off + i]];
+        }
+        c->counters.launches++;
+        if (launch_set_lens(a, c->stream) != hipSuccess) return poison(c);
+    }
+    return KVRT_OK;
+}
+
+int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt_storage *storage,
+                kvrt_ctx **out) {
+    if (!cfg || !specs || !out) return KVRT_EINVAL;
+    *out = nullptr;
+    if (cfg->struct_size != sizeof(kvrt_config)) return KVRT_EINVAL;
+    if (cfg->n_layers <= 0 || cfg->n_layers > 4096 || cfg->n_slots <= 0 || cfg->n_slots > (1 << 20) ||
+        cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 64)
+        return KVRT_EINVAL;
+    bool any_paged = false;
+    for (int i = 0; i < cfg->n_layers; ++i) {
+        const kvrt_layer_spec &s = specs[i];
+        if (s.shared_src >= 0) {
+            if (s.shared_src >= i || specs[s.shared_src].shared_src >= 0) return KVRT_EINVAL;
+            continue;
+        }
+        if (s.shared_src != -1) return KVRT_EINVAL;
+        if (s.head_dim != 64 && s.head_dim != 128 && s.head_dim != 256 && s.head_dim != 512) return KVRT_EINVAL;
+        if (s.kv_heads <= 0 || s.kv_heads > 64 || s.window < 0) return KVRT_EINVAL;
+        if (s.dtype != KVRT_BF16 && s.dtype != KVRT_INT8) return KVRT_EINVAL;
+        if (s.dtype == KVRT_INT8 && s.layout != KVRT_LAYOUT_PAGED) return KVRT_EINVAL;
+        if (s.layout == KVRT_LAYOUT_RING) {
+            if (s.window <= 0 || s.ring_rows < s.window + cfg->max_q - 1) return KVRT_EINVAL;
+        } else if (s.layout == KVRT_LAYOUT_PAGED) {
+            any_paged = true;
+        } else if (s.layout != KVRT_LAYOUT_CONTIG) {
+            return KVRT_EINVAL;
+        }
+    }
+    if (any_paged && (!is_pow2(cfg->block_size) || cfg->block_size > 1024 || cfg->pool_pages <= 0))
+        return KVRT_EINVAL;
+
+    kvrt_ctx *c = new (std::nothrow) kvrt_ctx();
+    if (!c) return KVRT_EDEVICE;
+    c->cfg = *cfg;
+    if (hipGetDevice(&c->device) != hipSuccess) {
+        delete c;
+        return KVRT_EDEVICE;
+    }
+    c->layers.resize(cfg->n_layers);
+    c->len.assign((size_t)cfg->n_slots * cfg->n_layers, 0);
+    c->paged = any_paged;
+    auto fail = [&](int code) {
+        kvrt_destroy(c);
+        return code;
+    };
+    for (int i = 0; i < cfg->n_layers; ++i) {
+        Layer &L = c->layers[i];
+        L.spec = specs[i];
+        L.owner = specs[i].shared_src >= 0 ? specs[i].shared_src : i;
+        if (specs[i].shared_src >= 0) L.spec = specs[specs[i].shared_src], L.spec.shared_src = specs[i].shared_src;
+        if (specs[i].shared_src >= 0) continue;
+        if (kvrt_layer_storage_bytes(cfg, &specs[i], &L.kv_bytes, &L.scale_bytes) != KVRT_OK) return fail(KVRT_EINVAL);
+        if (storage) {
+            const kvrt_storage &st = storage[i];
+            if (!st.k || !st.v || (L.scale_bytes && (!st.k_scale || !st.v_scale))) return fail(KVRT_EINVAL);
+            L.k = st.k;
+            L.v = st.v;
+            L.ks = static_cast<float *>(st.k_scale);
+            L.vs = static_cast<float *>(st.v_scale);
+            L.owned = false;
+        } else {
+            L.owned = true;
+            if (hipMalloc(&L.k, L.kv_bytes) != hipSuccess || hipMalloc(&L.v, L.kv_bytes) != hipSuccess)
+                return fail(KVRT_EDEVICE);
+            if (L.scale_bytes) {
+                if (hipMalloc((void **)&L.ks, L.scale_bytes) != hipSuccess ||
+                    hipMalloc((void **)&L.vs, L.scale_bytes) != hipSuccess)
+                    return fail(KVRT_EDEVICE);
+            }
+            if (launch_zero(L.k, L.kv_bytes, nullptr) != hipSuccess ||
+                launch_zero(L.v, L.kv_bytes, nullptr) != hipSuccess)
+                return fail(KVRT_EDEVICE);
+            if (L.scale_bytes && (launch_zero(L.ks, L.scale_bytes, nullptr) != hipSuccess ||
+                                  launch_zero(L.vs, L.scale_bytes, nullptr) != hipSuccess))
+                return fail(KVRT_EDEVICE);
+        }
+    }
+    const size_t len_bytes = ((c->len.size() * 4 + 15) / 16) * 16;
+    if (hipMalloc((void **)&c->d_len, len_bytes) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (launch_zero(c->d_len, len_bytes, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (hipMalloc((void **)&c->d_err, 16) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (launch_zero(c->d_err, 16, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (any_paged) {
+        c->pt_stride = (cfg->capacity + cfg->block_size - 1) / cfg->block_size;
+        c->pt.assign((size_t)cfg->n_slots * c->pt_stride, -1);
+        const size_t pt_bytes = ((c->pt.size() * 4 + 15) / 16) * 16;
+        if (hipMalloc((void **)&c->d_pt, pt_bytes) != hipSuccess) return fail(KVRT_EDEVICE);
+        if (hipMemcpy(c->d_pt, c->pt.data(), c->pt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(KVRT_EDEVICE);
+        c->free_pages.reserve(cfg->pool_pages);
+        for (int p = cfg->pool_pages - 1; p >= 0; --p) c->free_pages.push_back(p);
+        c->first_live.assign(cfg->n_slots, 0);
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return fail(KVRT_EDEVICE);
+    *out = c;
+    return KVRT_OK;
+}
+
+// Launch the split-K decode for n slots of one layer (fused when k/v given).
+int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_tensor *q,
+                const kvrt_tensor *k, const kvrt_tensor *v, const kvrt_tensor *out, float scale) {
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    const bool fused = k != nullptr;
+    const int D = s.head_dim, hkv = s.kv_heads;
+    if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
+        return KVRT_EINVAL;
+    const int64_t hq = q->dims[1], qn = q->dims[2];
+    if (q->dims[0] != n || q->dims[3] != D || hq <= 0 || hq % hkv != 0 || qn <= 0 || qn > c->cfg.max_q)
+        return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (out->dims[i] != q->dims[i]) return KVRT_EINVAL;
+    const int group = (int)(hq / hkv);
+    const int rows = group * (int)qn;
+    if (rows_tile(rows) == 0) return KVRT_EINVAL;
+    if (!std::isfinite(scale)) return KVRT_EINVAL;
+    if (fused) {
+        if (s.dtype != KVRT_BF16) return KVRT_EINVAL;
+        if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4) || !is_contiguous(k) || !is_contiguous(v))
+            return KVRT_EINVAL;
+        if (k->dims[0] != n || k->dims[1] != hkv || k->dims[2] != qn || k->dims[3] != D) return KVRT_EINVAL;
+        for (int i = 0; i < 4; ++i)
+            if (v->dims[i] != k->dims[i]) return KVRT_EINVAL;
+    }
+    // host-side state checks
+    int64_t max_keys = 0;
+    std::vector<int> from(n);
+    for (int i = 0; i < n; ++i) {
+        const int L = c->len_at(slots[i], layer);
+        const int Lnew = fused ? L + (int)qn : L;
+        from[i] = L;
+        if (Lnew < qn) return KVRT_ESTATE;
+        if (fused && Lnew > c->cfg.capacity) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_PAGED && Lnew - (int)qn - s.window + 1 < c->first_live[slots[i]] * c->cfg.block_size &&
+            (s.window == 0 || c->first_live[slots[i]] > 0))
+            return KVRT_ESTATE;  // the window would read evicted pages
+        max_keys = std::max<int64_t>(max_keys, visible_keys(s, Lnew, (int)qn));
+    }
+    const int n_split = choose_splits(n, hkv, max_keys);
+    const int R = rows_tile(rows);
+    const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
+    const size_t ml_elems = (size_t)n * hkv * n_split * R;
+    const size_t bytes = acc_elems * 4 + ml_elems * 8 + 256;
+    int rc = ensure_workspace(c, bytes);
+    if (rc != KVRT_OK) return rc;
+    std::vector<int32_t> pidx, pval;
+    if (fused && s.layout == KVRT_LAYOUT_PAGED) {
+        rc = map_items(c, n, slots, from, (int)qn, pidx, pval);
+        if (rc != KVRT_OK) return rc;
+    }
+    rc = enqueue_pages(c, pidx, pval);
+    if (rc != KVRT_OK) return rc;
+    DecodeArgs a{};
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.q = static_cast<const uint16_t *>(q->data);
+    a.out = static_cast<uint16_t *>(out->data);
+    a.k_new = fused ? static_cast<const uint16_t *>(k->data) : nullptr;
+    a.v_new = fused ? static_cast<const uint16_t *>(v->data) : nullptr;
+    a.part_acc = c->ws;
+    a.part_ml = reinterpret_cast<float2 *>(c->ws + ((acc_elems + 63) / 64) * 64);
+    a.err = c->d_err;
+    a.n_items = n;
+    a.group = group;
+    a.qn = (int)qn;
+    a.window = s.window;
+    a.n_split = n_split;
+    a.advance = fused ? 1 : 0;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
+    c->counters.launches += 2;
+    if (launch_decode(a, D, s.dtype, rows, c->stream) != hipSuccess) return poison(c);
+    const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
+    for (int i = 0; i < n; ++i) {
+        int &L = c->len_ref(slots[i], layer);
+        if (fused) {
+            L += (int)qn;
+            c->counters.appended_rows += (uint64_t)qn * hkv;
+            c->counters.appended_bytes += (uint64_t)qn * hkv * D * 2 * kb;
+        }
+        const uint64_t keys = (uint64_t)visible_keys(s, L, (int)qn);
+        c->counters.attended_keys += keys * hkv;
+        c->counters.attended_bytes += keys * hkv * (uint64_t)D * 2 * kb;
+    }
+    return KVRT_OK;
+}
+
+int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_tensor *k,
+                const kvrt_tensor *v) {
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    if (c->layers[layer].owner != layer) return KVRT_OK;  // shared layers own no rows
+    const int D = s.head_dim, hkv = s.kv_heads;
+    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i]) return KVRT_EINVAL;
+    const int64_t qn = k->dims[2];
+    if (k->dims[0] != n || k->dims[1] != hkv || k->dims[3] != D || qn <= 0 || qn > c->cfg.max_q)
+        return KVRT_EINVAL;
+    std::vector<int> from(n);
+    for (int i = 0; i < n; ++i) {
+        from[i] = c->len_at(slots[i], layer);
+        if ((int64_t)from[i] + qn > c->cfg.capacity) return KVRT_ESTATE;
+    }
+    std::vector<int32_t> pidx, pval;
+    if (s.layout == KVRT_LAYOUT_PAGED) {
+        const int r = map_items(c, n, slots, from, (int)qn, pidx, pval);
+        if (r != KVRT_OK) return r;
+        if ((int)pidx.size() > kPtUpdates) {  // too many edits for the kernarg block
+            const int rc = enqueue_pages(c, pidx, pval);
+            if (rc != KVRT_OK) return rc;
+            pidx.clear();
+            pval.clear();
+        }
+    }
+    AppendArgs a{};
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.k_src = static_cast<const uint16_t *>(k->data);
+    a.v_src = static_cast<const uint16_t *>(v->data);
+    a.src_item_stride = k->strides[0];
+    a.src_head_stride = k->strides[1];
+    a.src_row_stride = k->strides[2];
+    a.n_items = n;
+    a.rows = (int)qn;
+    a.import_mode = 0;
+    a.err = c->d_err;
+    a.n_upd = (int)pidx.size();
+    for (size_t i = 0; i < pidx.size(); ++i) {
+        a.upd_idx[i] = pidx[i];
+        a.upd_val[i] = pval[i];
+    }
+    for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
+    c->counters.launches++;
+    if (launch_append(a, D, s.dtype, 1, c->stream) != hipSuccess) return poison(c);
+    const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
+    for (int i = 0; i < n; ++i) {
+        c->len_ref(slots[i], layer) += (int)qn;
+        c->counters.appended_rows += (uint64_t)qn * hkv;
+        c->counters.appended_bytes += (uint64_t)qn * hkv * D * 2 * kb;
+    }
+    return KVRT_OK;
+}
+
+struct TensorWorkspace {
+    std::mutex mu;
+    float *ptr = nullptr;
+    size_t bytes = 0;
+    int device = -1;
+};
+TensorWorkspace g_tensor_ws;
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+uint32_t kvrt_abi_version(void) { return KVRT_ABI_VERSION; }
+
+uint64_t kvrt_capabilities(void) {
+    return KVRT_CAP_CONTIG | KVRT_CAP_RING | KVRT_CAP_PAGED | KVRT_CAP_INT8 | KVRT_CAP_FUSED_APPEND_ATTEND |
+           KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND;
+}
+
+const char *kvrt_strerror(int code) {
+    switch (code) {
+        case KVRT_OK: return "ok";
+        case KVRT_EINVAL: return "invalid argument";
+        case KVRT_ESTATE: return "state mismatch (length, capacity or rollback range)";
+        case KVRT_EDEVICE: return "device enqueue failed; context poisoned";
+        case KVRT_EPOISONED: return "context poisoned by an earlier device failure";
+        case KVRT_ENOMEM: return "page pool exhausted";
+        case KVRT_EFAULT: return "device-side bounds flag raised";
+        default: return "unknown error";
+    }
+}
+
+int kvrt_layer_storage_bytes(const kvrt_config *cfg, const kvrt_layer_spec *s, uint64_t *kv_bytes,
+                             uint64_t *scale_bytes) {
+    if (!cfg || !s || !kv_bytes || !scale_bytes) return KVRT_EINVAL;
+    const uint64_t es = s->dtype == KVRT_INT8 ? 1 : 2;
+    uint64_t rows_total;
+    if (s->layout == KVRT_LAYOUT_CONTIG) rows_total = (uint64_t)cfg->n_slots * s->kv_heads * cfg->capacity;
+    else if (s->layout == KVRT_LAYOUT_RING) rows_total = (uint64_t)cfg->n_slots * s->kv_heads * s->ring_rows;
+    else if (s->layout == KVRT_LAYOUT_PAGED) rows_total = (uint64_t)cfg->pool_pages * s->kv_heads * cfg->block_size;
+    else return KVRT_EINVAL;
+    *kv_bytes = ((rows_total * s->head_dim * es + 255) / 256) * 256;
+    *scale_bytes = s->dtype == KVRT_INT8 ? ((rows_total * 4 + 255) / 256) * 256 : 0;
+    return KVRT_OK;
+}
+
+int kvrt_create(const kvrt_config *config, const kvrt_layer_spec *layers, kvrt_ctx **out) {
+    return create_impl(config, layers, nullptr, out);
+}
+
+int kvrt_create_with_storage(const kvrt_config *config, const kvrt_layer_spec *layers,
+                             const kvrt_storage *storage, kvrt_ctx **out) {
+    if (!storage) return KVRT_EINVAL;
+    return create_impl(config, layers, storage, out);
+}
+
+int kvrt_destroy(kvrt_ctx *c) {
+    if (!c) return KVRT_EINVAL;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    else (void)hipDeviceSynchronize();
+    for (Layer &L : c->layers) {
+        if (!L.owned) continue;
+        if (L.k) (void)hipFree(L.k);
+        if (L.v) (void)hipFree(L.v);
+        if (L.ks) (void)hipFree(L.ks);
+        if (L.vs) (void)hipFree(L.vs);
+    }
+    if (c->d_len) (void)hipFree(c->d_len);
+    if (c->d_err) (void)hipFree(c->d_err);
+    if (c->d_pt) (void)hipFree(c->d_pt);
+    if (c->ws) (void)hipFree(c->ws);
+    for (float *w : c->retired_ws) (void)hipFree(w);
+    delete c;
+    return KVRT_OK;
+}
+
+int kvrt_bind_stream(kvrt_ctx *c, void *stream) {
+    if (!c) return KVRT_EINVAL;
+    if (c->poisoned) return KVRT_EPOISONED;
+    c->stream = static_cast<hipStream_t>(stream);
+    return KVRT_OK;
+}
+
+int kvrt_layer_storage(kvrt_ctx *c, int32_t layer, kvrt_storage *out) {
+    if (!c || !out || !valid_layer(c, layer)) return KVRT_EINVAL;
+    const Layer &L = c->layers[c->layers[layer].owner];
+    out->k = L.k;
+    out->v = L.v;
+    out->k_scale = L.ks;
+    out->v_scale = L.vs;
+    return KVRT_OK;
+}
+
+int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tensor *k, const kvrt_tensor *v,
+                      int32_t first_pos) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, slot) || !valid_layer(c, layer)) return KVRT_EINVAL;
+    if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // import the source layer instead
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i]) return KVRT_EINVAL;
+    const int64_t S = k->dims[2];
+    if (k->dims[0] != 1 || k->dims[1] != s.kv_heads || k->dims[3] != s.head_dim) return KVRT_EINVAL;
+    if (S < 0 || S > c->cfg.capacity || first_pos < 0 || first_pos > S) return KVRT_EINVAL;
+    int keep_from = first_pos;
+    std::vector<int32_t> pidx, pval;
+    if (s.layout == KVRT_LAYOUT_RING) {
+        keep_from = std::max<int64_t>(keep_from, S - s.ring_rows);
+    } else if (s.layout == KVRT_LAYOUT_PAGED) {
+        keep_from = (first_pos / c->cfg.block_size) * c->cfg.block_size;
+        rc = map_pages(c, slot, keep_from, (int)S, pidx, pval);
+        if (rc) return rc;
+        rc = enqueue_pages(c, pidx, pval);
+        if (rc) return rc;
+        c->first_live[slot] = std::max(c->first_live[slot], keep_from / c->cfg.block_size);
+    }
+    AppendArgs a{};
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.k_src = static_cast<const uint16_t *>(k->data);
+    a.v_src = static_cast<const uint16_t *>(v->data);
+    a.src_item_stride = 0;
+    a.src_head_stride = k->strides[1];
+    a.src_row_stride = k->strides[2];
+    a.n_items = 1;
+    a.rows = (int)S;
+    a.import_mode = 1;
+    a.keep_from = keep_from;
+    a.err = c->d_err;
+    a.slots[0] = slot;
+    if (S > 0) {
+        const int64_t chunks = (int64_t)s.kv_heads * S * (s.head_dim / 8);
+        int gx = (int)std::min<int64_t>(4096, (chunks + 255) / 256);
+        c->counters.launches++;
+        if (launch_append(a, s.head_dim, s.dtype, std::max(1, gx), c->stream) != hipSuccess) return poison(c);
+    } else {
+        std::vector<int32_t> idx{(int32_t)((size_t)slot * c->cfg.n_layers + layer)};
+        c->len_ref(slot, layer) = 0;
+        rc = set_device_lens(c, idx);
+        if (rc) return rc;
+    }
+    c->len_ref(slot, layer) = (int)S;
+    c->counters.appended_rows += (uint64_t)S * s.kv_heads;
+    c->counters.appended_bytes += (uint64_t)S * s.kv_heads * s.head_dim * 2 * (s.dtype == KVRT_INT8 ? 1 : 2);
+    return KVRT_OK;
+}
+
+int kvrt_append_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *k,
+                      const kvrt_tensor *v) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+    return append_impl(c, layer, n, slots, k, v);
+}
+
+int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,
+                      const kvrt_tensor *out_k, const kvrt_tensor *out_v, const kvrt_tensor *mask) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    const int out_dtype = s.dtype == KVRT_INT8 ? KVRT_FP32 : KVRT_BF16;
+    if (!tensor_ok(out_k, out_dtype, 4) || !tensor_ok(out_v, out_dtype, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (out_k->dims[i] != out_v->dims[i] || out_k->strides[i] != out_v->strides[i]) return KVRT_EINVAL;
+    const int64_t lmax = out_k->dims[2];
+    if (out_k->dims[0] != n || out_k->dims[1] != s.kv_heads || out_k->dims[3] != s.head_dim || lmax <= 0 ||
+        lmax > (1 << 30))
+        return KVRT_EINVAL;
+    if (mask) {
+        if (!mask->data || mask->ndim != 2 || mask->dims[0] != n || mask->dims[1] != lmax || mask->strides[1] != 1)
+            return KVRT_EINVAL;
+        if (mask->dtype != KVRT_BOOL && mask->dtype != KVRT_FP32 && mask->dtype != KVRT_BF16) return KVRT_EINVAL;
+    }
+    GatherArgs a{};
+    for (int i = 0; i < n; ++i) {
+        const int L = c->len_at(slots[i], layer);
+        int st;
+        if (start_pos) st = start_pos[i];
+        else if (s.layout == KVRT_LAYOUT_RING) st = std::max(0, L - (s.window - 1));
+        else if (s.layout == KVRT_LAYOUT_PAGED) st = std::min(L, c->first_live[slots[i]] * c->cfg.block_size);
+        else st = 0;
+        if (st < 0 || st > L || L - st > lmax) return KVRT_EINVAL;
+        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && st < L - s.ring_rows) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_PAGED) {
+            for (int p = st / c->cfg.block_size; p * c->cfg.block_size < L; ++p)
+                if (c->pt[(size_t)slots[i] * c->pt_stride + p] < 0) return KVRT_ESTATE;
+        }
+        a.start[i] = st;
+        a.slots[i] = slots[i];
+    }
+    a.has_start = 1;
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.out_k = out_k->data;
+    a.out_v = out_v->data;
+    a.out_item_stride = out_k->strides[0];
+    a.out_head_stride = out_k->strides[1];
+    a.out_row_stride = out_k->strides[2];
+    a.mask = mask ? mask->data : nullptr;
+    a.mask_item_stride = mask ? mask->strides[0] : 0;
+    a.mask_dtype = mask ? mask->dtype : KVRT_BOOL;
+    a.out_fp32 = out_dtype == KVRT_FP32;
+    a.n_items = n;
+    a.lmax = (int)lmax;
+    a.window = s.window;
+    a.err = c->d_err;
+    c->counters.launches++;
+    if (launch_gather(a, s.head_dim, s.dtype, c->stream) != hipSuccess) return poison(c);
+    c->counters.gathered_bytes += (uint64_t)n * s.kv_heads * lmax * s.head_dim * 2 * elem_size(out_dtype);
+    return KVRT_OK;
+}
+
+int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, slot) || layer < -1 || layer >= c->cfg.n_layers || new_len < 0) return KVRT_EINVAL;
+    std::vector<int> targets;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (layer >= 0 && l != layer) continue;
+        if (c->layers[l].owner != l) continue;
+        targets.push_back(l);
+    }
+    if (layer >= 0 && targets.empty()) targets.push_back(c->layers[layer].owner);
+    for (int l : targets) {
+        const kvrt_layer_spec &s = c->layers[l].spec;
+        const int L = c->len_at(slot, l);
+        if (new_len > L) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && new_len - s.window + 1 < L - s.ring_rows)
+            return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_PAGED && new_len < c->first_live[slot] * c->cfg.block_size && new_len < L)
+            return KVRT_ESTATE;
+    }
+    std::vector<int32_t> idx;
+    for (int l : targets) {
+        int &L = c->len_ref(slot, l);
+        if (L == new_len) continue;
+        c->counters.truncated_rows += (uint64_t)(L - new_len);
+        L = new_len;
+        idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
+    }
+    if (c->paged) {
+        // Release pages wholly beyond the longest remaining paged layer.
+        int keep = 0;
+        for (int l = 0; l < c->cfg.n_layers; ++l)
+            if (c->layers[l].owner == l && c->layers[l].spec.layout == KVRT_LAYOUT_PAGED)
+                keep = std::max(keep, c->len_at(slot, l));
+        const int bs = c->cfg.block_size;
+        for (int p = (keep + bs - 1) / bs; p < c->pt_stride; ++p) {
+            int32_t &e = c->pt[(size_t)slot * c->pt_stride + p];
+            if (e >= 0) {
+                c->free_pages.push_back(e);
+                e = -1;
+                c->counters.pages_in_use--;
+            }
+        }
+        if (keep == 0) c->first_live[slot] = 0;
+    }
+    c->counters.truncations++;
+    return set_device_lens(c, idx);
+}
+
+int kvrt_evict(kvrt_ctx *c, int32_t slot, int32_t keep_from) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!c->paged || !valid_slot(c, slot) || keep_from < 0) return KVRT_EINVAL;
+    const int bs = c->cfg.block_size;
+    const int last = keep_from / bs;  // pages [0, last) are wholly below keep_from
+    for (int p = c->first_live[slot]; p < last && p < c->pt_stride; ++p) {
+        int32_t &e = c->pt[(size_t)slot * c->pt_stride + p];
+        if (e >= 0) {
+            c->free_pages.push_back(e);
+            e = -1;
+            c->counters.pages_in_use--;
+            c->counters.pages_evicted++;
+        }
+    }
+    c->first_live[slot] = std::max(c->first_live[slot], std::min(last, c->pt_stride));
+    return KVRT_OK;
+}
+
+int kvrt_copy_prefix_async(kvrt_ctx *c, int32_t src_slot, int32_t dst_slot, int32_t n_tokens) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, src_slot) || !valid_slot(c, dst_slot) || src_slot == dst_slot || n_tokens < 0)
+        return KVRT_EINVAL;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (c->layers[l].owner != l) continue;
+        const kvrt_layer_spec &s = c->layers[l].spec;
+        if (s.layout == KVRT_LAYOUT_PAGED) return KVRT_EINVAL;
+        const int L = c->len_at(src_slot, l);
+        if (n_tokens > L) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && n_tokens - s.window + 1 < L - s.ring_rows)
+            return KVRT_ESTATE;
+    }
+    std::vector<int32_t> idx;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (c->layers[l].owner != l) continue;
+        const kvrt_layer_spec &s = c->layers[l].spec;
+        const KVView vw = make_view(c, l);
+        const int rows = s.layout == KVRT_LAYOUT_RING ? std::min(s.ring_rows, c->len_at(src_slot, l)) : n_tokens;
+        for (int kv = 0; kv < 2; ++kv) {
+            uint8_t *base = static_cast<uint8_t *>(kv == 0 ? vw.k : vw.v);
+            CopyRowsArgs a{};
+            a.src = base + (int64_t)src_slot * vw.slot_stride * 2;
+            a.dst = base + (int64_t)dst_slot * vw.slot_stride * 2;
+            a.d0 = 1;
+            a.d1 = s.kv_heads;
+            a.rows = rows;
+            a.row_bytes = (int64_t)s.head_dim * 2;
+            a.s0 = a.t0 = vw.slot_stride * 2;
+            a.s1 = a.t1 = vw.head_stride * 2;
+            a.sr = a.tr = vw.row_stride * 2;
+            c->counters.launches++;
+            if (launch_copy_rows(a, c->stream) != hipSuccess) return poison(c);
+        }
+        c->len_ref(dst_slot, l) = n_tokens;
+        idx.push_back((int32_t)((size_t)dst_slot * c->cfg.n_layers + l));
+    }
+    return set_device_lens(c, idx);
+}
+
+int kvrt_attend_decode_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *q,
+                             const kvrt_tensor *out, float scale) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+    return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
+}
+
+int kvrt_append_attend_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *q,
+                             const kvrt_tensor *k, const kvrt_tensor *v, const kvrt_tensor *out, float scale) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !k || !v) return KVRT_EINVAL;
+    if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // shared layers append nothing
+    if (c->layers[layer].spec.dtype == KVRT_INT8) {
+        // int8 rows are quantised by the append kernel, then read back.
+        rc = append_impl(c, layer, n, slots, k, v);
+        if (rc) return rc;
+        return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
+    }
+    return decode_impl(c, layer, n, slots, q, k, v, out, scale);
+}
+
+int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
+                              const int32_t *device_lengths, const kvrt_tensor *out, float scale, int32_t window,
+                              void *stream) {
+    if (!device_lengths || window < 0 || !std::isfinite(scale)) return KVRT_EINVAL;
+    if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
+        return KVRT_EINVAL;
+    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i] || out->dims[i] != q->dims[i])
+            return KVRT_EINVAL;
+    const int64_t n = q->dims[0], hq = q->dims[1], qn = q->dims[2], D = q->dims[3];
+    const int64_t hkv = k->dims[1], lmax = k->dims[2];
+    if (n <= 0 || n > kMaxItems || k->dims[0] != n || k->dims[3] != D || hkv <= 0 || hq % hkv != 0 || qn <= 0 ||
+        qn > 64)
+        return KVRT_EINVAL;
+    if (D != 64 && D != 128 && D != 256 && D != 512) return KVRT_EINVAL;
+    if (k->strides[2] != D) return KVRT_EINVAL;
+    const int group = (int)(hq / hkv);
+    const int rows = group * (int)qn;
+    if (rows_tile(rows) == 0) return KVRT_EINVAL;
+    DecodeArgs a{};
+    a.kv.k = k->data;
+    a.kv.v = v->data;
+    a.kv.layout = KVRT_LAYOUT_CONTIG;
+    a.kv.kv_heads = (int)hkv;
+    a.kv.rows = (int)lmax;
+    a.kv.slot_stride = k->strides[0];
+    a.kv.head_stride = k->strides[1];
+    a.kv.row_stride = k->strides[2];
+    a.len.lens = const_cast<int32_t *>(device_lengths);
+    a.len.stride = 1;
+    a.len.offset = 0;
+    a.q = static_cast<const uint16_t *>(q->data);
+    a.out = static_cast<uint16_t *>(out->data);
+    a.n_items = (int)n;
+    a.group = group;
+    a.qn = (int)qn;
+    a.window = window;
+    a.n_split = choose_splits((int)n, (int)hkv, window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax);
+    a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < n; ++i) a.slots[i] = i;
+    const int R = rows_tile(rows);
+    const size_t acc_elems = (size_t)n * hkv * a.n_split * R * D;
+    const size_t bytes = acc_elems * 4 + (size_t)n * hkv * a.n_split * R * 8 + 256 + 16;
+    std::lock_guard<std::mutex> lock(g_tensor_ws.mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
+    if (g_tensor_ws.ptr && (g_tensor_ws.bytes < bytes || g_tensor_ws.device != dev)) {
+        if (hipDeviceSynchronize() != hipSuccess) return KVRT_EDEVICE;
+        (void)hipFree(g_tensor_ws.ptr);
+        g_tensor_ws.ptr = nullptr;
+        g_tensor_ws.bytes = 0;
+    }
+    if (!g_tensor_ws.ptr) {
+        const size_t want = std::max(bytes, (size_t)1 << 20);
+        if (hipMalloc(&g_tensor_ws.ptr, want) != hipSuccess) return KVRT_EDEVICE;
+        if (launch_zero(g_tensor_ws.ptr, 16, static_cast<hipStream_t>(stream)) != hipSuccess) return KVRT_EDEVICE;
+        g_tensor_ws.bytes = want;
+        g_tensor_ws.device = dev;
+    }
+    // First 16 bytes hold the error flag of this path.
+    a.err = reinterpret_cast<int32_t *>(g_tensor_ws.ptr);
+    a.part_acc = g_tensor_ws.ptr + 64;
+    a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + 64 + ((acc_elems + 63) / 64) * 64);
+    if (launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream)) != hipSuccess)
+        return KVRT_EDEVICE;
+    return KVRT_OK;
+}
+
+int kvrt_copy_rows_async(const kvrt_tensor *src, const kvrt_tensor *dst, int64_t rows, void *stream) {
+    if (!src || !dst || !src->data || !dst->data || src->ndim != 4 || dst->ndim != 4 || src->dtype != dst->dtype)
+        return KVRT_EINVAL;
+    const int es = elem_size(src->dtype);
+    if (es != 2 && es != 4) return KVRT_EINVAL;
+    if (src->strides[3] != 1 || dst->strides[3] != 1) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (i != 2 && src->dims[i] != dst->dims[i]) return KVRT_EINVAL;
+    if (rows < 0 || rows > src->dims[2] || rows > dst->dims[2]) return KVRT_EINVAL;
+    const int64_t row_bytes = src->dims[3] * es;
+    if (row_bytes % 4 != 0 || (reinterpret_cast<uintptr_t>(src->data) & 3u) ||
+        (reinterpret_cast<uintptr_t>(dst->data) & 3u))
+        return KVRT_EINVAL;
+    CopyRowsArgs a{};
+    a.src = static_cast<const uint8_t *>(src->data);
+    a.dst = static_cast<uint8_t *>(dst->data);
+    a.d0 = src->dims[0];
+    a.d1 = src->dims[1];
+    a.rows = rows;
+    a.row_bytes = row_bytes;
+    a.s0 = src->strides[0] * es;
+    a.s1 = src->strides[1] * es;
+    a.sr = src->strides[2] * es;
+    a.t0 = dst->strides[0] * es;
+    a.t1 = dst->strides[1] * es;
+    a.tr = dst->strides[2] * es;
+    if ((a.s0 | a.s1 | a.sr | a.t0 | a.t1 | a.tr) & 3) return KVRT_EINVAL;
+    return launch_copy_rows(a, static_cast<hipStream_t>(stream)) == hipSuccess ? KVRT_OK : KVRT_EDEVICE;
+}
+
+int kvrt_session_state(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t *length) {
+    if (!c || !length || !valid_slot(c, slot) || !valid_layer(c, layer)) return KVRT_EINVAL;
+    *length = c->len_at(slot, layer);
+    return KVRT_OK;
+}
+
+int kvrt_sync_lengths(kvrt_ctx *c) {
+    if (!c) return KVRT_EINVAL;
+    if (c->poisoned) return KVRT_EPOISONED;
+    if (hipSetDevice(c->device) != hipSuccess) return poison(c);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    std::vector<int32_t> dev(c->len.size());
+    if (hipMemcpy(dev.data(), c->d_len, dev.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return poison(c);
+    for (size_t i = 0; i < dev.size(); ++i) {
+        if (dev[i] < 0 || dev[i] > c->cfg.capacity) return KVRT_EFAULT;
+    }
+    c->len = dev;
+    return KVRT_OK;
+}
+
+int kvrt_get_counters(kvrt_ctx *c, kvrt_counters *out) {
+    if (!c || !out) return KVRT_EINVAL;
+    *out = c->counters;
+    return KVRT_OK;
+}
+
+int kvrt_health(kvrt_ctx *c) {
+    if (!c) return KVRT_EINVAL;
+    if (c->poisoned) return KVRT_EPOISONED;
+    if (hipSetDevice(c->device) != hipSuccess) return poison(c);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    int32_t err = 0;
+    if (hipMemcpy(&err, c->d_err, sizeof(err), hipMemcpyDeviceToHost) != hipSuccess) return poison(c);
+    if (err != 0) return KVRT_EFAULT;
+    return KVRT_OK;
+}
+
+int kvrt_debug_inject_failure(kvrt_ctx *c) {
+    if (!c) return KVRT_EINVAL;
+    c->inject = true;
+    return KVRT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+"""Build libkvrt.so (gfx950) in-tree with hipcc.
+
+The library is compiled from ``csrc/kvrt_kernels.hip`` (kernels) and
+``csrc/kvrt_runtime.hip`` (host runtime, C ABI in ``include/kvrt.h``).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parent.parent / "include"
+LIB_PATH = PKG_DIR / "libkvrt.so"
+SOURCES = ("kvrt_kernels.hip", "kvrt_runtime.hip")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed FP32 VALU forms are kept out of every code object.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the kvrt HIP library cannot be built")
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        noise = "is not a recognized feature for this target"
+        err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source and link libkvrt.so next to this file."""
+    with tempfile.TemporaryDirectory(prefix="kvrt_build_") as tmp:
+        objs = [Path(tmp) / (Path(s).stem + ".o") for s in SOURCES]
+        with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+            futs = [pool.submit(_compile, CSRC / s, o) for s, o in zip(SOURCES, objs)]
+            for f in futs:
+                f.result()
+        tmp_lib = Path(tmp) / "libkvrt.so"
+        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp_lib)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link of libkvrt.so failed:\n{res.stderr}")
+        shutil.move(str(tmp_lib), str(LIB_PATH))
+    if verbose:
+        print(f"[kvrt] built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

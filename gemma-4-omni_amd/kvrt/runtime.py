@@ -1,0 +1,368 @@
+"""Python host side of the kvrt runtime (PyTorch-ROCm tensors in, libkvrt.so out).
+
+``KVRuntime`` owns one kvrt context: per-layer KV storage for ``n_slots``
+sessions/streams, host-authoritative lengths (mirrored on the device), the
+page pool for paged layers, and the split-K workspace. Every method enqueues
+hand-written gfx950 kernels on the current torch stream through the C ABI in
+``include/kvrt.h``; there is no PyTorch or CPU fallback behind any method.
+
+Storage is allocated by torch (so HF-shaped views of a contiguous layer are
+free) and bound to the context with ``kvrt_create_with_storage``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Iterable, Sequence
+
+import torch
+
+from . import _lib as L
+
+_DTYPE_CODES = {
+    torch.bfloat16: L.DT_BF16,
+    torch.int8: L.DT_INT8,
+    torch.float32: L.DT_FP32,
+    torch.bool: L.DT_BOOL,
+    torch.int32: L.DT_INT32,
+}
+_LAYOUTS = {"contig": L.LAYOUT_CONTIG, "ring": L.LAYOUT_RING, "paged": L.LAYOUT_PAGED}
+
+
+class KVRTError(RuntimeError):
+    """A kvrt C-ABI call returned a negative status."""
+
+    def __init__(self, code: int, where: str) -> None:
+        self.code = int(code)
+        super().__init__(f"{where}: kvrt error {code} ({L.strerror(code)})")
+
+
+def _check(code: int, where: str) -> None:
+    if code != L.KVRT_OK:
+        raise KVRTError(code, where)
+
+
+def tensor_desc(t: torch.Tensor) -> L.KvrtTensor:
+    """Strided descriptor of a device tensor (strides in elements)."""
+    if t.dtype not in _DTYPE_CODES:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    if t.dim() > L.KVRT_MAX_RANK:
+        raise ValueError("tensors of rank > 4 are not supported")
+    d = L.KvrtTensor()
+    d.data = t.data_ptr()
+    d.dtype = _DTYPE_CODES[t.dtype]
+    d.ndim = t.dim()
+    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
+        d.dims[i] = int(n)
+        d.strides[i] = int(s)
+    return d
+
+
+def current_stream_handle(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_cuda(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (kvrt has no CPU path)")
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    """One KV layer: layout, dtype, GQA shape, window and aliasing.
+
+    ``layout``: "contig" ([slots, kv_heads, capacity, D]), "ring" (sliding
+    window ring of ``ring_rows`` rows) or "paged" (shared page pool).
+    ``shared_src >= 0`` makes the layer read another layer's K/V (Gemma-4
+    shared-KV layers, native/gemma4_listener_microbatch/generated_topology.h:59-95).
+    """
+
+    kv_heads: int
+    head_dim: int
+    layout: str = "contig"
+    dtype: str = "bf16"
+    window: int = 0
+    ring_rows: int = 0
+    shared_src: int = -1
+
+    def to_c(self) -> L.KvrtLayerSpec:
+        s = L.KvrtLayerSpec()
+        s.layout = _LAYOUTS[self.layout]
+        s.dtype = L.DT_INT8 if self.dtype == "int8" else L.DT_BF16
+        s.kv_heads = self.kv_heads
+        s.head_dim = self.head_dim
+        s.window = self.window
+        s.ring_rows = self.ring_rows
+        s.shared_src = self.shared_src
+        s.reserved = 0
+        return s
+
+
+class KVRuntime:
+    """One kvrt context: the KV state of ``n_slots`` sessions over ``layers``."""
+
+    def __init__(
+        self,
+        layers: Sequence[LayerSpec],
+        n_slots: int,
+        capacity: int,
+        *,
+        max_q: int = 2,
+        block_size: int = 16,
+        pool_pages: int = 0,
+        device: torch.device | str | None = None,
+    ) -> None:
+        self.lib = L.load()
+        self.device = torch.device(device if device is not None else "cuda")
+        if self.device.type != "cuda" or not torch.cuda.is_available():
+            raise RuntimeError("KVRuntime needs a ROCm GPU (torch.cuda); there is no CPU path")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.layers = list(layers)
+        self.n_slots = int(n_slots)
+        self.capacity = int(capacity)
+        self.max_q = int(max_q)
+        self.block_size = int(block_size)
+        self.pool_pages = int(pool_pages)
+        self._ctx = ctypes.c_void_p()
+        cfg = L.KvrtConfig()
+        cfg.struct_size = ctypes.sizeof(L.KvrtConfig)
+        cfg.n_layers = len(self.layers)
+        cfg.n_slots = self.n_slots
+        cfg.capacity = self.capacity
+        cfg.block_size = self.block_size
+        cfg.pool_pages = self.pool_pages
+        cfg.max_q = self.max_q
+        cfg.reserved = 0
+        self._cfg = cfg
+        specs = (L.KvrtLayerSpec * len(self.layers))(*[s.to_c() for s in self.layers])
+        self._specs = specs
+        storage = (L.KvrtStorage * len(self.layers))()
+        self._store: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None] | None] = []
+        with torch.cuda.device(self.device):
+            for i, spec in enumerate(self.layers):
+                if spec.shared_src >= 0:
+                    self._store.append(None)
+                    continue
+                kvb, scb = ctypes.c_uint64(), ctypes.c_uint64()
+                _check(self.lib.kvrt_layer_storage_bytes(ctypes.byref(cfg), ctypes.byref(specs[i]),
+                                                         ctypes.byref(kvb), ctypes.byref(scb)),
+                       "kvrt_layer_storage_bytes")
+                shape = self._storage_shape(spec)
+                dt = torch.int8 if spec.dtype == "int8" else torch.bfloat16
+                es = 1 if dt == torch.int8 else 2
+                pad = kvb.value // es
+                k = torch.zeros(pad, dtype=dt, device=self.device)
+                v = torch.zeros(pad, dtype=dt, device=self.device)
+                n_el = math.prod(shape)
+                kv_views = (k[:n_el].view(shape), v[:n_el].view(shape))
+                ks = vs = None
+                storage[i].k = k.data_ptr()
+                storage[i].v = v.data_ptr()
+                if spec.dtype == "int8":
+                    ks_flat = torch.zeros(scb.value // 4, dtype=torch.float32, device=self.device)
+                    vs_flat = torch.zeros(scb.value // 4, dtype=torch.float32, device=self.device)
+                    n_sc = math.prod(shape[:-1])
+                    ks, vs = ks_flat[:n_sc].view(shape[:-1]), vs_flat[:n_sc].view(shape[:-1])
+                    storage[i].k_scale = ks_flat.data_ptr()
+                    storage[i].v_scale = vs_flat.data_ptr()
+                    self._keep = getattr(self, "_keep", []) + [ks_flat, vs_flat]
+                self._keep = getattr(self, "_keep", []) + [k, v]
+                self._store.append((kv_views[0], kv_views[1], ks, vs))
+            torch.cuda.synchronize(self.device)
+            _check(self.lib.kvrt_create_with_storage(ctypes.byref(cfg), specs, storage, ctypes.byref(self._ctx)),
+                   "kvrt_create_with_storage")
+
+    # ---- helpers -------------------------------------------------------------
+    def _storage_shape(self, spec: LayerSpec) -> tuple[int, ...]:
+        if spec.layout == "contig":
+            return (self.n_slots, spec.kv_heads, self.capacity, spec.head_dim)
+        if spec.layout == "ring":
+            return (self.n_slots, spec.kv_heads, spec.ring_rows, spec.head_dim)
+        return (self.pool_pages, spec.kv_heads, self.block_size, spec.head_dim)
+
+    def _owner(self, layer: int) -> int:
+        src = self.layers[layer].shared_src
+        return src if src >= 0 else layer
+
+    def _bind(self) -> None:
+        _check(self.lib.kvrt_bind_stream(self._ctx, ctypes.c_void_p(current_stream_handle(self.device))),
+               "kvrt_bind_stream")
+
+    @staticmethod
+    def _slots(slots: Iterable[int]) -> tuple[ctypes.Array, int]:
+        s = [int(x) for x in slots]
+        return (ctypes.c_int32 * len(s))(*s), len(s)
+
+    def storage(self, layer: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
+        """Typed views of a layer's K, V (and INT8 scale) storage."""
+        st = self._store[self._owner(layer)]
+        assert st is not None
+        return st
+
+    # ---- KV operations -----------------------------------------------------
+    def import_(self, slot: int, layer: int, k: torch.Tensor, v: torch.Tensor, first_pos: int = 0) -> None:
+        """Import an HF layer view [1, kv_heads, S, D] bf16 as positions 0..S-1."""
+        require_cuda(k, "k")
+        require_cuda(v, "v")
+        self._bind()
+        kd, vd = tensor_desc(k), tensor_desc(v)
+        _check(self.lib.kvrt_import_async(self._ctx, slot, layer, ctypes.byref(kd), ctypes.byref(vd), first_pos),
+               "kvrt_import_async")
+
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, slots: Sequence[int]) -> None:
+        """Append k, v [n, kv_heads, Q, D] bf16 at each slot's current length."""
+        require_cuda(k, "k")
+        require_cuda(v, "v")
+        self._bind()
+        arr, n = self._slots(slots)
+        kd, vd = tensor_desc(k), tensor_desc(v)
+        _check(self.lib.kvrt_append_async(self._ctx, layer, n, arr, ctypes.byref(kd), ctypes.byref(vd)),
+               "kvrt_append_async")
+
+    def attend(self, layer: int, q: torch.Tensor, slots: Sequence[int], scale: float,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+        """Decode attention of q [n, Hq, Q, D] over the last Q positions of each slot."""
+        require_cuda(q, "q")
+        q = q.contiguous()
+        out = torch.empty_like(q) if out is None else out
+        self._bind()
+        arr, n = self._slots(slots)
+        qd, od = tensor_desc(q), tensor_desc(out)
+        _check(self.lib.kvrt_attend_decode_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(od),
+                                                 float(scale)),
+               "kvrt_attend_decode_async")
+        return out
+
+    def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      slots: Sequence[int], scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Fused per-layer decode step: append k, v then attend q."""
+        require_cuda(q, "q")
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        out = torch.empty_like(q) if out is None else out
+        self._bind()
+        arr, n = self._slots(slots)
+        qd, kd, vd, od = tensor_desc(q), tensor_desc(k), tensor_desc(v), tensor_desc(out)
+        _check(self.lib.kvrt_append_attend_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(kd),
+                                                 ctypes.byref(vd), ctypes.byref(od), float(scale)),
+               "kvrt_append_attend_async")
+        return out
+
+    def gather(self, layer: int, slots: Sequence[int], lmax: int | None = None,
+               start_pos: Sequence[int] | None = None, mask_dtype: torch.dtype | None = torch.bool,
+               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+        """Zero-padded batch [n, kv_heads, Lmax, D] (+ mask [n, Lmax]) of n slots."""
+        spec = self.layers[self._owner(layer)]
+        slots = [int(s) for s in slots]
+        if lmax is None:
+            lens = [self.seq_length(s, layer) for s in slots]
+            if start_pos is not None:
+                lens = [a - b for a, b in zip(lens, start_pos)]
+            elif spec.layout == "ring":
+                lens = [min(x, spec.window - 1) for x in lens]
+            lmax = max(1, max(lens))
+        dt = torch.float32 if spec.dtype == "int8" else torch.bfloat16
+        out_k = torch.empty((len(slots), spec.kv_heads, lmax, spec.head_dim), dtype=dt, device=self.device)
+        out_v = torch.empty_like(out_k)
+        mask = None if mask_dtype is None else torch.empty((len(slots), lmax), dtype=mask_dtype, device=self.device)
+        self._bind()
+        arr, n = self._slots(slots)
+        sp = None if start_pos is None else (ctypes.c_int32 * n)(*[int(x) for x in start_pos])
+        kd, vd = tensor_desc(out_k), tensor_desc(out_v)
+        md = None if mask is None else ctypes.byref(tensor_desc(mask))
+        _check(self.lib.kvrt_gather_async(self._ctx, layer, n, arr, sp, ctypes.byref(kd), ctypes.byref(vd), md),
+               "kvrt_gather_async")
+        return out_k, out_v, mask
+
+    def truncate(self, slot: int, new_len: int, layer: int = -1) -> None:
+        """Rollback to new_len positions: a length edit, no KV bytes move."""
+        self._bind()
+        _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len)), "kvrt_truncate")
+
+    def evict(self, slot: int, keep_from: int) -> None:
+        _check(self.lib.kvrt_evict(self._ctx, slot, int(keep_from)), "kvrt_evict")
+
+    def copy_prefix(self, src_slot: int, dst_slot: int, n_tokens: int) -> None:
+        self._bind()
+        _check(self.lib.kvrt_copy_prefix_async(self._ctx, src_slot, dst_slot, int(n_tokens)),
+               "kvrt_copy_prefix_async")
+
+    # ---- state -----------------------------------------------------------------
+    def seq_length(self, slot: int, layer: int = 0) -> int:
+        out = ctypes.c_int32()
+        _check(self.lib.kvrt_session_state(self._ctx, slot, layer, ctypes.byref(out)), "kvrt_session_state")
+        return int(out.value)
+
+    def sync_lengths(self) -> None:
+        """Reload host lengths from the device (after HIP graph replays)."""
+        self._bind()
+        _check(self.lib.kvrt_sync_lengths(self._ctx), "kvrt_sync_lengths")
+
+    def counters(self) -> dict[str, int]:
+        c = L.KvrtCounters()
+        _check(self.lib.kvrt_get_counters(self._ctx, ctypes.byref(c)), "kvrt_get_counters")
+        return {name: int(getattr(c, name)) for name, _ in L.KvrtCounters._fields_}
+
+    def health(self) -> int:
+        """Synchronise and return the kvrt status code (0 = healthy)."""
+        # A poisoned context refuses the rebind; kvrt_health reports it.
+        self.lib.kvrt_bind_stream(self._ctx, ctypes.c_void_p(current_stream_handle(self.device)))
+        return int(self.lib.kvrt_health(self._ctx))
+
+    def layer_view(self, slot: int, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """HF-shaped [1, kv_heads, L, D] views of a slot's logical K/V.
+
+        CONTIG layers return zero-copy views of the storage; RING and PAGED
+        layers return a gathered copy (bf16, or fp32 dequantised for INT8).
+        """
+        spec = self.layers[self._owner(layer)]
+        n = self.seq_length(slot, layer)
+        if spec.layout == "contig":
+            k, v, _, _ = self.storage(layer)
+            return k[slot:slot + 1, :, :n, :], v[slot:slot + 1, :, :n, :]
+        k, v, _ = self.gather(layer, [slot], mask_dtype=None)
+        return k, v
+
+    def close(self) -> None:
+        if self._ctx:
+            self.lib.kvrt_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter teardown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def attend_tensors(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lengths: torch.Tensor,
+                   scale: float, window: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention over caller-owned K/V [n, kv_heads, Lmax, D] with per-item lengths.
+
+    q [n, Hq, Q, D] bf16; lengths int32 [n] on the device. Query row i of item
+    b sits at position lengths[b] - Q + i.
+    """
+    lib = L.load()
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (lengths, "lengths")):
+        require_cuda(t, name)
+    q = q.contiguous()
+    lengths = lengths.to(torch.int32).contiguous()
+    out = torch.empty_like(q) if out is None else out
+    qd, kd, vd, od = tensor_desc(q), tensor_desc(k), tensor_desc(v), tensor_desc(out)
+    _check(lib.kvrt_attend_tensors_async(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd),
+                                         ctypes.c_void_p(lengths.data_ptr()), ctypes.byref(od), float(scale),
+                                         int(window), ctypes.c_void_p(current_stream_handle(q.device))),
+           "kvrt_attend_tensors_async")
+    return out
+
+
+def copy_rows(src: torch.Tensor, dst: torch.Tensor, rows: int) -> None:
+    """dst[:, :, :rows] = src[:, :, :rows] for 4-D tensors (2- or 4-byte elements)."""
+    lib = L.load()
+    require_cuda(src, "src")
+    require_cuda(dst, "dst")
+    sd, dd = tensor_desc(src), tensor_desc(dst)
+    _check(lib.kvrt_copy_rows_async(ctypes.byref(sd), ctypes.byref(dd), int(rows),
+                                    ctypes.c_void_p(current_stream_handle(src.device))),
+           "kvrt_copy_rows_async")

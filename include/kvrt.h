@@ -1,0 +1,297 @@
+/*
+ * kvrt.h — C ABI of the MI355X (gfx950) KV-cache runtime.
+ *
+ * One shared library, libkvrt.so, holds the hand-written HIP kernels for the
+ * per-frame KV hot path of the duplex decode loops (Gemma-4-E2B-shaped
+ * thinker/listener, Qwen3-TTS-shaped talker):
+ *
+ *   append  (contiguous, sliding-window ring, paged bf16 / paged int8)
+ *   gather  (ragged N-stream micro-batch -> padded [N, H, Lmax, D] + mask)
+ *   truncate / evict (turn-local rollback as length / page-table edits)
+ *   attend  (GQA split-K decode attention, fp32 softmax and accumulators)
+ *
+ * Conventions (mirroring the reference native ABIs, e.g.
+ * native/gemma4_listener_microbatch/gemma4_listener.h:36-50 and
+ * native/qwen_talker/qwen_talker.h:55-68):
+ *   - every entry point is extern "C" and returns int: 0 ok, negative error
+ *     class (see KVRT_E*). Argument errors leave the context untouched.
+ *   - a failed device enqueue poisons the context; a poisoned context
+ *     refuses every later mutating call with KVRT_EPOISONED.
+ *   - host descriptors (kvrt_tensor, arrays of slot ids) are read
+ *     synchronously during the call and never retained.
+ *   - device payloads (queries, new K/V rows, outputs) are caller-owned and
+ *     borrowed for the duration of the enqueued work; KV storage is owned by
+ *     the context unless the caller binds its own storage at create time.
+ *   - every mutating call is asynchronous on the stream bound with
+ *     kvrt_bind_stream (default: the null stream). Lengths are tracked on the
+ *     host (authoritative, used for validation) and mirrored in device memory
+ *     where the kernels read them.
+ *   - one owner host thread per context; calls on one context are not
+ *     thread-safe.
+ *
+ * Stream handles are passed as void* (a hipStream_t) so that the header
+ * needs no HIP or torch types.
+ */
+#ifndef KVRT_H
+#define KVRT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVRT_ABI_VERSION 1u
+#define KVRT_MAX_RANK 4
+#define KVRT_MAX_ITEMS 64 /* slots per batched call */
+
+/* ---- return codes ------------------------------------------------------ */
+#define KVRT_OK 0
+#define KVRT_EINVAL (-1)    /* invalid argument, shape, dtype or slot id      */
+#define KVRT_ESTATE (-2)    /* state mismatch: capacity, rollback beyond ring */
+#define KVRT_EDEVICE (-3)   /* device enqueue/allocation failed: ctx poisoned */
+#define KVRT_EPOISONED (-4) /* ctx poisoned by an earlier device failure      */
+#define KVRT_ENOMEM (-5)    /* page pool exhausted                            */
+#define KVRT_EFAULT (-6)    /* device-side error flag raised (health check)   */
+
+/* ---- capability bits (kvrt_capabilities) -------------------------------- */
+#define KVRT_CAP_CONTIG (1ull << 0)
+#define KVRT_CAP_RING (1ull << 1)
+#define KVRT_CAP_PAGED (1ull << 2)
+#define KVRT_CAP_INT8 (1ull << 3)
+#define KVRT_CAP_FUSED_APPEND_ATTEND (1ull << 4)
+#define KVRT_CAP_GATHER (1ull << 5)
+#define KVRT_CAP_DEVICE_LENGTHS (1ull << 6)
+#define KVRT_CAP_TENSOR_ATTEND (1ull << 7)
+
+/* ---- enums ------------------------------------------------------------- */
+enum kvrt_layout {
+    KVRT_LAYOUT_CONTIG = 0, /* [slots, kv_heads, capacity, D] per layer        */
+    KVRT_LAYOUT_RING = 1,   /* [slots, kv_heads, ring_rows, D]; row = pos mod R */
+    KVRT_LAYOUT_PAGED = 2,  /* [pool_pages, kv_heads, block, D] + page table    */
+};
+
+enum kvrt_dtype {
+    KVRT_BF16 = 0,
+    KVRT_INT8 = 1, /* symmetric, one fp32 scale per (token, head) */
+    KVRT_FP32 = 2,
+    KVRT_BOOL = 3, /* 1 byte: 0 / 1 */
+    KVRT_INT32 = 4,
+};
+
+/* ---- descriptors --------------------------------------------------------- */
+/* Strided tensor view. Strides are in ELEMENTS; the last dimension must be
+ * contiguous (stride 1) for every K/V/Q/O tensor. */
+typedef struct kvrt_tensor {
+    void *data;
+    int32_t dtype;
+    int32_t ndim;
+    int64_t dims[KVRT_MAX_RANK];
+    int64_t strides[KVRT_MAX_RANK];
+} kvrt_tensor;
+
+typedef struct kvrt_layer_spec {
+    int32_t layout;     /* enum kvrt_layout                                   */
+    int32_t dtype;      /* KVRT_BF16 or KVRT_INT8 (INT8 requires PAGED)        */
+    int32_t kv_heads;   /* 1..64                                              */
+    int32_t head_dim;   /* 64, 128, 256 or 512                                */
+    int32_t window;     /* sliding window W (keys p-W+1..p visible), 0 = global */
+    int32_t ring_rows;  /* RING only: physical rows R >= W + max_q - 1         */
+    int32_t shared_src; /* -1, or an earlier layer whose K/V this layer reads  */
+    int32_t reserved;
+} kvrt_layer_spec;
+
+typedef struct kvrt_config {
+    uint32_t struct_size; /* sizeof(kvrt_config)                              */
+    int32_t n_layers;
+    int32_t n_slots;      /* sessions / streams                               */
+    int32_t capacity;     /* max logical tokens per slot                      */
+    int32_t block_size;   /* PAGED: tokens per page (power of two, e.g. 16)   */
+    int32_t pool_pages;   /* PAGED: pages in the shared pool                  */
+    int32_t max_q;        /* max rows per append / query rows per attend      */
+    int32_t reserved;
+} kvrt_config;
+
+/* Optional caller-owned storage for one layer (kvrt_create_with_storage).
+ * Sizes must equal kvrt_layer_storage_bytes for that layer. */
+typedef struct kvrt_storage {
+    void *k;
+    void *v;
+    void *k_scale; /* INT8 only: fp32 [pool_pages, kv_heads, block] */
+    void *v_scale;
+} kvrt_storage;
+
+typedef struct kvrt_counters {
+    uint64_t launches;
+    uint64_t appended_rows;     /* token rows appended (sum over slots, layers) */
+    uint64_t appended_bytes;    /* K+V payload bytes written by append          */
+    uint64_t attended_keys;     /* visible keys read by attention (per kv head) */
+    uint64_t attended_bytes;    /* K+V bytes read by attention                  */
+    uint64_t gathered_bytes;    /* bytes written by gather (incl. padding)      */
+    uint64_t truncations;
+    uint64_t truncated_rows;
+    uint64_t pages_in_use;
+    uint64_t pages_evicted;
+} kvrt_counters;
+
+typedef struct kvrt_ctx kvrt_ctx;
+
+/* ---- version / capabilities ---------------------------------------------- */
+/* Replaces gemma4_listener_batch_api_version / _capabilities
+ * (native/gemma4_listener_microbatch/gemma4_listener_microbatch.h:204-205;
+ * probed from Python at duplex_kernel/native_listener_microbatch.py:44-59). */
+uint32_t kvrt_abi_version(void);
+uint64_t kvrt_capabilities(void);
+const char *kvrt_strerror(int code);
+
+/* ---- lifetime -------------------------------------------------------------- */
+/* Replaces gemma4_cache_create (native/gemma4_listener_microbatch/
+ * gemma4_listener_cache.cu:68-179) and the talker KV arena allocation in
+ * qwen_talker_create (native/qwen_talker/qwen_talker.cu:27-113).
+ * Storage is zero-initialised once at create. */
+int kvrt_create(const kvrt_config *config, const kvrt_layer_spec *layers, kvrt_ctx **out);
+/* Same, with caller-owned storage for every non-shared layer (entries of
+ * shared layers are ignored). The caller keeps the storage alive until
+ * kvrt_destroy. */
+int kvrt_create_with_storage(const kvrt_config *config, const kvrt_layer_spec *layers,
+                             const kvrt_storage *storage, kvrt_ctx **out);
+/* Bytes of the K (== V) tensor and of the K (== V) scale tensor of a layer. */
+int kvrt_layer_storage_bytes(const kvrt_config *config, const kvrt_layer_spec *layer,
+                             uint64_t *kv_bytes, uint64_t *scale_bytes);
+/* Replaces gemma4_cache_destroy (gemma4_listener_cache.cu:463-475). */
+int kvrt_destroy(kvrt_ctx *ctx);
+/* Replaces the bound-stream contract of the batch API
+ * (gemma4_listener_microbatch_impl.inc:445-473). */
+int kvrt_bind_stream(kvrt_ctx *ctx, void *hip_stream);
+/* Device pointers of a layer's storage (shared layers report their source). */
+int kvrt_layer_storage(kvrt_ctx *ctx, int32_t layer, kvrt_storage *out);
+
+/* ---- KV operations --------------------------------------------------------- */
+/* Import a prefix: k, v are [1, kv_heads, S, D] (HF DynamicCache layer view,
+ * strided allowed, last dim contiguous) bf16. Sets the (slot, layer) length
+ * to S. RING keeps the last ring_rows rows; PAGED allocates pages (pages
+ * wholly below first_pos are not stored: first_pos = 0 stores all); INT8
+ * quantises on import.
+ * Replaces gemma4_cache_import_async (gemma4_listener_cache.cu:278-301),
+ * qwen_talker import_cache_prefix (qwen_talker_kernels.cu:276-294,
+ * qwen_talker.cu:1060-1110) and the Python copy at
+ * duplex_kernel/native_qwen_talker.py:781-874. */
+int kvrt_import_async(kvrt_ctx *ctx, int32_t slot, int32_t layer, const kvrt_tensor *k,
+                      const kvrt_tensor *v, int32_t first_pos);
+
+/* Append Q rows to n slots of one layer at each slot's current length:
+ * k, v are [n, kv_heads, Q, D] bf16 (HF key_states layout with batch = n).
+ * Lengths advance by Q. INT8 layers quantise in-kernel
+ * (scale = amax/127, q = clamp(rne(x/scale), -127, 127)).
+ * Replaces HF DynamicLayer.update (transformers cache_utils.py:127-146) as
+ * called through duplex_kernel/kv_cache.py:95-97, gemma4_cache_append_async
+ * (gemma4_listener_cache.cu:182-215) and write_audio_kv / write_joint_kv
+ * (qwen_talker_kernels.cu:207-251). */
+int kvrt_append_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                      const kvrt_tensor *k, const kvrt_tensor *v);
+
+/* Gather n slots of one layer into a zero-padded batch:
+ * out_k, out_v [n, kv_heads, Lmax, D] (bf16 for bf16 layers, fp32
+ * dequantised for INT8 layers); row j of item i holds position
+ * start_i + j for j < L_i - start_i, zeros after. mask [n, Lmax] (KVRT_BOOL:
+ * 1 valid / 0 pad, or KVRT_FP32 / KVRT_BF16: 0 valid / finfo.min pad) may be
+ * NULL. start_pos may be NULL (contig/paged: 0, ring: max(0, L-(W-1)) which
+ * is the HF DynamicSlidingWindowLayer retained range).
+ * Replaces _StaticPaddingWorkspace.padded / padded_mask
+ * (duplex_kernel/shape_stable_listener.py:28-69). */
+int kvrt_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                      const int32_t *start_pos, const kvrt_tensor *out_k,
+                      const kvrt_tensor *out_v, const kvrt_tensor *mask);
+
+/* Turn-local rollback: set the length of (slot, layer) to new_len
+ * (layer = -1: every layer). Moves no KV bytes. Fails with KVRT_ESTATE when
+ * new_len exceeds the current length, or when a RING layer would need rows
+ * already overwritten (L > ring_rows and new_len - window + 1 < L - ring_rows,
+ * i.e. a rollback deeper than ring_rows - window + 1 positions).
+ * Replaces TurnKVState.truncate_to_prefix / _slice_kv
+ * (duplex_kernel/kv_cache.py:99-104, :205-216) and gemma4_cache_truncate_async
+ * (gemma4_listener_cache.cu:409-421). */
+int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len);
+
+/* PAGED: release every page of slot wholly below position keep_from (all
+ * layers share one page table per slot). Positions below keep_from must not
+ * be attended afterwards (the layer window guarantees it). No counterpart in
+ * the reference (paged KV is absent there); bounded-memory decode. */
+int kvrt_evict(kvrt_ctx *ctx, int32_t slot, int32_t keep_from);
+
+/* Copy the first n_tokens rows of every non-shared layer from src_slot to
+ * dst_slot (CONTIG layers; dst lengths become n_tokens). Replaces
+ * copy_static_cache_prefix (duplex_kernel/thinker_cache.py:83-190) and
+ * gemma4_cache_copy_async (gemma4_listener_cache.cu:306-345). */
+int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, int32_t n_tokens);
+
+/* GQA decode attention over the last Q positions of n slots of one layer:
+ * q [n, Hq, Q, D] bf16 contiguous, out [n, Hq, Q, D] bf16 contiguous.
+ * q head h reads kv head h / (Hq / kv_heads) (HF repeat_kv order). Query row
+ * i sits at position p = L - Q + i and sees keys k with k <= p and, for a
+ * sliding layer, k >= p - W + 1. Scores s = (q.k) * scale, softmax and all
+ * accumulation in fp32; out rounded to bf16 (RNE).
+ * Replaces HF sdpa_attention_forward over repeat_kv'd K/V
+ * (shape_stable_listener.py:241-251), gemma4_listener_debug_attention
+ * (gemma4_listener_aten.cpp:100-286), kernel_stream_sdpa_q4_bf16
+ * (gemma4_listener_kernels.cuh:534-665) and qwen_attention_gqa
+ * (qwen_talker_kernels.cu:875-921). */
+int kvrt_attend_decode_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                             const kvrt_tensor *q, const kvrt_tensor *out, float scale);
+
+/* Fused per-layer decode step: append k, v ([n, kv_heads, Q, D]) then attend
+ * q ([n, Hq, Q, D]) — the same results as kvrt_append_async followed by
+ * kvrt_attend_decode_async, in fewer launches. Replaces the per-session
+ * append + attention pair of gemma4_batch_execute_layer
+ * (gemma4_listener_microbatch_impl.inc:2939-2962) and the talker
+ * write_audio_kv + repeat_kv + SDPA sequence (qwen_talker.cu:693-756). */
+int kvrt_append_attend_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                             const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
+                             const kvrt_tensor *out, float scale);
+
+/* ---- context-free tensor kernels ------------------------------------------ */
+/* Decode attention over caller-owned HF-shaped K/V: k, v [n, kv_heads, Lmax, D]
+ * bf16 (strided, last dim contiguous), lengths int32[n] in DEVICE memory,
+ * q/out [n, Hq, Q, D]; window as above (0 = global). Used for the padded
+ * batch produced by kvrt_gather_async and for HF cache objects.
+ * Replaces sdpa_attention_forward on padded K/V + mask
+ * (shape_stable_listener.py:232-251). */
+int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
+                              const int32_t *device_lengths, const kvrt_tensor *out,
+                              float scale, int32_t window, void *hip_stream);
+
+/* Row copy between two 4-D strided tensors of the same element size
+ * (2 or 4 bytes) over dims (d0, d1, rows, D): dst[:, :, :rows] = src[:, :, :rows].
+ * Replaces the per-layer StaticLayer slice copy of copy_static_cache_prefix
+ * (duplex_kernel/thinker_cache.py:164-170). */
+int kvrt_copy_rows_async(const kvrt_tensor *src, const kvrt_tensor *dst, int64_t rows,
+                         void *hip_stream);
+
+/* ---- state / diagnostics ----------------------------------------------------- */
+/* Host-authoritative length of (slot, layer). Replaces
+ * gemma4_cache_valid_kv_len (gemma4_listener_cache.cu:423-425) and
+ * _kv_seq_len (duplex_kernel/kv_cache.py:190-201). */
+int kvrt_session_state(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t *length);
+/* Synchronise the bound stream and reload the host lengths from the device
+ * mirror. Needed after replaying a captured HIP graph of append / fused
+ * calls: replays advance the device lengths only. The split count and
+ * workspace of a captured call are fixed at capture; lengths must stay within
+ * capacity and, for PAGED layers, within mapped pages. No counterpart in the
+ * reference (its graphs use a device cursor, qwen_talker_kernels.cu:349-374). */
+int kvrt_sync_lengths(kvrt_ctx *ctx);
+int kvrt_get_counters(kvrt_ctx *ctx, kvrt_counters *out);
+/* Synchronise the bound stream, then report KVRT_OK, KVRT_EPOISONED,
+ * KVRT_EDEVICE (HIP error) or KVRT_EFAULT (kernel-side bounds flag).
+ * Replaces the stream-query health path (gemma4_listener.cu:180-192) and the
+ * talker device error flag (qwen_talker_kernels.cu:243-246). */
+int kvrt_health(kvrt_ctx *ctx);
+/* Host-side fault injection for failure-path tests: the next mutating call
+ * fails as a device enqueue failure (poisoning the ctx). No kernel runs. */
+int kvrt_debug_inject_failure(kvrt_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVRT_H */

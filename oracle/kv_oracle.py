@@ -1,0 +1,278 @@
+"""CPU oracle for the KV append / gather / truncate / attend hot path.
+
+TEST INFRASTRUCTURE ONLY. This module restates, in numpy, what the reference
+computes on this path. Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker;
+the product (``gemma-4-omni_amd/kvrt``) never imports or calls it.
+
+Semantics restated (reference paths relative to the andr-lab/gemma-4-omni
+tree; HF = transformers.cache_utils, a third-party dependency pinned at
+5.5.0 by the reference Dockerfile:49-51):
+
+* append  — HF ``DynamicLayer.update`` = ``torch.cat([keys, k], dim=-2)``
+  (cache_utils.py:127-146), reached via duplex_kernel/kv_cache.py:95-97;
+  native: gemma4_cache_append_async (native/gemma4_listener_microbatch/
+  gemma4_listener_cache.cu:182-215), write_audio_kv (native/qwen_talker/
+  qwen_talker_kernels.cu:207-251).
+* truncate — ``_slice_kv`` keep the first ``keep_len`` rows
+  (duplex_kernel/kv_cache.py:205-216); native cursor edit
+  gemma4_cache_truncate_async (gemma4_listener_cache.cu:409-421).
+* gather  — ``_StaticPaddingWorkspace.padded/padded_mask``: zero buffer of the
+  target length, valid prefix copied, mask tail ``False`` / ``finfo.min``
+  (duplex_kernel/shape_stable_listener.py:28-69).
+* attend  — ``F.scaled_dot_product_attention`` over ``repeat_kv``'d K/V with
+  fp32 softmax (shape_stable_listener.py:241-251); visibility as
+  kernel_build_explicit_sdpa_mask (gemma4_listener_kernels.cuh:500-525):
+  key k visible to query position p iff k <= p and, for window W > 0,
+  k >= p - W + 1; GQA q head h reads kv head h // (Hq / Hkv).
+* sliding retention — HF ``DynamicSlidingWindowLayer`` keeps the last W-1
+  rows after an update (cache_utils.py:229-261); window start of the native
+  cache ``base - W + 1`` (gemma4_listener_cache.cu:448-452).
+* window range — gemma4_q4_range_from_position
+  (gemma4_listener_kernels.cuh:23-49).
+* int8 KV (no reference implementation; closed form): per (token, head)
+  scale = amax / 127 (fp32), q = clamp(round_half_even(x / scale), -127, 127),
+  dequant = q * scale (fp32); amax == 0 gives scale 0 and q = 0.
+
+bf16 values are carried as float32 arrays holding exactly-representable
+bf16 values (or as uint16 bit patterns where bitwise identity is asserted).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit pattern, round to nearest even (quiet NaN kept)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return (r & 0xFFFF).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bf16 value (returned as float32)."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+# ---------------------------------------------------------------------------
+# window / position math
+# ---------------------------------------------------------------------------
+
+
+def q_range_from_position(base_position: int, q_len: int, capacity: int, sliding_window: int):
+    """(total_k_len, start_offset, valid) of a Q-row step at base_position.
+
+    Restates gemma4_q4_range_from_position (gemma4_listener_kernels.cuh:23-39).
+    """
+    total = base_position + q_len
+    start = base_position - sliding_window + 1 if (sliding_window > 0 and base_position >= sliding_window) else 0
+    valid = q_len > 0 and total <= capacity and start < total
+    return min(total, 2**32 - 1), start, valid
+
+
+def visible_range(query_position: int, window: int) -> tuple[int, int]:
+    """Inclusive [lo, hi] of the keys visible to one query position."""
+    lo = max(0, query_position - window + 1) if window > 0 else 0
+    return lo, query_position
+
+
+def ring_capacity(window: int, max_q: int, max_seq_len: int) -> int:
+    """Rows a sliding layer must retain: W + q - 1, capped by max_seq_len.
+
+    Restates derive_contract (native/gemma4_listener_microbatch/
+    sliding_repeat_capacity.h:30-60).
+    """
+    return min(window + max_q - 1, max_seq_len)
+
+
+# ---------------------------------------------------------------------------
+# int8 quantisation
+# ---------------------------------------------------------------------------
+
+
+def quantize_int8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric int8 per row (last axis): returns (q int8 [..., D], scale fp32 [...])."""
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.max(np.abs(x), axis=-1).astype(np.float32)
+    scale = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.rint(x / scale[..., None]).astype(np.float32)
+    r = np.where(amax[..., None] > 0, np.clip(r, -127, 127), 0)
+    return r.astype(np.int8), scale
+
+
+def dequantize_int8(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    return (q.astype(np.float32) * scale[..., None].astype(np.float32)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+
+def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_positions: np.ndarray, scale: float,
+           window: int = 0, key_positions: np.ndarray | None = None) -> np.ndarray:
+    """Masked GQA attention, float64 softmax.
+
+    q [Hq, Q, D]; k, v [Hkv, L, D] (already dequantised, float32);
+    q_positions [Q] absolute query positions; key_positions [L] absolute key
+    positions (default 0..L-1). Returns float32 [Hq, Q, D]; a row with no
+    visible key is 0.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    hq, qn, d = q.shape
+    hkv, n_keys, _ = k.shape
+    if hq % hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    g = hq // hkv
+    kp = np.arange(n_keys) if key_positions is None else np.asarray(key_positions)
+    out = np.zeros((hq, qn, d), dtype=np.float64)
+    for h in range(hq):
+        kh = h // g  # HF repeat_kv: kv head j serves q heads j*g .. j*g+g-1
+        s = (q[h] @ k[kh].T) * float(scale)  # [Q, L]
+        for i in range(qn):
+            lo, hi = visible_range(int(q_positions[i]), window)
+            vis = (kp >= lo) & (kp <= hi)
+            if not vis.any():
+                continue
+            row = np.where(vis, s[i], -np.inf)
+            row = row - row[vis].max()
+            p = np.exp(row)
+            p /= p.sum()
+            out[h, i] = p @ v[kh]
+    return out.astype(np.float32)
+
+
+def attend_bruteforce(q, k, v, q_positions, scale, window=0):
+    """Pure-Python-loop attention (tiny shapes only): golden-vector generator."""
+    hq, qn, d = len(q), len(q[0]), len(q[0][0])
+    hkv, n_keys = len(k), len(k[0])
+    g = hq // hkv
+    out = [[[0.0] * d for _ in range(qn)] for _ in range(hq)]
+    import math
+    for h in range(hq):
+        kh = h // g
+        for i in range(qn):
+            p_pos = q_positions[i]
+            vis = [j for j in range(n_keys) if j <= p_pos and (window <= 0 or j >= p_pos - window + 1)]
+            if not vis:
+                continue
+            scores = {j: sum(q[h][i][t] * k[kh][j][t] for t in range(d)) * scale for j in vis}
+            m = max(scores.values())
+            w = {j: math.exp(s - m) for j, s in scores.items()}
+            z = sum(w.values())
+            for t in range(d):
+                out[h][i][t] = sum(w[j] * v[kh][j][t] for j in vis) / z
+    return out
+
+
+# ---------------------------------------------------------------------------
+# logical cache model
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class OracleLayer:
+    kv_heads: int
+    head_dim: int
+    window: int = 0
+    int8: bool = False
+
+
+@dataclass
+class OracleCache:
+    """Logical KV of n_slots sessions: per (slot, layer) full-history rows.
+
+    Keeps every appended row (float32 values; int8 layers keep the quantised
+    ints and scales), which is the logical view all layouts must reproduce.
+    """
+
+    layers: list
+    n_slots: int
+    k: dict = field(default_factory=dict)
+    v: dict = field(default_factory=dict)
+    ks: dict = field(default_factory=dict)
+    vs: dict = field(default_factory=dict)
+
+    def _get(self, slot, layer):
+        key = (slot, layer)
+        if key not in self.k:
+            spec = self.layers[layer]
+            dt = np.int8 if spec.int8 else np.float32
+            self.k[key] = np.zeros((spec.kv_heads, 0, spec.head_dim), dtype=dt)
+            self.v[key] = np.zeros((spec.kv_heads, 0, spec.head_dim), dtype=dt)
+            self.ks[key] = np.zeros((spec.kv_heads, 0), dtype=np.float32)
+            self.vs[key] = np.zeros((spec.kv_heads, 0), dtype=np.float32)
+        return key
+
+    def length(self, slot: int, layer: int) -> int:
+        return self.k[self._get(slot, layer)].shape[1]
+
+    def append(self, slot: int, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        """k, v [Hkv, Q, D] float32 (bf16 values): concatenate along positions."""
+        key = self._get(slot, layer)
+        if self.layers[layer].int8:
+            kq, ksc = quantize_int8(k)
+            vq, vsc = quantize_int8(v)
+            self.k[key] = np.concatenate([self.k[key], kq], axis=1)
+            self.v[key] = np.concatenate([self.v[key], vq], axis=1)
+            self.ks[key] = np.concatenate([self.ks[key], ksc], axis=1)
+            self.vs[key] = np.concatenate([self.vs[key], vsc], axis=1)
+        else:
+            self.k[key] = np.concatenate([self.k[key], np.asarray(k, np.float32)], axis=1)
+            self.v[key] = np.concatenate([self.v[key], np.asarray(v, np.float32)], axis=1)
+
+    def truncate(self, slot: int, layer: int, keep_len: int) -> None:
+        key = self._get(slot, layer)
+        for d in (self.k, self.v, self.ks, self.vs):
+            d[key] = d[key][:, :keep_len]
+
+    def values(self, slot: int, layer: int) -> tuple[np.ndarray, np.ndarray]:
+        """Dequantised float32 K, V [Hkv, L, D]."""
+        key = self._get(slot, layer)
+        if self.layers[layer].int8:
+            return dequantize_int8(self.k[key], self.ks[key]), dequantize_int8(self.v[key], self.vs[key])
+        return self.k[key], self.v[key]
+
+    def gather(self, layer: int, slots: list[int], lmax: int, start: list[int] | None = None):
+        """Padded [n, Hkv, lmax, D] float32 K, V and bool mask [n, lmax]."""
+        spec = self.layers[layer]
+        n = len(slots)
+        ko = np.zeros((n, spec.kv_heads, lmax, spec.head_dim), np.float32)
+        vo = np.zeros_like(ko)
+        mask = np.zeros((n, lmax), bool)
+        for i, s in enumerate(slots):
+            kk, vv = self.values(s, layer)
+            st = 0 if start is None else start[i]
+            m = kk.shape[1] - st
+            ko[i, :, :m] = kk[:, st:]
+            vo[i, :, :m] = vv[:, st:]
+            mask[i, :m] = True
+        return ko, vo, mask
+
+    def attend(self, slot: int, layer: int, q: np.ndarray, scale: float) -> np.ndarray:
+        """q [Hq, Q, D] at the last Q positions of (slot, layer)."""
+        kk, vv = self.values(slot, layer)
+        n_keys = kk.shape[1]
+        qn = q.shape[1]
+        pos = np.arange(n_keys - qn, n_keys)
+        return attend(q, kk, vv, pos, scale, self.layers[layer].window)
+
+
+def sliding_retained(length: int, window: int) -> tuple[int, int]:
+    """[start, length) rows an HF DynamicSlidingWindowLayer keeps after updates."""
+    return max(0, length - (window - 1)), length

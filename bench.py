@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""KV append + decode-attention benchmark on one MI355X.
+
+Workload (the north-star step of BASELINE.json): 4 micro-batched streams,
+each running
+  * a Gemma-4-E2B-shaped thinker stack: 30 layers, 8 q heads / 1 KV head,
+    head_dim 256, bf16; 5 sliding (512-token ring) : 1 global, global layers
+    at 4096 positions of context;
+  * a Qwen3-TTS-shaped talker stack: 28 layers, 16 q / 8 KV heads,
+    head_dim 128, bf16, 4096 positions of context;
+and per step and layer: append one token of K/V, then GQA decode attention
+over the visible keys (fused kvrt_append_attend_async, one launch per layer
+and model, all 4 streams in the launch). One step = 58 launches, captured
+once in a HIP graph and replayed. Inputs are synthetic (seeded N(0,1)) and
+resident in HBM before the timed region.
+
+A token = one decode position of one stream in one model, so a step
+appends 8 tokens (4 streams x {thinker, talker}).
+
+Prints ONE JSON line (see the keys below). ``--gpus N`` with N > 1 exits:
+this benchmark runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "gemma-4-omni_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK = 8.0e12  # B/s, MI355X published HBM3E bandwidth
+
+THINKER = dict(layers=30, hq=8, hkv=1, d=256, window=512, pattern=6)  # layer i global iff (i+1) % 6 == 0
+TALKER = dict(layers=28, hq=16, hkv=8, d=128)
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--streams", type=int, default=4)
+    p.add_argument("--ctx", type=int, default=4096, help="context positions at the first timed step")
+    p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--kernel-reps", type=int, default=50, help="event-timed launches of the dominant kernel")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
+    p.add_argument("--calib-copy", action="store_true",
+                   help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
+    return p.parse_args()
+
+
+def thinker_is_global(i: int) -> bool:
+    return (i + 1) % THINKER["pattern"] == 0
+
+
+def build_runtimes(args, capacity: int):
+    from kvrt import KVRuntime, LayerSpec
+
+    th_specs = []
+    for i in range(THINKER["layers"]):
+        if thinker_is_global(i):
+            th_specs.append(LayerSpec(kv_heads=THINKER["hkv"], head_dim=THINKER["d"]))
+        else:
+            th_specs.append(LayerSpec(kv_heads=THINKER["hkv"], head_dim=THINKER["d"], layout="ring",
+                                      window=THINKER["window"], ring_rows=THINKER["window"]))
+    tk_specs = [LayerSpec(kv_heads=TALKER["hkv"], head_dim=TALKER["d"]) for _ in range(TALKER["layers"])]
+    thinker = KVRuntime(th_specs, args.streams, capacity, max_q=1, device="cuda")
+    talker = KVRuntime(tk_specs, args.streams, capacity, max_q=1, device="cuda")
+    return thinker, talker
+
+
+def prefill(rt, hkv: int, d: int, n_layers: int, streams: int, ctx: int, gen: torch.Generator) -> None:
+    for layer in range(n_layers):
+        for s in range(streams):
+            k = torch.randn((1, hkv, ctx, d), generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+            v = torch.randn((1, hkv, ctx, d), generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+            rt.import_(s, layer, k, v)
+    torch.cuda.synchronize()
+
+
+class Step:
+    """Per-layer q/k/v/out buffers and the 58-launch decode step."""
+
+    def __init__(self, thinker, talker, streams: int, gen: torch.Generator) -> None:
+        self.thinker, self.talker = thinker, talker
+        self.slots = list(range(streams))
+
+        def mk(shape, scale):
+            return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16)
+
+        n = streams
+        self.th = [(mk((n, THINKER["hq"], 1, THINKER["d"]), 0.5), mk((n, THINKER["hkv"], 1, THINKER["d"]), 0.5),
+                    mk((n, THINKER["hkv"], 1, THINKER["d"]), 0.5),
+                    torch.empty((n, THINKER["hq"], 1, THINKER["d"]), dtype=torch.bfloat16, device="cuda"))
+                   for _ in range(THINKER["layers"])]
+        self.tk = [(mk((n, TALKER["hq"], 1, TALKER["d"]), 0.5), mk((n, TALKER["hkv"], 1, TALKER["d"]), 0.5),
+                    mk((n, TALKER["hkv"], 1, TALKER["d"]), 0.5),
+                    torch.empty((n, TALKER["hq"], 1, TALKER["d"]), dtype=torch.bfloat16, device="cuda"))
+                   for _ in range(TALKER["layers"])]
+        self.th_scale = 1.0 / math.sqrt(THINKER["d"])
+        self.tk_scale = 1.0 / math.sqrt(TALKER["d"])
+
+    def __call__(self) -> None:
+        for i, (q, k, v, o) in enumerate(self.th):
+            self.thinker.append_attend(i, q, k, v, self.slots, self.th_scale, out=o)
+        for i, (q, k, v, o) in enumerate(self.tk):
+            self.talker.append_attend(i, q, k, v, self.slots, self.tk_scale, out=o)
+
+
+def step_bytes(streams: int, ctx_after: int) -> dict:
+    """Algorithmic HBM bytes of one step whose appends end at length ctx_after.
+
+    Visible K+V rows read, plus append writes and source reads, plus q reads
+    and output writes (repeat/mask/padding traffic excluded by definition).
+    """
+    th_row = THINKER["hkv"] * THINKER["d"] * 2 * 2  # K+V bf16 bytes per position
+    tk_row = TALKER["hkv"] * TALKER["d"] * 2 * 2
+    th_q = THINKER["hq"] * THINKER["d"] * 2
+    tk_q = TALKER["hq"] * TALKER["d"] * 2
+    th = 0
+    for i in range(THINKER["layers"]):
+        vis = ctx_after if thinker_is_global(i) else min(ctx_after, THINKER["window"])
+        th += vis * th_row + 2 * th_row + 2 * th_q
+    tk_layer = ctx_after * tk_row + 2 * tk_row + 2 * tk_q
+    tk = TALKER["layers"] * tk_layer
+    return {"thinker": streams * th, "talker": streams * tk, "talker_layer": streams * tk_layer,
+            "total": streams * (th + tk)}
+
+
+def time_dominant_kernel(talker, step: Step, reps: int) -> tuple[float, int]:
+    """Average duration of one talker-layer decode launch (HIP events on its stream).
+
+    A GPU sleep ahead of each (event, launch, event) triple lets the host
+    enqueue all three before the GPU reaches them, so the events bracket the
+    kernel and not the host launch latency.
+    """
+    q, k, v, o = step.tk[0]
+    stream = torch.cuda.current_stream()
+    times = []
+    bytes_total = 0
+    for _ in range(reps):
+        L_before = talker.seq_length(0, 0)
+        torch.cuda._sleep(2_000_000)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        talker.append_attend(0, q, k, v, step.slots, step.tk_scale, out=o)
+        e1.record(stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3)
+        bytes_total += step_bytes(len(step.slots), L_before + 1)["talker_layer"]
+    times.sort()
+    # mean of the central 80 % (drop warm-up and preemption outliers)
+    lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
+    mean_t = sum(times[lo:hi]) / (hi - lo)
+    return mean_t, bytes_total // reps
+
+
+def cpu_baseline(args) -> dict | None:
+    """The reference's Python path restated on CPU tensors (oracle/torch_ref.py)."""
+    if args.cpu_seconds <= 0:
+        return None
+    from oracle import torch_ref as R
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(0)
+    n = args.streams
+    th_layers = [R.RefLayer(0 if thinker_is_global(i) else THINKER["window"]) for i in range(THINKER["layers"])]
+    tk_layers = [R.RefLayer(0) for _ in range(TALKER["layers"])]
+    for i, layer in enumerate(th_layers):
+        keep = args.ctx if thinker_is_global(i) else THINKER["window"] - 1
+        kv = torch.randn((n, THINKER["hkv"], keep, THINKER["d"]), generator=gen).to(torch.bfloat16)
+        layer.keys, layer.values = kv, kv.clone()
+        layer.cumulative_length = args.ctx
+    for layer in tk_layers:
+        kv = torch.randn((n, TALKER["hkv"], args.ctx, TALKER["d"]), generator=gen).to(torch.bfloat16)
+        layer.keys, layer.values = kv, kv.clone()
+        layer.cumulative_length = args.ctx
+    qt = torch.randn((n, THINKER["hq"], 1, THINKER["d"]), generator=gen).to(torch.bfloat16)
+    kt = torch.randn((n, THINKER["hkv"], 1, THINKER["d"]), generator=gen).to(torch.bfloat16)
+    qk = torch.randn((n, TALKER["hq"], 1, TALKER["d"]), generator=gen).to(torch.bfloat16)
+    kk = torch.randn((n, TALKER["hkv"], 1, TALKER["d"]), generator=gen).to(torch.bfloat16)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for i, layer in enumerate(th_layers):
+            fk, fv = layer.update(kt, kt)
+            R.attend(qt, fk, fv, 1 / 16.0, 0 if thinker_is_global(i) else THINKER["window"],
+                     first_key_pos=layer.cumulative_length - fk.shape[2])
+        for layer in tk_layers:
+            fk, fv = layer.update(kk, kk)
+            R.attend(qk, fk, fv, 1 / math.sqrt(128))
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or steps >= 50:
+            break
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(2 * n * steps / el, 3),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{steps} step(s) of the same {n}-stream thinker+talker step at {args.ctx} context on CPU: "
+                   "torch.cat append (HF DynamicLayer/DynamicSlidingWindowLayer.update) + "
+                   "F.scaled_dot_product_attention(enable_gqa) per layer, bf16"),
+        "ms_per_step": round(1e3 * el / steps, 3),
+        "cpu_model": cpu_model,
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
+              "sessions shard across GPUs with no exchange, so run one process per GPU.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    margin = args.warmup + args.steps + args.kernel_reps + 8
+    capacity = args.ctx + margin
+    thinker, talker = build_runtimes(args, capacity)
+    # Prefill to ctx - 1 so that the first timed append lands at position ctx - 1 + warm-up.
+    prefill(thinker, THINKER["hkv"], THINKER["d"], THINKER["layers"], args.streams, args.ctx - 1, gen)
+    prefill(talker, TALKER["hkv"], TALKER["d"], TALKER["layers"], args.streams, args.ctx - 1, gen)
+    step = Step(thinker, talker, args.streams, gen)
+
+    step()  # eager step: sizes the split-K workspaces before any capture
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        # capture recorded the launches without running them
+        thinker.sync_lengths()
+        talker.sync_lengths()
+    run = graph.replay if graph is not None else step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    if graph is not None:  # replays advance the device lengths only
+        thinker.sync_lengths()
+        talker.sync_lengths()
+    len0 = talker.seq_length(0, 0)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    thinker.sync_lengths()
+    talker.sync_lengths()
+    len1 = talker.seq_length(0, 0)
+    if len1 - len0 != args.steps:
+        raise RuntimeError(f"device lengths advanced by {len1 - len0}, expected {args.steps}")
+    for rt in (thinker, talker):
+        if rt.health() != 0:
+            raise RuntimeError("kvrt health check failed after the timed region")
+
+    total_bytes = sum(step_bytes(args.streams, L)["total"] for L in range(len0 + 1, len1 + 1))
+    ms = 1e3 * elapsed / args.steps
+    tokens_per_step = 2 * args.streams
+    k_time, k_bytes = time_dominant_kernel(talker, step, args.kernel_reps)
+    if talker.health() != 0:
+        raise RuntimeError("kvrt health check failed after the kernel timing")
+    achieved = k_bytes / k_time
+    if args.calib_copy:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+    cpu = cpu_baseline(args)
+    out = {
+        "metric": "KV append+decode-attn tokens/s, HBM GB/s (% of peak), 1 MI355X",
+        "value": round(tokens_per_step * args.steps / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "north-star step: 4 streams x (thinker 30L [25 ring-512 + 5 global] Hq8/Hkv1 D256 "
+                        "+ talker 28L Hq16/Hkv8 D128), 1 token append + GQA decode per layer, bf16",
+            "streams": args.streams,
+            "context_first_step": len0 + 1,
+            "context_last_step": len1,
+            "launches_per_step": THINKER["layers"] + TALKER["layers"],
+            "hip_graph": graph is not None,
+            "tokens_per_step": tokens_per_step,
+        },
+        "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
+        "step_hbm_frac": round(total_bytes / elapsed / HBM_PEAK, 4),
+        "step_algorithmic_bytes": total_bytes // args.steps,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "kvrt::decode_kernel<128,2,bf16,contig> (talker layer, 4 streams, fused append)",
+            "achieved": round(achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": None,
+            "avg_launch_us": round(k_time * 1e6, 3),
+            "algorithmic_bytes_per_launch": k_bytes,
+        },
+        "cpu_baseline": cpu,
+        "host": platform.node(),
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

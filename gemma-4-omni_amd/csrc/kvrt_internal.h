@@ -99,7 +99,7 @@ struct DecodeArgs {
     int32_t qn;             // Q
     int32_t window;
     int32_t n_split;        // wave splits per (item, kv head) = gridDim.x * kWaves
-    int32_t advance;        // merge kernel adds qn to each item's length
+    int32_t advance;        // the merge kernel adds qn to each item's length
     float scale_log2;       // softmax scale * log2(e)
     int32_t slots[kMaxItems];
 };
@@ -122,7 +122,7 @@ struct CopyRowsArgs {
 // ---- launchers (kvrt_kernels.hip) ----------------------------------------
 hipError_t launch_append(const AppendArgs &a, int head_dim, int dtype, int grid_x, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream_t s);
-// Attention over the view with split-K partials, then the merge kernel.
+// Split-K attention over the view, then the merge kernel.
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head,
                          hipStream_t s);
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);

@@ -4,8 +4,10 @@
 //                   PAGED rows (bf16 copy or int8 quantise-on-write)
 //   gather_kernel   ragged N-stream gather into a zero-padded batch + mask
 //   decode_kernel   GQA split-K decode attention, one wave per key split,
-//                   fp32 online softmax, partial (m, l, acc) per split
-//   merge_kernel    deterministic log-sum-exp merge of the splits -> bf16
+//                   fp32 online softmax; the waves of a workgroup merge in
+//                   LDS and write one partial (m, l, acc) per workgroup
+//   merge_kernel    log-sum-exp merge of the partials in fixed order
+//                   (deterministic) -> bf16, then the fused length advance
 //   set_i32_kernel  length / page-table edits carried in the kernarg block
 //   copy_rows_kernel, zero_kernel
 //
@@ -202,6 +204,76 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 // ---------------------------------------------------------------------------
 // decode attention (split-K)
 // ---------------------------------------------------------------------------
+// LDS floats a decode workgroup needs: the wave partials of waves 1..3
+// (workgroup merge, when R*D is small enough) or the fix-up weights.
+template <int D, int R>
+struct DecodeLds {
+    static constexpr bool kWgMerge = R * D <= 4096;
+    static constexpr int kMaxParts = 256;  // partials merged by the fix-up
+    static constexpr int kMerge = kWgMerge ? (kWaves - 1) * R * D : 0;
+    static constexpr int kFixup = kMaxParts * R + 2 * R;
+    static constexpr int kFloats = kMerge > kFixup ? kMerge : kFixup;
+};
+
+// Log-sum-exp merge of the n_parts partials of one (item, kv head) into bf16
+// outputs. Weights exp2(m_s - M) / L are computed once per (part, row) into
+// LDS; the output sums then stream the partials with independent loads.
+// Parts are summed in index order, so the result does not depend on which
+// workgroup performs the merge.
+template <int D, int R>
+__device__ void merge_group(const DecodeArgs &a, int item, int kvh, int hkv, int n_parts, float *lds) {
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const int hq = hkv * a.group;
+    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
+    float *w = lds;                      // [n_parts][R]: m, then the weight
+    float *lsum = lds + n_parts * R;     // [n_parts][R] partial l (reused below)
+    float *row_inv = lds + 2 * n_parts * R;  // [R]: 1 / L_r
+    float *row_max = row_inv + R;             // [R]: M_r
+    for (int i = threadIdx.x; i < n_parts * R; i += blockDim.x) {
+        const float2 ml = a.part_ml[pbase + i];
+        w[i] = ml.x;
+        lsum[i] = ml.y;
+    }
+    __syncthreads();
+    // one wave per row: max and sum over the parts
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int r = wave; r < rows; r += kWaves) {
+        float m = kNegBig;
+        for (int s = lane; s < n_parts; s += 64) m = fmaxf(m, w[s * R + r]);
+        m = group_max<64>(m);
+        float l = 0.f;
+        for (int s = lane; s < n_parts; s += 64) l += lsum[s * R + r] * __builtin_amdgcn_exp2f(w[s * R + r] - m);
+        l = group_sum<64>(l);
+        if (lane == 0) {
+            row_max[r] = m;
+            row_inv[r] = l > 0.f ? 1.0f / l : 0.f;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_parts * R; i += blockDim.x) {
+        const int r = i % R;
+        w[i] = r < rows ? __builtin_amdgcn_exp2f(w[i] - row_max[r]) * row_inv[r] : 0.f;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
+        const int r = idx / D, d = idx % D;
+        const float *src = a.part_acc + (pbase + r) * D + d;
+        float acc = 0.f;
+        int s = 0;
+        for (; s + 8 <= n_parts; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(s + u) * R * D];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fmaf(w[(s + u) * R + r], v[u], acc);
+        }
+        for (; s < n_parts; ++s) acc = fmaf(w[s * R + r], src[(int64_t)s * R * D], acc);
+        const int j = r / Qn, i = r % Qn;
+        a.out[(((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(acc);
+    }
+}
+
 // grid (n_split / kWaves, kv_heads, n_items), 256 threads = kWaves waves.
 // Wave w of workgroup x owns key split s = x*kWaves + w: a contiguous key
 // range. Inside a wave, LPR = D/VEC lanes share one key row (VEC elements =
@@ -423,8 +495,52 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             m_run[r] = M;
         }
     }
-    if (sub == 0) {
-        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + split) * R;
+    using Lds = DecodeLds<D, R>;
+    __shared__ float lds[Lds::kFloats];
+    __shared__ float2 lds_ml[kWaves * R];
+    int part;
+    if constexpr (Lds::kWgMerge) {
+        // Workgroup merge: waves 1..3 hand their partials to wave 0 in LDS.
+        part = blockIdx.x;
+        if (sub == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (wave > 0) {
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) lds[((wave - 1) * R + r) * D + seg * VEC + e] = acc[r][e];
+                }
+                if (seg == 0) lds_ml[wave * R + r] = make_float2(m_run[r], l_run[r]);
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float M = m_run[r];
+#pragma unroll
+                for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
+                const float w0 = __builtin_amdgcn_exp2f(m_run[r] - M);
+                float L = l_run[r] * w0;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc[r][e] *= w0;
+#pragma unroll
+                for (int w2 = 1; w2 < kWaves; ++w2) {
+                    const float2 ml = lds_ml[w2 * R + r];
+                    const float ww = __builtin_amdgcn_exp2f(ml.x - M);
+                    L = fmaf(ml.y, ww, L);
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e)
+                        acc[r][e] = fmaf(lds[((w2 - 1) * R + r) * D + seg * VEC + e], ww, acc[r][e]);
+                }
+                m_run[r] = M;
+                l_run[r] = L;
+            }
+        }
+    } else {
+        part = split;
+    }
+    if (sub == 0 && (!Lds::kWgMerge || wave == 0)) {
+        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + part) * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (r < rows) {
@@ -436,37 +552,24 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             }
         }
     }
+
 }
 
-// grid (kv_heads, n_items), 256 threads. Splits are merged in index order, so
-// the result does not depend on workgroup scheduling.
+// grid (kv_heads, n_items), 256 threads: merges the parts of one (item, kv
+// head) written by decode_kernel. Runs after it in stream order, so every
+// part is visible without device-scope fences (which on gfx950 write back
+// and invalidate the whole L2 of an XCD). The merge of kv head 0 also
+// advances the item's length after a fused append: all decode workgroups
+// have read the lengths by then.
 template <int D, int R>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-    const int item = blockIdx.y;
-    const int kvh = blockIdx.x;
-    const int hkv = gridDim.x;
-    const int Qn = a.qn;
-    const int rows = a.group * Qn;
-    const int hq = hkv * a.group;
-    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;
-    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
-        const int r = idx / D, d = idx % D;
-        float M = kNegBig;
-        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, a.part_ml[pbase + s * R + r].x);
-        float L = 0.f, A = 0.f;
-        for (int s = 0; s < a.n_split; ++s) {
-            const float2 ml = a.part_ml[pbase + s * R + r];
-            const float w = __builtin_amdgcn_exp2f(ml.x - M);
-            L = fmaf(ml.y, w, L);
-            A = fmaf(a.part_acc[(pbase + s * R + r) * D + d], w, A);
-        }
-        const float o = L > 0.f ? A / L : 0.f;
-        const int j = r / Qn, i = r % Qn;
-        a.out[(((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(o);
-    }
-    if (a.advance && kvh == 0 && threadIdx.x == 0) {
-        a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += Qn;
-    }
+    using Lds = DecodeLds<D, R>;
+    __shared__ float lds[Lds::kFloats];
+    const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
+    const int n_parts = Lds::kWgMerge ? a.n_split / kWaves : a.n_split;
+    merge_group<D, R>(a, item, kvh, hkv, n_parts, lds);
+    if (a.advance && kvh == 0 && threadIdx.x == 0)
+        a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += a.qn;
 }
 
 // ---------------------------------------------------------------------------

@@ -98,7 +98,11 @@ int begin(kvrt_ctx *c) {
         c->inject = false;
         return poison(c);
     }
-    if (hipSetDevice(c->device) != hipSuccess) return poison(c);
+    // Switch devices only when needed: hipSetDevice is refused inside a
+    // stream capture, and calls of one context are captured into graphs.
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return poison(c);
+    if (cur != c->device && hipSetDevice(c->device) != hipSuccess) return poison(c);
     return KVRT_OK;
 }
 
@@ -175,10 +179,60 @@ bool is_contiguous(const kvrt_tensor *t) {
     return true;
 }
 
+constexpr int kMaxWgPerHead = 64;
+
+int target_wgs() {
+    static const int v = env_int("KVRT_TARGET_WGS", 512);
+    return v;
+}
+int min_keys_per_wave() {
+    static const int v = env_int("KVRT_MIN_KEYS_PER_WAVE", 32);
+    return v;
+}
+
+// Number of wave splits per (item, kv head): enough workgroups to fill the
+// chip, but at least min_keys keys per wave. n_items * kv_heads * (splits /
+// kWaves) <= target_wgs + n_items * kv_heads, which bounds the workspace.
+int choose_splits(int n_items, int kv_heads, int64_t max_keys) {
+    const int per_head = n_items * kv_heads;
+    const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave();
+    int wg = (target_wgs() + per_head - 1) / per_head;
+    const int64_t cap = std::max<int64_t>(1, (max_keys + per_wg - 1) / per_wg);
+    if (wg > cap) wg = (int)cap;
+    if (wg > kMaxWgPerHead) wg = kMaxWgPerHead;  // fix-up merges <= 256 wave partials
+    if (wg < 1) wg = 1;
+    return wg * kWaves;
+}
+
+// Split-K workspace bytes for n items of kv_heads heads, R rows, head dim D.
+size_t workspace_bytes(int n_items, int kv_heads, int n_split, int R, int D) {
+    const size_t parts = (size_t)n_items * kv_heads * n_split * R;
+    return ((parts * D + 63) / 64) * 64 * 4 + parts * 8 + 256;
+}
+
+// Largest workspace any call on this context can need (max_q rows of up to
+// 16 q heads per kv head -> R <= 16).
+size_t workspace_bound(const kvrt_ctx *c) {
+    const int n = std::min(c->cfg.n_slots, kMaxItems);
+    size_t best = 0;
+    for (const Layer &L : c->layers) {
+        const int hkv = L.spec.kv_heads;
+        const int total_wgs = std::min(target_wgs() + n * hkv, n * hkv * kMaxWgPerHead);
+        const size_t parts = (size_t)total_wgs * kWaves * 16;
+        best = std::max(best, ((parts * L.spec.head_dim + 63) / 64) * 64 * 4 + parts * 8 + 256);
+    }
+    return best;
+}
+
 int ensure_workspace(kvrt_ctx *c, size_t bytes) {
     if (bytes <= c->ws_bytes) return KVRT_OK;
+    // Never allocate inside a stream capture (the bound sized at create
+    // covers every call, so this only triggers if the tuning changed).
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone)
+        return KVRT_ESTATE;
     if (c->ws) {
-        c->retired_ws.push_back(c->ws);
+        c->retired_ws.push_back(c->ws);  // a captured graph may still use it
         c->ws = nullptr;
         c->ws_bytes = 0;
     }
@@ -189,19 +243,6 @@ int ensure_workspace(kvrt_ctx *c, size_t bytes) {
     }
     c->ws_bytes = want;
     return KVRT_OK;
-}
-
-// Number of wave splits per (item, kv head): enough workgroups to fill the
-// chip, but at least min_keys keys per wave.
-int choose_splits(int n_items, int kv_heads, int64_t max_keys) {
-    static const int target_wgs = env_int("KVRT_TARGET_WGS", 512);
-    static const int min_keys = env_int("KVRT_MIN_KEYS_PER_WAVE", 64);
-    const int per_head = n_items * kv_heads;
-    int wg = (target_wgs + per_head - 1) / per_head;
-    const int64_t cap = std::max<int64_t>(1, (max_keys + (int64_t)kWaves * min_keys - 1) / ((int64_t)kWaves * min_keys));
-    if (wg > cap) wg = (int)cap;
-    if (wg < 1) wg = 1;
-    return wg * kWaves;
 }
 
 int visible_keys(const kvrt_layer_spec &s, int len, int q) {
@@ -383,6 +424,8 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
         for (int p = cfg->pool_pages - 1; p >= 0; --p) c->free_pages.push_back(p);
         c->first_live.assign(cfg->n_slots, 0);
     }
+    c->ws_bytes = 0;
+    if (ensure_workspace(c, workspace_bound(c)) != KVRT_OK) return fail(KVRT_EDEVICE);
     if (hipDeviceSynchronize() != hipSuccess) return fail(KVRT_EDEVICE);
     *out = c;
     return KVRT_OK;
@@ -430,9 +473,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int n_split = choose_splits(n, hkv, max_keys);
     const int R = rows_tile(rows);
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
-    const size_t ml_elems = (size_t)n * hkv * n_split * R;
-    const size_t bytes = acc_elems * 4 + ml_elems * 8 + 256;
-    int rc = ensure_workspace(c, bytes);
+    int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
     if (rc != KVRT_OK) return rc;
     std::vector<int32_t> pidx, pval;
     if (fused && s.layout == KVRT_LAYOUT_PAGED) {
@@ -531,6 +572,9 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     }
     return KVRT_OK;
 }
+
+// Floats before the partials in the context-free workspace (error flag).
+constexpr size_t kTensorWsHead = 64;
 
 struct TensorWorkspace {
     std::mutex mu;
@@ -893,7 +937,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
             return KVRT_EINVAL;
     const int64_t n = q->dims[0], hq = q->dims[1], qn = q->dims[2], D = q->dims[3];
     const int64_t hkv = k->dims[1], lmax = k->dims[2];
-    if (n <= 0 || n > kMaxItems || k->dims[0] != n || k->dims[3] != D || hkv <= 0 || hq % hkv != 0 || qn <= 0 ||
+    if (n <= 0 || n > kMaxItems || k->dims[0] != n || k->dims[3] != D || hkv <= 0 || hkv > 64 || hq % hkv != 0 || qn <= 0 ||
         qn > 64)
         return KVRT_EINVAL;
     if (D != 64 && D != 128 && D != 256 && D != 512) return KVRT_EINVAL;
@@ -924,7 +968,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     for (int i = 0; i < n; ++i) a.slots[i] = i;
     const int R = rows_tile(rows);
     const size_t acc_elems = (size_t)n * hkv * a.n_split * R * D;
-    const size_t bytes = acc_elems * 4 + (size_t)n * hkv * a.n_split * R * 8 + 256 + 16;
+    const size_t bytes = (kTensorWsHead + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * R * 8;
     std::lock_guard<std::mutex> lock(g_tensor_ws.mu);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
@@ -937,14 +981,15 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     if (!g_tensor_ws.ptr) {
         const size_t want = std::max(bytes, (size_t)1 << 20);
         if (hipMalloc(&g_tensor_ws.ptr, want) != hipSuccess) return KVRT_EDEVICE;
-        if (launch_zero(g_tensor_ws.ptr, 16, static_cast<hipStream_t>(stream)) != hipSuccess) return KVRT_EDEVICE;
+        if (launch_zero(g_tensor_ws.ptr, kTensorWsHead * 4, static_cast<hipStream_t>(stream)) != hipSuccess)
+            return KVRT_EDEVICE;
         g_tensor_ws.bytes = want;
         g_tensor_ws.device = dev;
     }
-    // First 16 bytes hold the error flag of this path.
+    // Head of the workspace: the error flag of this path.
     a.err = reinterpret_cast<int32_t *>(g_tensor_ws.ptr);
-    a.part_acc = g_tensor_ws.ptr + 64;
-    a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + 64 + ((acc_elems + 63) / 64) * 64);
+    a.part_acc = g_tensor_ws.ptr + kTensorWsHead;
+    a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + kTensorWsHead + ((acc_elems + 63) / 64) * 64);
     if (launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream)) != hipSuccess)
         return KVRT_EDEVICE;
     return KVRT_OK;

@@ -52,6 +52,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--streams", type=int, default=4)
     p.add_argument("--ctx", type=int, default=4096, help="context positions at the first timed step")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--one-stream", action="store_true",
+                   help="run thinker and talker on one stream (default: thinker on a second stream)")
     p.add_argument("--kernel-reps", type=int, default=50, help="event-timed launches of the dominant kernel")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
@@ -91,7 +93,7 @@ def prefill(rt, hkv: int, d: int, n_layers: int, streams: int, ctx: int, gen: to
 class Step:
     """Per-layer q/k/v/out buffers and the 58-launch decode step."""
 
-    def __init__(self, thinker, talker, streams: int, gen: torch.Generator) -> None:
+    def __init__(self, thinker, talker, streams: int, gen: torch.Generator, overlap: bool = True) -> None:
         self.thinker, self.talker = thinker, talker
         self.slots = list(range(streams))
 
@@ -110,11 +112,28 @@ class Step:
         self.th_scale = 1.0 / math.sqrt(THINKER["d"])
         self.tk_scale = 1.0 / math.sqrt(TALKER["d"])
 
+        # The thinker and talker are independent models: the thinker runs on
+        # a second stream (default priority) forked from and joined back to
+        # the caller's stream, so its latency-bound launches overlap the
+        # talker's bandwidth-bound ones (also inside the captured graph).
+        self.side = torch.cuda.Stream() if overlap else None
+
     def __call__(self) -> None:
-        for i, (q, k, v, o) in enumerate(self.th):
-            self.thinker.append_attend(i, q, k, v, self.slots, self.th_scale, out=o)
+        main = torch.cuda.current_stream()
+        if self.side is not None:
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                self._thinker()
+        else:
+            self._thinker()
         for i, (q, k, v, o) in enumerate(self.tk):
             self.talker.append_attend(i, q, k, v, self.slots, self.tk_scale, out=o)
+        if self.side is not None:
+            main.wait_stream(self.side)
+
+    def _thinker(self) -> None:
+        for i, (q, k, v, o) in enumerate(self.th):
+            self.thinker.append_attend(i, q, k, v, self.slots, self.th_scale, out=o)
 
 
 def step_bytes(streams: int, ctx_after: int) -> dict:
@@ -138,7 +157,8 @@ def step_bytes(streams: int, ctx_after: int) -> dict:
 
 
 def time_dominant_kernel(talker, step: Step, reps: int) -> tuple[float, int]:
-    """Average duration of one talker-layer decode launch (HIP events on its stream).
+    """Average duration of one talker-layer attention launch pair (decode +
+    merge kernels), HIP events on the stream they run on.
 
     A GPU sleep ahead of each (event, launch, event) triple lets the host
     enqueue all three before the GPU reaches them, so the events bracket the
@@ -164,6 +184,18 @@ def time_dominant_kernel(talker, step: Step, reps: int) -> tuple[float, int]:
     lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
     mean_t = sum(times[lo:hi]) / (hi - lo)
     return mean_t, bytes_total // reps
+
+
+def pmc_traffic() -> tuple[int | None, str | None]:
+    """HBM bytes per launch of the dominant launch pair, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a 256 MiB
+    copy); None when that summary is absent."""
+    path = ROOT / "profiles" / "pmc_traffic.json"
+    try:
+        data = json.loads(path.read_text())
+        return int(data["traffic_bytes_per_launch"]), str(data["source"])
+    except (OSError, KeyError, ValueError):
+        return None, None
 
 
 def cpu_baseline(args) -> dict | None:
@@ -244,7 +276,7 @@ def main() -> int:
     # Prefill to ctx - 1 so that the first timed append lands at position ctx - 1 + warm-up.
     prefill(thinker, THINKER["hkv"], THINKER["d"], THINKER["layers"], args.streams, args.ctx - 1, gen)
     prefill(talker, TALKER["hkv"], TALKER["d"], TALKER["layers"], args.streams, args.ctx - 1, gen)
-    step = Step(thinker, talker, args.streams, gen)
+    step = Step(thinker, talker, args.streams, gen, overlap=not args.one_stream)
 
     step()  # eager step: sizes the split-K workspaces before any capture
     torch.cuda.synchronize()
@@ -291,6 +323,7 @@ def main() -> int:
         b.copy_(a)
         torch.cuda.synchronize()
     cpu = cpu_baseline(args)
+    traffic, traffic_src = pmc_traffic()
     out = {
         "metric": "KV append+decode-attn tokens/s, HBM GB/s (% of peak), 1 MI355X",
         "value": round(tokens_per_step * args.steps / elapsed, 2),
@@ -312,6 +345,7 @@ def main() -> int:
             "context_last_step": len1,
             "launches_per_step": THINKER["layers"] + TALKER["layers"],
             "hip_graph": graph is not None,
+            "thinker_talker_streams": 1 if args.one_stream else 2,
             "tokens_per_step": tokens_per_step,
         },
         "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
@@ -319,12 +353,14 @@ def main() -> int:
         "step_algorithmic_bytes": total_bytes // args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": "kvrt::decode_kernel<128,2,bf16,contig> (talker layer, 4 streams, fused append)",
+            "kernel": "talker layer attention, 4 streams, fused append: kvrt::decode_kernel<128,2,bf16,contig> "
+                      "+ kvrt::merge_kernel<128,2> (one kvrt_append_attend_async launch pair)",
             "achieved": round(achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "avg_launch_us": round(k_time * 1e6, 3),
             "algorithmic_bytes_per_launch": k_bytes,
         },

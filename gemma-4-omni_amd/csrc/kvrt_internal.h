@@ -133,5 +133,7 @@ hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s);
 
 // Smallest instantiated row tile >= rows (1, 2, 4, 8, 16); 0 if too large.
 int rows_tile(int rows);
+// Keys one wave consumes per main-loop iteration of decode_kernel.
+int keys_per_iteration(int head_dim, int rows_tile, int dtype);
 
 }  // namespace kvrt

@@ -211,7 +211,7 @@ struct DecodeLds {
     static constexpr bool kWgMerge = R * D <= 4096;
     static constexpr int kMaxParts = 256;  // partials merged by the fix-up
     static constexpr int kMerge = kWgMerge ? (kWaves - 1) * R * D : 0;
-    static constexpr int kFixup = kMaxParts * R + 2 * R;
+    static constexpr int kFixup = 2 * kMaxParts * R + 2 * R;  // m, l per (part, row) + M, 1/L per row
     static constexpr int kFloats = kMerge > kFixup ? kMerge : kFixup;
 };
 
@@ -221,7 +221,8 @@ struct DecodeLds {
 // Parts are summed in index order, so the result does not depend on which
 // workgroup performs the merge.
 template <int D, int R>
-__device__ void merge_group(const DecodeArgs &a, int item, int kvh, int hkv, int n_parts, float *lds) {
+__device__ void merge_group(const DecodeArgs &a, int item, int kvh, int hkv, int n_parts, float *lds,
+                            int out_begin, int out_end) {
     const int Qn = a.qn;
     const int rows = a.group * Qn;
     const int hq = hkv * a.group;
@@ -256,19 +257,19 @@ __device__ void merge_group(const DecodeArgs &a, int item, int kvh, int hkv, int
         w[i] = r < rows ? __builtin_amdgcn_exp2f(w[i] - row_max[r]) * row_inv[r] : 0.f;
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
+    for (int idx = out_begin + threadIdx.x; idx < out_end; idx += blockDim.x) {
         const int r = idx / D, d = idx % D;
         const float *src = a.part_acc + (pbase + r) * D + d;
         float acc = 0.f;
-        int s = 0;
-        for (; s + 8 <= n_parts; s += 8) {
+        // Batches of 8 independent loads keep the part reads in flight together.
+        for (int s = 0; s < n_parts; s += 8) {
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(s + u) * R * D];
+            for (int u = 0; u < 8; ++u) v[u] = (s + u < n_parts) ? src[(int64_t)(s + u) * R * D] : 0.f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc = fmaf(w[(s + u) * R + r], v[u], acc);
+            for (int u = 0; u < 8; ++u)
+                if (s + u < n_parts) acc = fmaf(w[(s + u) * R + r], v[u], acc);
         }
-        for (; s < n_parts; ++s) acc = fmaf(w[s * R + r], src[(int64_t)s * R * D], acc);
         const int j = r / Qn, i = r % Qn;
         a.out[(((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(acc);
     }
@@ -555,20 +556,23 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
 
 }
 
-// grid (kv_heads, n_items), 256 threads: merges the parts of one (item, kv
-// head) written by decode_kernel. Runs after it in stream order, so every
+// grid (kv_heads, n_items, chunks), 256 threads: chunk c merges outputs
+// [256c, 256c + 256) of the R*D outputs of one (item, kv head), from the
+// parts written by decode_kernel. Runs after it in stream order, so every
 // part is visible without device-scope fences (which on gfx950 write back
-// and invalidate the whole L2 of an XCD). The merge of kv head 0 also
-// advances the item's length after a fused append: all decode workgroups
-// have read the lengths by then.
+// and invalidate the whole L2 of an XCD). Chunk 0 of kv head 0 also advances
+// the item's length after a fused append: all decode workgroups have read
+// the lengths by then.
 template <int D, int R>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     using Lds = DecodeLds<D, R>;
     __shared__ float lds[Lds::kFloats];
     const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
     const int n_parts = Lds::kWgMerge ? a.n_split / kWaves : a.n_split;
-    merge_group<D, R>(a, item, kvh, hkv, n_parts, lds);
-    if (a.advance && kvh == 0 && threadIdx.x == 0)
+    const int total = a.group * a.qn * D;
+    const int begin = blockIdx.z * 256;
+    merge_group<D, R>(a, item, kvh, hkv, n_parts, lds, begin, min(total, begin + 256));
+    if (a.advance && kvh == 0 && blockIdx.z == 0 && threadIdx.x == 0)
         a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += a.qn;
 }
 
@@ -605,6 +609,13 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
 // ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
+int keys_per_iteration(int head_dim, int rows_tile_, int dtype) {
+    const int vec = dtype == KVRT_INT8 ? 16 : 8;
+    const int kpw = 64 / (head_dim / vec);
+    const int u = rows_tile_ <= 4 ? 8 : (rows_tile_ == 8 ? 4 : 2);
+    return kpw * u;
+}
+
 int rows_tile(int rows) {
     if (rows <= 1) return 1;
     if (rows <= 2) return 2;
@@ -670,7 +681,8 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items), dim3(256), 0, s, a);
+    const int chunks = (a.group * a.qn * HD + 255) / 256;
+    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items, chunks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

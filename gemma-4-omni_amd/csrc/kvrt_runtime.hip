@@ -185,17 +185,19 @@ int target_wgs() {
     static const int v = env_int("KVRT_TARGET_WGS", 512);
     return v;
 }
-int min_keys_per_wave() {
-    static const int v = env_int("KVRT_MIN_KEYS_PER_WAVE", 32);
-    return v;
+// Keys a wave must own at least: one main-loop iteration of the kernel
+// variant (8..32 keys), unless KVRT_MIN_KEYS_PER_WAVE asks for more.
+int min_keys_per_wave(int keys_per_iter) {
+    static const int v = env_int("KVRT_MIN_KEYS_PER_WAVE", 1);
+    return std::max(v, keys_per_iter);
 }
 
 // Number of wave splits per (item, kv head): enough workgroups to fill the
 // chip, but at least min_keys keys per wave. n_items * kv_heads * (splits /
 // kWaves) <= target_wgs + n_items * kv_heads, which bounds the workspace.
-int choose_splits(int n_items, int kv_heads, int64_t max_keys) {
+int choose_splits(int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
     const int per_head = n_items * kv_heads;
-    const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave();
+    const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave(keys_per_iter);
     int wg = (target_wgs() + per_head - 1) / per_head;
     const int64_t cap = std::max<int64_t>(1, (max_keys + per_wg - 1) / per_wg);
     if (wg > cap) wg = (int)cap;
@@ -470,8 +472,8 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
             return KVRT_ESTATE;  // the window would read evicted pages
         max_keys = std::max<int64_t>(max_keys, visible_keys(s, Lnew, (int)qn));
     }
-    const int n_split = choose_splits(n, hkv, max_keys);
     const int R = rows_tile(rows);
+    const int n_split = choose_splits(n, hkv, max_keys, keys_per_iteration(D, R, s.dtype));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
     if (rc != KVRT_OK) return rc;
@@ -963,7 +965,8 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.group = group;
     a.qn = (int)qn;
     a.window = window;
-    a.n_split = choose_splits((int)n, (int)hkv, window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax);
+    a.n_split = choose_splits((int)n, (int)hkv, window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
+                              keys_per_iteration((int)D, rows_tile(rows), KVRT_BF16));
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = i;
     const int R = rows_tile(rows);

@@ -321,3 +321,27 @@ def test_error_paths_fail_closed_and_poison():
         rt.append(0, k[:1], k[:1], [1])
     assert e.value.code == -4
     assert rt.health() == -4
+
+
+@pytest.mark.parametrize("hq,hkv,d,length", [(16, 1, 512, 16000), (16, 8, 128, 16000), (8, 1, 256, 9000)])
+def test_many_splits_long_context(hq, hkv, d, length):
+    """One stream, long context: the split count hits its cap (64 workgroups
+    per kv head; 256 wave partials when the workgroup merge is off)."""
+    from kvrt import LayerSpec
+
+    gen = torch.Generator().manual_seed(length + d)
+    spec = LayerSpec(kv_heads=hkv, head_dim=d)
+    rt = _rt([spec], n_slots=1, capacity=length + 4, max_q=1)
+    orc = O.OracleCache(_oracle_layers([spec]), 1)
+    k = randn_bf16(gen, (1, hkv, length, d))
+    v = randn_bf16(gen, (1, hkv, length, d))
+    rt.import_(0, 0, k.cuda(), v.cuda())
+    orc.append(0, 0, to_np(k[0]), to_np(v[0]))
+    q = randn_bf16(gen, (1, hq, 1, d), 0.5)
+    kn = randn_bf16(gen, (1, hkv, 1, d), 0.5)
+    vn = randn_bf16(gen, (1, hkv, 1, d), 0.5)
+    out = rt.append_attend(0, q.cuda(), kn.cuda(), vn.cuda(), [0], 1 / math.sqrt(d))
+    orc.append(0, 0, to_np(kn[0]), to_np(vn[0]))
+    ref = orc.attend(0, 0, to_np(q[0]), 1 / math.sqrt(d))
+    assert np.abs(to_np(out[0]) - ref).max() <= ATOL
+    assert rt.health() == 0

@@ -16,6 +16,7 @@ namespace kvrt {
 constexpr int kMaxItems = KVRT_MAX_ITEMS;
 constexpr int kWaves = 4;            // waves per attention workgroup
 constexpr int kPtUpdates = 128;      // page-table edits carried by one launch
+constexpr int kMaxPositions = KVRT_MAX_POSITIONS;  // explicit positions carried by one write
 
 // Where the rows of one layer live. Row (slot, head, pos) starts at element
 //   CONTIG: slot*slot_stride + head*head_stride + pos*row_stride
@@ -56,12 +57,19 @@ struct AppendArgs {
     int32_t n_items;
     int32_t rows;           // Q (append) or S (import)
     int32_t import_mode;    // 0: pos0 = device length, length += rows
-                            // 1: pos0 = 0, length = rows
-    int32_t keep_from;      // import: rows below this position are not stored
+                            //    (one workgroup per item: graph-replay safe)
+                            // 1: pos0 = base_pos (host), length = base_pos + rows
+                            //    (any grid: nothing reads the length)
+                            // 2: row r of item i at pos[i*rows + r],
+                            //    length = max(length, pos_end[i])
+    int32_t base_pos;       // mode 1: position of row 0
+    int32_t keep_from;      // mode 1: rows below this position are not stored
     int32_t *err;           // device error flag
     int32_t n_upd;          // page-table edits applied before the writes
     int32_t upd_idx[kPtUpdates];
     int32_t upd_val[kPtUpdates];
+    int32_t pos[kMaxPositions];   // mode 2 only
+    int32_t pos_end[kMaxItems];   // mode 2 only: max position + 1 per item
     int32_t slots[kMaxItems];
 };
 

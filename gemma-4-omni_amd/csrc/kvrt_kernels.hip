@@ -41,8 +41,8 @@ __device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int hea
 // append / import
 // ---------------------------------------------------------------------------
 // grid (grid_x, n_items), 256 threads. Thread chunk = 8 elements of one row.
-// Append mode runs with grid_x == 1, so the workgroup that advances an item's
-// length is the only one that reads it.
+// Mode 0 (device cursor) runs with grid_x == 1, so the workgroup that
+// advances an item's length is the only one that reads it.
 template <int D, int KDT, int LAYOUT>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     constexpr int LPR = D / 8;
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         __syncthreads();
     }
     int32_t *lp = a.len.lens + (int64_t)slot * a.len.stride + a.len.offset;
-    const int pos0 = a.import_mode ? 0 : *lp;
+    const int pos0 = a.import_mode == 0 ? *lp : a.base_pos;
     const int64_t chunks = (int64_t)a.kv.kv_heads * a.rows * LPR;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += step) {
@@ -64,8 +64,8 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         const int64_t rowid = c / LPR;
         const int r = (int)(rowid % a.rows);
         const int h = (int)(rowid / a.rows);
-        const int pos = pos0 + r;
-        if (a.import_mode && pos < a.keep_from) continue;  // uniform over the row group
+        const int pos = a.import_mode == 2 ? a.pos[item * a.rows + r] : pos0 + r;
+        if (a.import_mode == 1 && pos < a.keep_from) continue;  // uniform over the row group
         const int64_t src = item * a.src_item_stride + h * a.src_head_stride + r * a.src_row_stride + seg * 8;
         const uint4 kx = *reinterpret_cast<const uint4 *>(a.k_src + src);
         const uint4 vx = *reinterpret_cast<const uint4 *>(a.v_src + src);
@@ -120,7 +120,10 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         }
     }
     __syncthreads();
-    if (blockIdx.x == 0 && threadIdx.x == 0) *lp = a.import_mode ? a.rows : pos0 + a.rows;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (a.import_mode == 2) *lp = max(*lp, a.pos_end[item]);
+        else *lp = pos0 + a.rows;
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -388,6 +388,9 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
         if (storage) {
             const kvrt_storage &st = storage[i];
             if (!st.k || !st.v || (L.scale_bytes && (!st.k_scale || !st.v_scale))) return fail(KVRT_EINVAL);
+            if (((reinterpret_cast<uintptr_t>(st.k) | reinterpret_cast<uintptr_t>(st.v) |
+                  reinterpret_cast<uintptr_t>(st.k_scale) | reinterpret_cast<uintptr_t>(st.v_scale)) & 15u) != 0)
+                return fail(KVRT_EINVAL);  // 16-byte rows and fills need aligned storage
             L.k = st.k;
             L.v = st.v;
             L.ks = static_cast<float *>(st.k_scale);
@@ -528,8 +531,22 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     for (int i = 0; i < 4; ++i)
         if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i]) return KVRT_EINVAL;
     const int64_t qn = k->dims[2];
-    if (k->dims[0] != n || k->dims[1] != hkv || k->dims[3] != D || qn <= 0 || qn > c->cfg.max_q)
+    if (k->dims[0] != n || k->dims[1] != hkv || k->dims[3] != D || qn <= 0 || qn > c->cfg.capacity)
         return KVRT_EINVAL;
+    // Up to max_q rows: the device cursor picks the position (graph-replay
+    // safe). Longer appends (prefill) take the host position, one item per
+    // launch, and spread over many workgroups.
+    if (qn > c->cfg.max_q && n > 1) {
+        for (int i = 0; i < n; ++i) {
+            kvrt_tensor ki = *k, vi = *v;
+            ki.dims[0] = vi.dims[0] = 1;
+            ki.data = static_cast<uint16_t *>(k->data) + i * k->strides[0];
+            vi.data = static_cast<uint16_t *>(v->data) + i * v->strides[0];
+            const int rc = append_impl(c, layer, 1, slots + i, &ki, &vi);
+            if (rc != KVRT_OK) return rc;
+        }
+        return KVRT_OK;
+    }
     std::vector<int> from(n);
     for (int i = 0; i < n; ++i) {
         from[i] = c->len_at(slots[i], layer);
@@ -564,8 +581,17 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         a.upd_val[i] = pval[i];
     }
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
+    int grid_x = 1;
+    if (qn > c->cfg.max_q) {  // n == 1 here
+        a.import_mode = 1;
+        a.base_pos = from[0];
+        // a ring keeps only its last ring_rows positions
+        a.keep_from = s.layout == KVRT_LAYOUT_RING ? from[0] + (int)qn - s.ring_rows : 0;
+        const int64_t chunks = (int64_t)hkv * qn * (D / 8);
+        grid_x = (int)std::max<int64_t>(1, std::min<int64_t>(4096, (chunks + 255) / 256));
+    }
     c->counters.launches++;
-    if (launch_append(a, D, s.dtype, 1, c->stream) != hipSuccess) return poison(c);
+    if (launch_append(a, D, s.dtype, grid_x, c->stream) != hipSuccess) return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
     for (int i = 0; i < n; ++i) {
         c->len_ref(slots[i], layer) += (int)qn;
@@ -709,6 +735,7 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
     a.n_items = 1;
     a.rows = (int)S;
     a.import_mode = 1;
+    a.base_pos = 0;
     a.keep_from = keep_from;
     a.err = c->d_err;
     a.slots[0] = slot;
@@ -735,6 +762,92 @@ int kvrt_append_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slot
     if (rc) return rc;
     if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
     return append_impl(c, layer, n, slots, k, v);
+}
+
+int kvrt_write_positions_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots,
+                               const int32_t *positions, const kvrt_tensor *k, const kvrt_tensor *v) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !positions) return KVRT_EINVAL;
+    if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // shared layers own no rows
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    if (s.layout != KVRT_LAYOUT_CONTIG || s.dtype != KVRT_BF16) return KVRT_EINVAL;
+    const int D = s.head_dim, hkv = s.kv_heads;
+    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i]) return KVRT_EINVAL;
+    const int64_t qn = k->dims[2];
+    if (k->dims[0] != n || k->dims[1] != hkv || k->dims[3] != D || (int64_t)n * qn > kMaxPositions)
+        return KVRT_EINVAL;
+    if (qn == 0) return KVRT_OK;  // an empty write leaves every length unchanged
+    AppendArgs a{};
+    for (int i = 0; i < n; ++i) {
+        int end = 0;
+        for (int r = 0; r < qn; ++r) {
+            const int p = positions[i * qn + r];
+            if (p < 0 || p >= c->cfg.capacity) return KVRT_ESTATE;
+            for (int r2 = 0; r2 < r; ++r2)
+                if (positions[i * qn + r2] == p) return KVRT_EINVAL;  // two rows, one position
+            end = std::max(end, p + 1);
+            a.pos[i * qn + r] = p;
+        }
+        a.pos_end[i] = end;
+        a.slots[i] = slots[i];
+    }
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.k_src = static_cast<const uint16_t *>(k->data);
+    a.v_src = static_cast<const uint16_t *>(v->data);
+    a.src_item_stride = k->strides[0];
+    a.src_head_stride = k->strides[1];
+    a.src_row_stride = k->strides[2];
+    a.n_items = n;
+    a.rows = (int)qn;
+    a.import_mode = 2;
+    a.err = c->d_err;
+    c->counters.launches++;
+    if (launch_append(a, D, s.dtype, 1, c->stream) != hipSuccess) return poison(c);
+    for (int i = 0; i < n; ++i) {
+        int &L = c->len_ref(slots[i], layer);
+        L = std::max(L, a.pos_end[i]);
+        c->counters.appended_rows += (uint64_t)qn * hkv;
+        c->counters.appended_bytes += (uint64_t)qn * hkv * D * 2 * 2;
+    }
+    return KVRT_OK;
+}
+
+int kvrt_reset_slot_async(kvrt_ctx *c, int32_t slot) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, slot)) return KVRT_EINVAL;
+    std::vector<int32_t> idx;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (c->layers[l].owner != l) continue;
+        const kvrt_layer_spec &s = c->layers[l].spec;
+        if (s.layout != KVRT_LAYOUT_PAGED) {
+            const KVView vw = make_view(c, l);
+            const uint64_t bytes = (uint64_t)vw.slot_stride * 2;
+            for (void *base : {vw.k, vw.v}) {
+                c->counters.launches++;
+                if (launch_zero(static_cast<uint8_t *>(base) + (uint64_t)slot * bytes, bytes, c->stream) != hipSuccess)
+                    return poison(c);
+            }
+        }
+        c->len_ref(slot, l) = 0;
+        idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
+    }
+    if (c->paged) {
+        for (int p = 0; p < c->pt_stride; ++p) {
+            int32_t &e = c->pt[(size_t)slot * c->pt_stride + p];
+            if (e >= 0) {
+                c->free_pages.push_back(e);
+                e = -1;
+                c->counters.pages_in_use--;
+            }
+        }
+        c->first_live[slot] = 0;
+    }
+    return set_device_lens(c, idx);
 }
 
 int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,

@@ -113,6 +113,8 @@ SIGNATURES = [
     ("kvrt_layer_storage", c_int32, [c_void_p, c_int32, POINTER(KvrtStorage)]),
     ("kvrt_import_async", c_int32, [c_void_p, c_int32, c_int32, _T, _T, c_int32]),
     ("kvrt_append_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T]),
+    ("kvrt_write_positions_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T]),
+    ("kvrt_reset_slot_async", c_int32, [c_void_p, c_int32]),
     ("kvrt_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T, _T]),
     ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),

@@ -173,6 +173,7 @@ class KVRuntime:
             torch.cuda.synchronize(self.device)
             _check(self.lib.kvrt_create_with_storage(ctypes.byref(cfg), specs, storage, ctypes.byref(self._ctx)),
                    "kvrt_create_with_storage")
+        self._free_slots = list(range(self.n_slots - 1, -1, -1))
 
     # ---- helpers -------------------------------------------------------------
     def _storage_shape(self, spec: LayerSpec) -> tuple[int, ...]:
@@ -201,6 +202,22 @@ class KVRuntime:
         assert st is not None
         return st
 
+    # ---- slots -----------------------------------------------------------------
+    def acquire_slot(self) -> int:
+        """Take the lowest free slot (session/stream id); raise when none is left."""
+        if not self._free_slots:
+            raise RuntimeError(f"kvrt: all {self.n_slots} slots are in use")
+        return self._free_slots.pop()
+
+    def release_slot(self, slot: int) -> None:
+        """Return a slot to the free list; its lengths drop to 0 (no bytes move)."""
+        slot = int(slot)
+        if not 0 <= slot < self.n_slots or slot in self._free_slots:
+            raise ValueError(f"kvrt: slot {slot} is not in use")
+        self.truncate(slot, 0)
+        self._free_slots.append(slot)
+        self._free_slots.sort(reverse=True)
+
     # ---- KV operations -----------------------------------------------------
     def import_(self, slot: int, layer: int, k: torch.Tensor, v: torch.Tensor, first_pos: int = 0) -> None:
         """Import an HF layer view [1, kv_heads, S, D] bf16 as positions 0..S-1."""
@@ -220,6 +237,33 @@ class KVRuntime:
         kd, vd = tensor_desc(k), tensor_desc(v)
         _check(self.lib.kvrt_append_async(self._ctx, layer, n, arr, ctypes.byref(kd), ctypes.byref(vd)),
                "kvrt_append_async")
+
+    def write_positions(self, layer: int, k: torch.Tensor, v: torch.Tensor, slots: Sequence[int],
+                        positions: Sequence[Sequence[int]]) -> None:
+        """Write k, v [n, kv_heads, Q, D] at explicit positions [n][Q] (CONTIG layers).
+
+        Each slot's length becomes max(length, max position + 1). A position
+        outside [0, capacity) raises ``KVRTError`` (code -2) and writes nothing.
+        """
+        require_cuda(k, "k")
+        require_cuda(v, "v")
+        flat = [int(p) for row in positions for p in row]
+        if len(flat) != k.shape[0] * k.shape[2]:
+            raise ValueError("positions must hold Q entries per slot")
+        if k.shape[2] == 0:
+            return  # an empty write changes nothing
+        self._bind()
+        arr, n = self._slots(slots)
+        pos = (ctypes.c_int32 * max(1, len(flat)))(*flat)
+        kd, vd = tensor_desc(k), tensor_desc(v)
+        _check(self.lib.kvrt_write_positions_async(self._ctx, layer, n, arr, pos, ctypes.byref(kd),
+                                                   ctypes.byref(vd)),
+               "kvrt_write_positions_async")
+
+    def reset_slot(self, slot: int) -> None:
+        """Zero every stored row of a slot and set its lengths to 0."""
+        self._bind()
+        _check(self.lib.kvrt_reset_slot_async(self._ctx, int(slot)), "kvrt_reset_slot_async")
 
     def attend(self, layer: int, q: torch.Tensor, slots: Sequence[int], scale: float,
                out: torch.Tensor | None = None) -> torch.Tensor:
@@ -251,10 +295,17 @@ class KVRuntime:
 
     def gather(self, layer: int, slots: Sequence[int], lmax: int | None = None,
                start_pos: Sequence[int] | None = None, mask_dtype: torch.dtype | None = torch.bool,
+               out: tuple[torch.Tensor, torch.Tensor] | None = None,
                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
-        """Zero-padded batch [n, kv_heads, Lmax, D] (+ mask [n, Lmax]) of n slots."""
+        """Zero-padded batch [n, kv_heads, Lmax, D] (+ mask [n, Lmax]) of n slots.
+
+        ``out`` may supply the K and V destinations (strided views with a
+        contiguous last dimension); Lmax is then their third dimension.
+        """
         spec = self.layers[self._owner(layer)]
         slots = [int(s) for s in slots]
+        if out is not None:
+            lmax = int(out[0].shape[2])
         if lmax is None:
             lens = [self.seq_length(s, layer) for s in slots]
             if start_pos is not None:
@@ -263,8 +314,13 @@ class KVRuntime:
                 lens = [min(x, spec.window - 1) for x in lens]
             lmax = max(1, max(lens))
         dt = torch.float32 if spec.dtype == "int8" else torch.bfloat16
-        out_k = torch.empty((len(slots), spec.kv_heads, lmax, spec.head_dim), dtype=dt, device=self.device)
-        out_v = torch.empty_like(out_k)
+        if out is not None:
+            out_k, out_v = out
+            require_cuda(out_k, "out_k")
+            require_cuda(out_v, "out_v")
+        else:
+            out_k = torch.empty((len(slots), spec.kv_heads, lmax, spec.head_dim), dtype=dt, device=self.device)
+            out_v = torch.empty_like(out_k)
         mask = None if mask_dtype is None else torch.empty((len(slots), lmax), dtype=mask_dtype, device=self.device)
         self._bind()
         arr, n = self._slots(slots)

@@ -44,7 +44,8 @@ extern "C" {
 
 #define KVRT_ABI_VERSION 1u
 #define KVRT_MAX_RANK 4
-#define KVRT_MAX_ITEMS 64 /* slots per batched call */
+#define KVRT_MAX_ITEMS 64      /* slots per batched call                 */
+#define KVRT_MAX_POSITIONS 128 /* rows per kvrt_write_positions_async call */
 
 /* ---- return codes ------------------------------------------------------ */
 #define KVRT_OK 0
@@ -190,6 +191,27 @@ int kvrt_import_async(kvrt_ctx *ctx, int32_t slot, int32_t layer, const kvrt_ten
  * (qwen_talker_kernels.cu:207-251). */
 int kvrt_append_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
                       const kvrt_tensor *k, const kvrt_tensor *v);
+
+/* Write Q rows to n slots of one CONTIG bf16 layer at explicit absolute
+ * positions: k, v are [n, kv_heads, Q, D]; positions is a HOST int32 array
+ * [n * Q] (row r of item i lands at positions[i * Q + r]; n * Q <= 128, no
+ * position twice within an item). Each (slot, layer) length becomes
+ * max(length, largest position + 1); positions never written read as the
+ * zeros of kvrt_create / kvrt_reset_slot_async. A position outside
+ * [0, capacity) fails with KVRT_ESTATE before anything is written; Q = 0
+ * changes nothing.
+ * Replaces _SlotKVCache.update (duplex_kernel/future_prefix.py:523-571:
+ * index_copy_ at cache_position, per-layer length = max position + 1) and
+ * write_joint_kv_kernel (native/qwen_talker/qwen_talker_kernels.cu:207-225:
+ * prefix row and audio row at two positions). */
+int kvrt_write_positions_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                               const int32_t *positions, const kvrt_tensor *k, const kvrt_tensor *v);
+
+/* Zero every stored row of a slot (all layers), set its lengths to 0 and
+ * release its pages (PAGED layers). Replaces _SlotKVCache.reset
+ * (duplex_kernel/future_prefix.py:582-586) and the arena memset before a
+ * talker prefix import (native/qwen_talker/qwen_talker.cu:1060-1110). */
+int kvrt_reset_slot_async(kvrt_ctx *ctx, int32_t slot);
 
 /* Gather n slots of one layer into a zero-padded batch:
  * out_k, out_v [n, kv_heads, Lmax, D] (bf16 for bf16 layers, fp32

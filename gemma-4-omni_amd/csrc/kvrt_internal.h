@@ -17,6 +17,7 @@ constexpr int kMaxItems = KVRT_MAX_ITEMS;
 constexpr int kWaves = 4;            // waves per attention workgroup
 constexpr int kPtUpdates = 128;      // page-table edits carried by one launch
 constexpr int kMaxPositions = KVRT_MAX_POSITIONS;  // explicit positions carried by one write
+constexpr int kMaxInt8Rows = 8;      // query rows per kv head of an INT8 decode (g * Q)
 
 // Where the rows of one layer live. Row (slot, head, pos) starts at element
 //   CONTIG: slot*slot_stride + head*head_stride + pos*row_stride

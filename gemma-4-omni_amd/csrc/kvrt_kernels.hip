@@ -56,7 +56,12 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         __syncthreads();
     }
     int32_t *lp = a.len.lens + (int64_t)slot * a.len.stride + a.len.offset;
-    const int pos0 = a.import_mode == 0 ? *lp : a.base_pos;
+    // Both values are loaded and then selected: a select between the two
+    // addresses would take the address of the kernel argument block and
+    // copy it to scratch memory.
+    const int dev_len = *lp;
+    const int host_pos = a.base_pos;
+    const int pos0 = a.import_mode == 0 ? dev_len : host_pos;
     const int64_t chunks = (int64_t)a.kv.kv_heads * a.rows * LPR;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += step) {
@@ -556,7 +561,6 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             }
         }
     }
-
 }
 
 // grid (kv_heads, n_items, chunks), 256 threads: chunk c merges outputs
@@ -676,8 +680,12 @@ template <int HD, int RT>
 static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s) {
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     if (dtype == KVRT_INT8) {
-        if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a);
+        // int8 rows carry 16 values per lane: 16 query rows would not fit in registers
+        if constexpr (RT > kMaxInt8Rows) return hipErrorInvalidValue;
+        else {
+            if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a);
+        }
     } else {
         KVRT_DISPATCH_LAYOUT(a.kv.layout,
             hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, LY>), grid, block, 0, s, a));

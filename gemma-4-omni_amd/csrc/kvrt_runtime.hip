@@ -452,6 +452,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int group = (int)(hq / hkv);
     const int rows = group * (int)qn;
     if (rows_tile(rows) == 0) return KVRT_EINVAL;
+    if (s.dtype == KVRT_INT8 && rows_tile(rows) > kMaxInt8Rows) return KVRT_EINVAL;
     if (!std::isfinite(scale)) return KVRT_EINVAL;
     if (fused) {
         if (s.dtype != KVRT_BF16) return KVRT_EINVAL;

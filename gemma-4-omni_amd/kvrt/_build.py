@@ -5,7 +5,9 @@ The library is compiled from ``csrc/kvrt_kernels.hip`` (kernels) and
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import shutil
 import subprocess
 import tempfile
@@ -38,13 +40,34 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the kvrt HIP library cannot be built")
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+RESOURCES_PATH = PKG_DIR / "kernel_resources.json"
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]"
+                     r"|LDS Size \[bytes/block\]):\s+(\S+)")
+
+
+def _resources(stderr: str) -> dict[str, dict[str, str]]:
+    """Per-kernel VGPR / scratch / LDS / occupancy from the compiler's resource remarks."""
+    out: dict[str, dict[str, str]] = {}
+    name = None
+    for m in _REMARK.finditer(stderr):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            name = val
+            out[name] = {}
+        elif name is not None:
+            out[name][key.split(" ")[0]] = val
+    return out
+
+
+def _compile(src: Path, obj: Path) -> dict[str, dict[str, str]]:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj),
+           "-Rpass-analysis=kernel-resource-usage"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         noise = "is not a recognized feature for this target"
-        err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+        err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "remark" not in l)
         raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+    return _resources(res.stderr)
 
 
 def build(verbose: bool = False) -> Path:
@@ -53,8 +76,16 @@ def build(verbose: bool = False) -> Path:
         objs = [Path(tmp) / (Path(s).stem + ".o") for s in SOURCES]
         with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
             futs = [pool.submit(_compile, CSRC / s, o) for s, o in zip(SOURCES, objs)]
+            resources: dict[str, dict[str, str]] = {}
             for f in futs:
-                f.result()
+                resources.update(f.result())
+        # Every kernel of the hot path must run from registers and LDS: scratch
+        # (private segment) use means spilled registers or a by-value kernel
+        # argument copied to memory, both of which cost a memory round trip per use.
+        spilled = {k: v["ScratchSize"] for k, v in resources.items() if v.get("ScratchSize", "0") != "0"}
+        if spilled:
+            raise RuntimeError(f"kernels using scratch memory: {spilled}")
+        RESOURCES_PATH.write_text(json.dumps(resources, indent=1, sort_keys=True) + "\n")
         tmp_lib = Path(tmp) / "libkvrt.so"
         cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp_lib)]
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -253,7 +253,8 @@ int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, in
  * q head h reads kv head h / (Hq / kv_heads) (HF repeat_kv order). Query row
  * i sits at position p = L - Q + i and sees keys k with k <= p and, for a
  * sliding layer, k >= p - W + 1. Scores s = (q.k) * scale, softmax and all
- * accumulation in fp32; out rounded to bf16 (RNE).
+ * accumulation in fp32; out rounded to bf16 (RNE). (Hq / kv_heads) * Q must
+ * be <= 16, and <= 8 for INT8 layers.
  * Replaces HF sdpa_attention_forward over repeat_kv'd K/V
  * (shape_stable_listener.py:241-251), gemma4_listener_debug_attention
  * (gemma4_listener_aten.cpp:100-286), kernel_stream_sdpa_q4_bf16

@@ -30,70 +30,73 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// ---- wave64 cross-lane exchange ------------------------------------------
-// DPP controls: quad_perm xor1 = [1,0,3,2] = 0xB1, xor2 = [2,3,0,1] = 0x4E,
-// row_half_mirror = 0x141 (lane i <- 7-i within 8), row_mirror = 0x140
-// (lane i <- 15-i within 16), row_ror:8 = 0x128 (lane i <- i^8 within 16).
+// ---- wave64 cross-lane reductions ------------------------------------------
+// pair<OP, M>(x) combines x with the value of lane (lane ^ M), for every lane:
+//   M = 1, 2: DPP quad_perm [1,0,3,2] (0xB1) / [2,3,0,1] (0x4E)
+//   M = 8:    DPP row_ror:8 (0x128): lane i <- lane i ^ 8 within a row of 16
+//   M = 16:   v_permlane16_swap: with both operands = x, the two results hold
+//             the even-row and odd-row copies, i.e. x and its lane ^ 16 partner
+//   M = 32:   v_permlane32_swap: the same for the two 32-lane halves
+//   M = 4:    ds_swizzle xor 4 (rarely used: only group reductions over 8+
+//             lanes pass through it, and those use the row mirrors instead)
+// All are VALU data-path operations except M = 4.
+struct OpSum {
+    static __device__ __forceinline__ float f(float a, float b) { return a + b; }
+};
+struct OpMax {
+    static __device__ __forceinline__ float f(float a, float b) { return fmaxf(a, b); }
+};
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// Exact lane exchange with lane ^ MASK (MASK a power of two < 64).
-template <int MASK>
-__device__ __forceinline__ float xor_lane(float x) {
-    if constexpr (MASK == 1) return dpp<0xB1>(x);
-    else if constexpr (MASK == 2) return dpp<0x4E>(x);
-    else if constexpr (MASK == 8) return dpp<0x128>(x);
-    else if constexpr (MASK == 16)
-        // ds_swizzle bit mode: and 0x1F, or 0, xor 0x10 (within 32 lanes).
-        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
-    else
-        return __shfl_xor(x, MASK, 64);
+template <class OP, int M>
+__device__ __forceinline__ float pair(float x) {
+    if constexpr (M == 1) return OP::f(x, dpp<0xB1>(x));
+    else if constexpr (M == 2) return OP::f(x, dpp<0x4E>(x));
+    else if constexpr (M == 8) return OP::f(x, dpp<0x128>(x));
+    else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return OP::f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return OP::f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else {
+        static_assert(M == 4, "pair: M must be a power of two below 64");
+        return OP::f(x, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x101F)));  // xor 4
+    }
 }
 
-// Sum over aligned groups of G lanes (G in 1..64, power of two). Every lane
-// of a group ends with the group total. Uses mirrors for 4 and 8/16, which
-// pair the two halves of the group just as xor does.
-template <int G>
-__device__ __forceinline__ float group_sum(float x) {
-    if constexpr (G >= 2) x += dpp<0xB1>(x);
-    if constexpr (G >= 4) x += dpp<0x4E>(x);
-    if constexpr (G >= 8) x += dpp<0x141>(x);
-    if constexpr (G >= 16) x += dpp<0x140>(x);
-    if constexpr (G >= 32) x += xor_lane<16>(x);
-    if constexpr (G >= 64) x += xor_lane<32>(x);
+// Reduction over aligned groups of G lanes (G a power of two, 1..64); every
+// lane of a group ends with the group result. Steps 4 and 8 use the row
+// mirrors (lane i <- 7 - i within 8, i <- 15 - i within 16): once the
+// smaller groups are uniform they pair the two halves exactly as xor does.
+template <class OP, int G>
+__device__ __forceinline__ float group_reduce(float x) {
+    if constexpr (G >= 2) x = pair<OP, 1>(x);
+    if constexpr (G >= 4) x = pair<OP, 2>(x);
+    if constexpr (G >= 8) x = OP::f(x, dpp<0x141>(x));
+    if constexpr (G >= 16) x = OP::f(x, dpp<0x140>(x));
+    if constexpr (G >= 32) x = pair<OP, 16>(x);
+    if constexpr (G >= 64) x = pair<OP, 32>(x);
     return x;
 }
+template <int G> __device__ __forceinline__ float group_sum(float x) { return group_reduce<OpSum, G>(x); }
+template <int G> __device__ __forceinline__ float group_max(float x) { return group_reduce<OpMax, G>(x); }
 
-template <int G>
-__device__ __forceinline__ float group_max(float x) {
-    if constexpr (G >= 2) x = fmaxf(x, dpp<0xB1>(x));
-    if constexpr (G >= 4) x = fmaxf(x, dpp<0x4E>(x));
-    if constexpr (G >= 8) x = fmaxf(x, dpp<0x141>(x));
-    if constexpr (G >= 16) x = fmaxf(x, dpp<0x140>(x));
-    if constexpr (G >= 32) x = fmaxf(x, xor_lane<16>(x));
-    if constexpr (G >= 64) x = fmaxf(x, xor_lane<32>(x));
-    return x;
-}
-
-// Combine lanes that are STRIDE apart, for strides STRIDE, 2*STRIDE, ... < 64
-// (the key sub-groups of one wave, which hold the same head dims).
-template <int STRIDE>
-__device__ __forceinline__ float strided_sum(float x) {
+// Reduction over the lanes STRIDE, 2*STRIDE, ... apart (the key sub-groups of
+// one wave, which hold the same head dims); STRIDE is a power of two.
+template <class OP, int STRIDE>
+__device__ __forceinline__ float strided_reduce(float x) {
     if constexpr (STRIDE < 64) {
-        x += xor_lane<STRIDE>(x);
-        if constexpr (STRIDE * 2 < 64) x = strided_sum<STRIDE * 2>(x);
+        x = pair<OP, STRIDE>(x);
+        if constexpr (STRIDE * 2 < 64) x = strided_reduce<OP, STRIDE * 2>(x);
     }
     return x;
 }
-template <int STRIDE>
-__device__ __forceinline__ float strided_max(float x) {
-    if constexpr (STRIDE < 64) {
-        x = fmaxf(x, xor_lane<STRIDE>(x));
-        if constexpr (STRIDE * 2 < 64) x = strided_max<STRIDE * 2>(x);
-    }
-    return x;
-}
+template <int S> __device__ __forceinline__ float strided_sum(float x) { return strided_reduce<OpSum, S>(x); }
+template <int S> __device__ __forceinline__ float strided_max(float x) { return strided_reduce<OpMax, S>(x); }
 
 }  // namespace kvrt

@@ -19,6 +19,12 @@ constexpr int kPtUpdates = 128;      // page-table edits carried by one launch
 constexpr int kMaxPositions = KVRT_MAX_POSITIONS;  // explicit positions carried by one write
 constexpr int kMaxInt8Rows = 8;      // query rows per kv head of an INT8 decode (g * Q)
 
+// Key-row groups a decode wave keeps in flight per main-loop pass, by row
+// tile R: all of them are loaded before the first is used, so a wave has
+// U * 2 KiB (bf16: K and V, 16 B per lane) outstanding; fewer for larger R,
+// whose query rows and accumulators take the registers.
+constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
+
 // Where the rows of one layer live. Row (slot, head, pos) starts at element
 //   CONTIG: slot*slot_stride + head*head_stride + pos*row_stride
 //   RING:   slot*slot_stride + head*head_stride + (pos % rows)*row_stride

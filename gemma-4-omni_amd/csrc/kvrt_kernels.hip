@@ -212,76 +212,13 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 // ---------------------------------------------------------------------------
 // decode attention (split-K)
 // ---------------------------------------------------------------------------
-// LDS floats a decode workgroup needs: the wave partials of waves 1..3
-// (workgroup merge, when R*D is small enough) or the fix-up weights.
+// LDS floats a decode workgroup needs for its cross-wave merge: the partials
+// of waves 1..3, when R * D is small enough to stage them.
 template <int D, int R>
 struct DecodeLds {
     static constexpr bool kWgMerge = R * D <= 4096;
-    static constexpr int kMaxParts = 256;  // partials merged by the fix-up
-    static constexpr int kMerge = kWgMerge ? (kWaves - 1) * R * D : 0;
-    static constexpr int kFixup = 2 * kMaxParts * R + 2 * R;  // m, l per (part, row) + M, 1/L per row
-    static constexpr int kFloats = kMerge > kFixup ? kMerge : kFixup;
+    static constexpr int kFloats = kWgMerge ? (kWaves - 1) * R * D : 1;
 };
-
-// Log-sum-exp merge of the n_parts partials of one (item, kv head) into bf16
-// outputs. Weights exp2(m_s - M) / L are computed once per (part, row) into
-// LDS; the output sums then stream the partials with independent loads.
-// Parts are summed in index order, so the result does not depend on which
-// workgroup performs the merge.
-template <int D, int R>
-__device__ void merge_group(const DecodeArgs &a, int item, int kvh, int hkv, int n_parts, float *lds,
-                            int out_begin, int out_end) {
-    const int Qn = a.qn;
-    const int rows = a.group * Qn;
-    const int hq = hkv * a.group;
-    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
-    float *w = lds;                      // [n_parts][R]: m, then the weight
-    float *lsum = lds + n_parts * R;     // [n_parts][R] partial l (reused below)
-    float *row_inv = lds + 2 * n_parts * R;  // [R]: 1 / L_r
-    float *row_max = row_inv + R;             // [R]: M_r
-    for (int i = threadIdx.x; i < n_parts * R; i += blockDim.x) {
-        const float2 ml = a.part_ml[pbase + i];
-        w[i] = ml.x;
-        lsum[i] = ml.y;
-    }
-    __syncthreads();
-    // one wave per row: max and sum over the parts
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int r = wave; r < rows; r += kWaves) {
-        float m = kNegBig;
-        for (int s = lane; s < n_parts; s += 64) m = fmaxf(m, w[s * R + r]);
-        m = group_max<64>(m);
-        float l = 0.f;
-        for (int s = lane; s < n_parts; s += 64) l += lsum[s * R + r] * __builtin_amdgcn_exp2f(w[s * R + r] - m);
-        l = group_sum<64>(l);
-        if (lane == 0) {
-            row_max[r] = m;
-            row_inv[r] = l > 0.f ? 1.0f / l : 0.f;
-        }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < n_parts * R; i += blockDim.x) {
-        const int r = i % R;
-        w[i] = r < rows ? __builtin_amdgcn_exp2f(w[i] - row_max[r]) * row_inv[r] : 0.f;
-    }
-    __syncthreads();
-    for (int idx = out_begin + threadIdx.x; idx < out_end; idx += blockDim.x) {
-        const int r = idx / D, d = idx % D;
-        const float *src = a.part_acc + (pbase + r) * D + d;
-        float acc = 0.f;
-        // Batches of 8 independent loads keep the part reads in flight together.
-        for (int s = 0; s < n_parts; s += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = (s + u < n_parts) ? src[(int64_t)(s + u) * R * D] : 0.f;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (s + u < n_parts) acc = fmaf(w[(s + u) * R + r], v[u], acc);
-        }
-        const int j = r / Qn, i = r % Qn;
-        a.out[(((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(acc);
-    }
-}
 
 // grid (n_split / kWaves, kv_heads, n_items), 256 threads = kWaves waves.
 // Wave w of workgroup x owns key split s = x*kWaves + w: a contiguous key
@@ -294,7 +231,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     constexpr int VEC = (KDT == KVRT_INT8) ? 16 : 8;
     constexpr int LPR = D / VEC;
     constexpr int KPW = 64 / LPR;
-    constexpr int U = (R <= 4) ? 8 : (R == 8 ? 4 : 2);
+    constexpr int U = keys_unroll(R);
     constexpr int QW = VEC / 2;  // packed bf16 pairs of q per lane and row
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad head_dim");
 
@@ -389,40 +326,45 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     }
 
     const int64_t new_base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * VEC;
+    bool bad = false;  // a visible key on an unmapped page (PAGED)
     for (int base = ws; base < we; base += KPW * U) {
+        // Load phase, branch-free so that all 2U loads issue back to back:
+        // a key past the wave's range (or on an unmapped page) reads a valid
+        // row instead (the wave's first key / pool page 0) and is masked out
+        // of the softmax; fused rows >= len come from the new K/V by an
+        // address select.
         uint4 kx[U], vx[U];
         float ksc[U], vsc[U];
         int key[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            key[u] = base + u * KPW + sub;
-            kx[u] = make_uint4(0, 0, 0, 0);
-            vx[u] = make_uint4(0, 0, 0, 0);
-            ksc[u] = vsc[u] = 0.f;
-            if (key[u] < we) {
-                if (fused && key[u] >= len) {
-                    const int64_t o = new_base + (int64_t)(key[u] - len) * D;
-                    kx[u] = *reinterpret_cast<const uint4 *>(a.k_new + o);
-                    vx[u] = *reinterpret_cast<const uint4 *>(a.v_new + o);
-                } else {
-                    const int64_t o = row_offset<LAYOUT>(a.kv, slot, kvh, key[u], D);
-                    if (o >= 0) {
-                        if constexpr (KDT == KVRT_BF16) {
-                            kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.k) + o + seg * VEC);
-                            vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.v) + o + seg * VEC);
-                        } else {
-                            kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.k) + o + seg * VEC);
-                            vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.v) + o + seg * VEC);
-                            ksc[u] = a.kv.ks[o / D];
-                            vsc[u] = a.kv.vs[o / D];
-                        }
-                    } else {
-                        key[u] = 0x7fffffff;  // unmapped page: masked out
-                        if (seg == 0) a.err[0] = 1;
-                    }
+            const int kk = base + u * KPW + sub;
+            const int kc = kk < we ? kk : ws;  // clamped: always a readable row
+            int64_t o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            bool ok = kk < we;
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+                bad |= ok && o < 0;
+                ok = ok && o >= 0;
+                o = o < 0 ? 0 : o;
+            }
+            key[u] = ok ? kk : 0x7fffffff;
+            if constexpr (KDT == KVRT_BF16) {
+                const uint16_t *kp = static_cast<const uint16_t *>(a.kv.k) + o + seg * VEC;
+                const uint16_t *vp = static_cast<const uint16_t *>(a.kv.v) + o + seg * VEC;
+                if (fused) {
+                    const bool nw = kc >= len;
+                    const int64_t on = new_base + (int64_t)(kc - len) * D;
+                    kp = nw ? a.k_new + on : kp;
+                    vp = nw ? a.v_new + on : vp;
                 }
+                kx[u] = *reinterpret_cast<const uint4 *>(kp);
+                vx[u] = *reinterpret_cast<const uint4 *>(vp);
+                ksc[u] = vsc[u] = 0.f;
             } else {
-                key[u] = 0x7fffffff;
+                kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.k) + o + seg * VEC);
+                vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.v) + o + seg * VEC);
+                ksc[u] = a.kv.ks[o / D];
+                vsc[u] = a.kv.vs[o / D];
             }
         }
         // scores (log2 domain)
@@ -491,6 +433,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             }
         }
     }
+
+    if (bad) a.err[0] = 1;
 
     // merge the KPW key sub-groups of the wave (lanes LPR apart)
 #pragma unroll
@@ -563,22 +507,56 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     }
 }
 
-// grid (kv_heads, n_items, chunks), 256 threads: chunk c merges outputs
-// [256c, 256c + 256) of the R*D outputs of one (item, kv head), from the
-// parts written by decode_kernel. Runs after it in stream order, so every
-// part is visible without device-scope fences (which on gfx950 write back
-// and invalidate the whole L2 of an XCD). Chunk 0 of kv head 0 also advances
-// the item's length after a fused append: all decode workgroups have read
-// the lengths by then.
+// grid (kv_heads, n_items, chunks), 256 threads: thread t of chunk c merges
+// output 256c + t of the R*D outputs of one (item, kv head) from the partials
+// decode_kernel wrote. Runs after it in stream order, so every partial is
+// visible without device-scope fences (which on gfx950 write back and
+// invalidate the whole L2 of an XCD). Each thread issues the (m, l) pair and
+// the accumulator of 16 partials at once — one dependent memory round trip
+// per 16 partials — and merges them in index order (deterministic):
+//   M = max m_s, L = sum l_s 2^(m_s - M), out = sum acc_s 2^(m_s - M) / L.
+// Chunk 0 of kv head 0 also advances the item's length after a fused append:
+// every decode workgroup has read the lengths by then.
 template <int D, int R>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-    using Lds = DecodeLds<D, R>;
-    __shared__ float lds[Lds::kFloats];
+    constexpr int B = 16;
     const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
-    const int n_parts = Lds::kWgMerge ? a.n_split / kWaves : a.n_split;
-    const int total = a.group * a.qn * D;
-    const int begin = blockIdx.z * 256;
-    merge_group<D, R>(a, item, kvh, hkv, n_parts, lds, begin, min(total, begin + 256));
+    const int n_parts = DecodeLds<D, R>::kWgMerge ? a.n_split / kWaves : a.n_split;
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const int idx = blockIdx.z * 256 + threadIdx.x;
+    if (idx < rows * D) {
+        const int r = idx / D, d = idx % D;
+        const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
+        const float2 *ml = a.part_ml + pbase + r;
+        const float *acc = a.part_acc + (pbase + r) * D + d;
+        float M = kNegBig, L = 0.f, O = 0.f;
+        for (int s0 = 0; s0 < n_parts; s0 += B) {
+            float2 m[B];
+            float v[B];
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+                const bool ok = s0 + u < n_parts;
+                m[u] = ok ? ml[(int64_t)(s0 + u) * R] : make_float2(kNegBig, 0.f);
+                v[u] = ok ? acc[(int64_t)(s0 + u) * R * D] : 0.f;
+            }
+            float bm = M;
+#pragma unroll
+            for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
+            const float c = __builtin_amdgcn_exp2f(M - bm);
+            L *= c;
+            O *= c;
+            M = bm;
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+                const float w = __builtin_amdgcn_exp2f(m[u].x - M);
+                L = fmaf(m[u].y, w, L);
+                O = fmaf(v[u], w, O);
+            }
+        }
+        const int j = r / Qn, i = r % Qn;
+        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(L > 0.f ? O / L : 0.f);
+    }
     if (a.advance && kvh == 0 && blockIdx.z == 0 && threadIdx.x == 0)
         a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += a.qn;
 }
@@ -619,8 +597,7 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
 int keys_per_iteration(int head_dim, int rows_tile_, int dtype) {
     const int vec = dtype == KVRT_INT8 ? 16 : 8;
     const int kpw = 64 / (head_dim / vec);
-    const int u = rows_tile_ <= 4 ? 8 : (rows_tile_ == 8 ? 4 : 2);
-    return kpw * u;
+    return kpw * keys_unroll(rows_tile_);
 }
 
 int rows_tile(int rows) {

@@ -52,8 +52,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--streams", type=int, default=4)
     p.add_argument("--ctx", type=int, default=4096, help="context positions at the first timed step")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--groups", type=int, default=1,
+                   help="session groups per model: each (model, group) gets its own kvrt context and HIP stream")
     p.add_argument("--one-stream", action="store_true",
-                   help="run thinker and talker on one stream (default: thinker on a second stream)")
+                   help="run every launch on the caller's stream (default: one stream per model and group)")
     p.add_argument("--kernel-reps", type=int, default=50, help="event-timed launches of the dominant kernel")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
@@ -65,7 +67,7 @@ def thinker_is_global(i: int) -> bool:
     return (i + 1) % THINKER["pattern"] == 0
 
 
-def build_runtimes(args, capacity: int):
+def build_runtimes(args, capacity: int, n_slots: int):
     from kvrt import KVRuntime, LayerSpec
 
     th_specs = []
@@ -76,8 +78,8 @@ def build_runtimes(args, capacity: int):
             th_specs.append(LayerSpec(kv_heads=THINKER["hkv"], head_dim=THINKER["d"], layout="ring",
                                       window=THINKER["window"], ring_rows=THINKER["window"]))
     tk_specs = [LayerSpec(kv_heads=TALKER["hkv"], head_dim=TALKER["d"]) for _ in range(TALKER["layers"])]
-    thinker = KVRuntime(th_specs, args.streams, capacity, max_q=1, device="cuda")
-    talker = KVRuntime(tk_specs, args.streams, capacity, max_q=1, device="cuda")
+    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, device="cuda")
+    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, device="cuda")
     return thinker, talker
 
 
@@ -90,50 +92,58 @@ def prefill(rt, hkv: int, d: int, n_layers: int, streams: int, ctx: int, gen: to
     torch.cuda.synchronize()
 
 
-class Step:
-    """Per-layer q/k/v/out buffers and the 58-launch decode step."""
+class Model:
+    """One model (thinker or talker) over one group of sessions: a kvrt
+    context of its own, per-layer q/k/v/out buffers, and the HIP stream its
+    launches go to."""
 
-    def __init__(self, thinker, talker, streams: int, gen: torch.Generator, overlap: bool = True) -> None:
-        self.thinker, self.talker = thinker, talker
-        self.slots = list(range(streams))
+    def __init__(self, rt, cfg: dict, n: int, gen: torch.Generator, stream) -> None:
+        self.rt, self.stream = rt, stream
+        self.slots = list(range(n))
+        self.scale = 1.0 / math.sqrt(cfg["d"])
 
         def mk(shape, scale):
             return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16)
 
-        n = streams
-        self.th = [(mk((n, THINKER["hq"], 1, THINKER["d"]), 0.5), mk((n, THINKER["hkv"], 1, THINKER["d"]), 0.5),
-                    mk((n, THINKER["hkv"], 1, THINKER["d"]), 0.5),
-                    torch.empty((n, THINKER["hq"], 1, THINKER["d"]), dtype=torch.bfloat16, device="cuda"))
-                   for _ in range(THINKER["layers"])]
-        self.tk = [(mk((n, TALKER["hq"], 1, TALKER["d"]), 0.5), mk((n, TALKER["hkv"], 1, TALKER["d"]), 0.5),
-                    mk((n, TALKER["hkv"], 1, TALKER["d"]), 0.5),
-                    torch.empty((n, TALKER["hq"], 1, TALKER["d"]), dtype=torch.bfloat16, device="cuda"))
-                   for _ in range(TALKER["layers"])]
-        self.th_scale = 1.0 / math.sqrt(THINKER["d"])
-        self.tk_scale = 1.0 / math.sqrt(TALKER["d"])
+        self.bufs = [(mk((n, cfg["hq"], 1, cfg["d"]), 0.5), mk((n, cfg["hkv"], 1, cfg["d"]), 0.5),
+                      mk((n, cfg["hkv"], 1, cfg["d"]), 0.5),
+                      torch.empty((n, cfg["hq"], 1, cfg["d"]), dtype=torch.bfloat16, device="cuda"))
+                     for _ in range(cfg["layers"])]
 
-        # The thinker and talker are independent models: the thinker runs on
-        # a second stream (default priority) forked from and joined back to
-        # the caller's stream, so its latency-bound launches overlap the
-        # talker's bandwidth-bound ones (also inside the captured graph).
-        self.side = torch.cuda.Stream() if overlap else None
+    def run(self) -> None:
+        for i, (q, k, v, o) in enumerate(self.bufs):
+            self.rt.append_attend(i, q, k, v, self.slots, self.scale, out=o)
+
+
+class Step:
+    """The decode step: for every model and session group, one fused append +
+    attention launch per layer.
+
+    Each (model, group) has its own kvrt context and its own HIP stream
+    (default priority), forked from and joined back to the caller's stream,
+    so independent launches overlap — also inside the captured graph. With
+    one group per model, the thinker's latency-bound launches overlap the
+    talker's bandwidth-bound ones; more groups also overlap the per-launch
+    fixed costs of one model's session groups.
+    """
+
+    def __init__(self, models: list[Model]) -> None:
+        self.models = models
 
     def __call__(self) -> None:
         main = torch.cuda.current_stream()
-        if self.side is not None:
-            self.side.wait_stream(main)
-            with torch.cuda.stream(self.side):
-                self._thinker()
-        else:
-            self._thinker()
-        for i, (q, k, v, o) in enumerate(self.tk):
-            self.talker.append_attend(i, q, k, v, self.slots, self.tk_scale, out=o)
-        if self.side is not None:
-            main.wait_stream(self.side)
-
-    def _thinker(self) -> None:
-        for i, (q, k, v, o) in enumerate(self.th):
-            self.thinker.append_attend(i, q, k, v, self.slots, self.th_scale, out=o)
+        for m in self.models:
+            if m.stream is None:
+                continue
+            m.stream.wait_stream(main)
+            with torch.cuda.stream(m.stream):
+                m.run()
+        for m in self.models:
+            if m.stream is None:
+                m.run()
+        for m in self.models:
+            if m.stream is not None:
+                main.wait_stream(m.stream)
 
 
 def step_bytes(streams: int, ctx_after: int) -> dict:
@@ -156,29 +166,29 @@ def step_bytes(streams: int, ctx_after: int) -> dict:
             "total": streams * (th + tk)}
 
 
-def time_dominant_kernel(talker, step: Step, reps: int) -> tuple[float, int]:
+def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int]:
     """Average duration of one talker-layer attention launch pair (decode +
-    merge kernels), HIP events on the stream they run on.
+    merge kernels) over one session group, HIP events on the stream they run on.
 
     A GPU sleep ahead of each (event, launch, event) triple lets the host
     enqueue all three before the GPU reaches them, so the events bracket the
-    kernel and not the host launch latency.
+    kernels and not the host launch latency.
     """
-    q, k, v, o = step.tk[0]
+    q, k, v, o = model.bufs[0]
     stream = torch.cuda.current_stream()
     times = []
     bytes_total = 0
     for _ in range(reps):
-        L_before = talker.seq_length(0, 0)
+        L_before = model.rt.seq_length(0, 0)
         torch.cuda._sleep(2_000_000)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        talker.append_attend(0, q, k, v, step.slots, step.tk_scale, out=o)
+        model.rt.append_attend(0, q, k, v, model.slots, model.scale, out=o)
         e1.record(stream)
         e1.synchronize()
         times.append(e0.elapsed_time(e1) * 1e-3)
-        bytes_total += step_bytes(len(step.slots), L_before + 1)["talker_layer"]
+        bytes_total += step_bytes(len(model.slots), L_before + 1)["talker_layer"]
     times.sort()
     # mean of the central 80 % (drop warm-up and preemption outliers)
     lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
@@ -272,11 +282,22 @@ def main() -> int:
     gen = torch.Generator(device="cuda").manual_seed(1)
     margin = args.warmup + args.steps + args.kernel_reps + 8
     capacity = args.ctx + margin
-    thinker, talker = build_runtimes(args, capacity)
-    # Prefill to ctx - 1 so that the first timed append lands at position ctx - 1 + warm-up.
-    prefill(thinker, THINKER["hkv"], THINKER["d"], THINKER["layers"], args.streams, args.ctx - 1, gen)
-    prefill(talker, TALKER["hkv"], TALKER["d"], TALKER["layers"], args.streams, args.ctx - 1, gen)
-    step = Step(thinker, talker, args.streams, gen, overlap=not args.one_stream)
+    if args.streams % args.groups:
+        raise SystemExit("--streams must be a multiple of --groups")
+    n = args.streams // args.groups
+    models: list[Model] = []
+    runtimes = []
+    for g in range(args.groups):
+        thinker, talker = build_runtimes(args, capacity, n)
+        # Prefill to ctx - 1 so that the first timed append lands at position ctx - 1 + warm-up.
+        prefill(thinker, THINKER["hkv"], THINKER["d"], THINKER["layers"], n, args.ctx - 1, gen)
+        prefill(talker, TALKER["hkv"], TALKER["d"], TALKER["layers"], n, args.ctx - 1, gen)
+        side = None if args.one_stream else torch.cuda.Stream
+        models.append(Model(talker, TALKER, n, gen, side() if side else None))
+        models.append(Model(thinker, THINKER, n, gen, side() if side else None))
+        runtimes += [talker, thinker]
+    talker0 = models[0]
+    step = Step(models)
 
     step()  # eager step: sizes the split-K workspaces before any capture
     torch.cuda.synchronize()
@@ -286,35 +307,35 @@ def main() -> int:
         with torch.cuda.graph(graph):
             step()
         # capture recorded the launches without running them
-        thinker.sync_lengths()
-        talker.sync_lengths()
+        for rt in runtimes:
+            rt.sync_lengths()
     run = graph.replay if graph is not None else step
     for _ in range(args.warmup):
         run()
     torch.cuda.synchronize()
     if graph is not None:  # replays advance the device lengths only
-        thinker.sync_lengths()
-        talker.sync_lengths()
-    len0 = talker.seq_length(0, 0)
+        for rt in runtimes:
+            rt.sync_lengths()
+    len0 = talker0.rt.seq_length(0, 0)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         run()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    thinker.sync_lengths()
-    talker.sync_lengths()
-    len1 = talker.seq_length(0, 0)
+    for rt in runtimes:
+        rt.sync_lengths()
+    len1 = talker0.rt.seq_length(0, 0)
     if len1 - len0 != args.steps:
         raise RuntimeError(f"device lengths advanced by {len1 - len0}, expected {args.steps}")
-    for rt in (thinker, talker):
+    for rt in runtimes:
         if rt.health() != 0:
             raise RuntimeError("kvrt health check failed after the timed region")
 
     total_bytes = sum(step_bytes(args.streams, L)["total"] for L in range(len0 + 1, len1 + 1))
     ms = 1e3 * elapsed / args.steps
     tokens_per_step = 2 * args.streams
-    k_time, k_bytes = time_dominant_kernel(talker, step, args.kernel_reps)
-    if talker.health() != 0:
+    k_time, k_bytes = time_dominant_kernel(talker0, args.kernel_reps)
+    if talker0.rt.health() != 0:
         raise RuntimeError("kvrt health check failed after the kernel timing")
     achieved = k_bytes / k_time
     if args.calib_copy:
@@ -343,9 +364,10 @@ def main() -> int:
             "streams": args.streams,
             "context_first_step": len0 + 1,
             "context_last_step": len1,
-            "launches_per_step": THINKER["layers"] + TALKER["layers"],
+            "launches_per_step": args.groups * (THINKER["layers"] + TALKER["layers"]),
+            "session_groups": args.groups,
             "hip_graph": graph is not None,
-            "thinker_talker_streams": 1 if args.one_stream else 2,
+            "hip_streams": 1 if args.one_stream else 2 * args.groups,
             "tokens_per_step": tokens_per_step,
         },
         "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
@@ -353,7 +375,7 @@ def main() -> int:
         "step_algorithmic_bytes": total_bytes // args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": "talker layer attention, 4 streams, fused append: kvrt::decode_kernel<128,2,bf16,contig> "
+            "kernel": f"talker layer attention, {n} streams, fused append: kvrt::decode_kernel<128,2,bf16,contig> "
                       "+ kvrt::merge_kernel<128,2> (one kvrt_append_attend_async launch pair)",
             "achieved": round(achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9,

@@ -119,6 +119,20 @@ struct DecodeArgs {
     int32_t slots[kMaxItems];
 };
 
+struct PrefillArgs {
+    KVView kv;
+    Lengths len;
+    const uint16_t *q;      // [n, Hq, Q, D] contiguous
+    uint16_t *out;          // [n, Hq, Q, D] contiguous
+    int32_t *err;
+    int32_t n_items;
+    int32_t group;          // Hq / kv_heads (waves per workgroup)
+    int32_t qn;             // Q (query rows per item)
+    int32_t window;
+    float scale_log2;
+    int32_t slots[kMaxItems];
+};
+
 struct SetLenArgs {
     int32_t *lens;
     int32_t n;
@@ -140,6 +154,10 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
 // Split-K attention over the view, then the merge kernel.
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head,
                          hipStream_t s);
+// Chunked-prefill attention on MFMA (bf16 CONTIG / RING / PAGED layers).
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
+// Largest GQA group (waves per workgroup) of the prefill kernel for a head dim.
+constexpr int prefill_max_group(int head_dim) { return head_dim >= 256 ? 8 : 16; }
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
 hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,
                             hipStream_t s);

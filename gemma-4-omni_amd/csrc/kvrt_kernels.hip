@@ -562,6 +562,156 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// chunked-prefill attention (MFMA)
+// ---------------------------------------------------------------------------
+// grid (ceil(Q / 16), kv_heads, n_items), 64 * g threads: wave j is q head
+// kvh * g + j over the 16 query rows of block x; the g waves share each
+// 32-key K/V tile staged in LDS (K row-major, V transposed). Per tile and
+// wave:
+//   S^T (32 keys x 16 queries) = K Q^T      2 * D/32  v_mfma_f32_16x16x32_bf16
+//   online softmax per query column (fp32, exp2 domain)
+//   O^T (D x 16) += V^T P^T                 D/16      v_mfma_f32_16x16x32_bf16
+// with P split into two bf16 terms for the second product and everything
+// accumulated in fp32. MFMA lane layouts (16x16x32): A[row l%16][k 8(l/16)+j],
+// B[k 8(l/16)+j][col l%16], D[row 4(l/16)+v][col l%16].
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPfKeys = 32;  // keys per LDS tile
+
+// Key (within a tile) of row i of S^T block b. Chosen so that lane group G
+// (lanes 16G..16G+15) ends up with the scores of keys 8G..8G+7 across the two
+// blocks, which are exactly the keys of its B operand in V^T P^T.
+__device__ __forceinline__ int pf_key(int b, int i) { return 8 * (i >> 2) + 4 * b + (i & 3); }
+
+__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+template <int D, int LAYOUT>
+__global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillArgs a) {
+    constexpr int KP = D + 8;        // K tile row pitch (bf16): 16 B of padding per row
+    constexpr int VP = kPfKeys + 8;  // V^T tile row pitch (bf16)
+    __shared__ __align__(16) uint16_t sk[kPfKeys * KP];
+    __shared__ __align__(16) uint16_t sv[D * VP];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int item = blockIdx.z, kvh = blockIdx.y, hkv = gridDim.y;
+    const int g = a.group, hq = hkv * g, head = kvh * g + wave;
+    const int slot = a.slots[item];
+    const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    const int Qn = a.qn;
+    const int qrow0 = blockIdx.x * 16;
+    const int base_pos = L - Qn;               // position of query row 0
+    const int qr = qrow0 + col;                // this lane's query row (S^T / O^T column)
+    const bool qvalid = qr < Qn;
+    const int pq = base_pos + qr;
+    const int lo_q = a.window > 0 ? pq - a.window + 1 : 0;
+    const int kend = base_pos + min(Qn, qrow0 + 16);  // keys < kend: up to the block's last query
+    const int kstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
+
+    // Q^T as the B operand: lane (col, grp) holds d = 32c + 8grp .. +7 of query qr.
+    uint4 qop[D / 32];
+    {
+        const uint16_t *qp = a.q + (((int64_t)item * hq + head) * Qn + (qvalid ? qr : 0)) * D + 8 * grp;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c)
+            qop[c] = qvalid ? *reinterpret_cast<const uint4 *>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
+    }
+    float m = kNegBig, l = 0.f;  // running max (uniform per query) and this lane's partial sum
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bool bad = false;
+    const uint16_t *kg = static_cast<const uint16_t *>(a.kv.k);
+    const uint16_t *vg = static_cast<const uint16_t *>(a.kv.v);
+
+    for (int t0 = kstart; t0 < kend; t0 += kPfKeys) {
+        __syncthreads();  // the previous tile has been consumed
+        for (int c = threadIdx.x; c < kPfKeys * (D / 8); c += blockDim.x) {
+            const int kr = c / (D / 8), seg = c % (D / 8);
+            const int key = t0 + kr;
+            const int kc = key < kend ? key : kstart;  // readable row; masked below
+            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+                bad |= off < 0;
+                off = off < 0 ? 0 : off;
+            }
+            const uint4 kx = *reinterpret_cast<const uint4 *>(kg + off + 8 * seg);
+            const uint4 vx = *reinterpret_cast<const uint4 *>(vg + off + 8 * seg);
+            *reinterpret_cast<uint4 *>(&sk[kr * KP + 8 * seg]) = kx;
+            const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sv[(8 * seg + 2 * e) * VP + kr] = (uint16_t)(vw[e] & 0xffffu);
+                sv[(8 * seg + 2 * e + 1) * VP + kr] = (uint16_t)(vw[e] >> 16);
+            }
+        }
+        __syncthreads();
+        // S^T blocks: rows = keys pf_key(b, i), cols = queries
+        f32x4_t s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            s[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            const uint16_t *kp = &sk[pf_key(b, col) * KP + 8 * grp];
+#pragma unroll
+            for (int c = 0; c < D / 32; ++c) s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c), qop[c], s[b]);
+        }
+        // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile
+        float sc[8];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = t0 + 8 * grp + j;
+            const float raw = j < 4 ? s[0][j] : s[1][j - 4];
+            const bool vis = qvalid && key < kend && key <= pq && key >= lo_q;
+            sc[j] = vis ? raw * a.scale_log2 : -INFINITY;
+            tmax = fmaxf(tmax, sc[j]);
+        }
+        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+        const float mn = fmaxf(m, tmax);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        l *= corr;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) o[b] *= corr;
+        // P = P_hi + P_lo, both bf16 (P_lo = the rounding error of P_hi): the
+        // two products keep P to ~2^-17 relative, where one bf16 P (2^-9)
+        // would be visible in bf16 outputs of few-key rows.
+        uint32_t ph[4], pl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float p0 = __builtin_amdgcn_exp2f(sc[2 * j] - m);
+            const float p1 = __builtin_amdgcn_exp2f(sc[2 * j + 1] - m);
+            l += p0 + p1;
+            const uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
+            ph[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            pl[j] = (uint32_t)f32_to_bf16(p0 - bf16_to_f32(h0)) | ((uint32_t)f32_to_bf16(p1 - bf16_to_f32(h1)) << 16);
+        }
+        const uint4 pop_hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+        const uint4 pop_lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        // O^T += V^T P^T: A row i = d (16b + col), k = keys 8grp .. +7
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) {
+            const uint4 va = *reinterpret_cast<const uint4 *>(&sv[(16 * b + col) * VP + 8 * grp]);
+            o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
+        }
+    }
+    if (bad) a.err[0] = 1;
+    l = pair<OpSum, 32>(pair<OpSum, 16>(l));
+    if (!qvalid) return;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    uint16_t *op = a.out + (((int64_t)item * hq + head) * Qn + qr) * D + 4 * grp;
+#pragma unroll
+    for (int b = 0; b < D / 16; ++b) {
+        const uint32_t w0 = (uint32_t)f32_to_bf16(o[b][0] * inv) | ((uint32_t)f32_to_bf16(o[b][1] * inv) << 16);
+        const uint32_t w1 = (uint32_t)f32_to_bf16(o[b][2] * inv) | ((uint32_t)f32_to_bf16(o[b][3] * inv) << 16);
+        *reinterpret_cast<uint2 *>(op + 16 * b) = make_uint2(w0, w1);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // small control kernels
 // ---------------------------------------------------------------------------
 __global__ void set_i32_kernel(SetLenArgs a) {
@@ -686,6 +836,13 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_
         default: return hipErrorInvalidValue;
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
+    dim3 grid((a.qn + 15) / 16, a.kv.kv_heads, a.n_items), block(64 * a.group);
+    KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
+        hipLaunchKernelGGL((prefill_kernel<HD, LY>), grid, block, 0, s, a)));
+    return hipGetLastError();
 }
 
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s) {

@@ -339,7 +339,7 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     *out = nullptr;
     if (cfg->struct_size != sizeof(kvrt_config)) return KVRT_EINVAL;
     if (cfg->n_layers <= 0 || cfg->n_layers > 4096 || cfg->n_slots <= 0 || cfg->n_slots > (1 << 20) ||
-        cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 64)
+        cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 65536)
         return KVRT_EINVAL;
     bool any_paged = false;
     for (int i = 0; i < cfg->n_layers; ++i) {
@@ -622,7 +622,7 @@ uint32_t kvrt_abi_version(void) { return KVRT_ABI_VERSION; }
 
 uint64_t kvrt_capabilities(void) {
     return KVRT_CAP_CONTIG | KVRT_CAP_RING | KVRT_CAP_PAGED | KVRT_CAP_INT8 | KVRT_CAP_FUSED_APPEND_ATTEND |
-           KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND;
+           KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND | KVRT_CAP_PREFILL_MFMA;
 }
 
 const char *kvrt_strerror(int code) {
@@ -1039,6 +1039,56 @@ int kvrt_append_attend_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_
         return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
     }
     return decode_impl(c, layer, n, slots, q, k, v, out, scale);
+}
+
+int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *q,
+                              const kvrt_tensor *out, float scale) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    if (s.dtype != KVRT_BF16) return KVRT_EINVAL;
+    const int D = s.head_dim, hkv = s.kv_heads;
+    if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
+        return KVRT_EINVAL;
+    const int64_t hq = q->dims[1], qn = q->dims[2];
+    if (q->dims[0] != n || q->dims[3] != D || hq <= 0 || hq % hkv != 0 || qn <= 0 || qn > c->cfg.capacity)
+        return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (out->dims[i] != q->dims[i]) return KVRT_EINVAL;
+    const int group = (int)(hq / hkv);
+    if (group > prefill_max_group(D) || !std::isfinite(scale)) return KVRT_EINVAL;
+    uint64_t tile_keys = 0;
+    for (int i = 0; i < n; ++i) {
+        const int L = c->len_at(slots[i], layer);
+        if (L < qn) return KVRT_ESTATE;
+        // the oldest key any query of the chunk can see
+        const int oldest = s.window > 0 ? std::max<int64_t>(0, L - qn - s.window + 1) : 0;
+        if (s.layout == KVRT_LAYOUT_RING && L - oldest > s.ring_rows) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_PAGED && oldest < c->first_live[slots[i]] * c->cfg.block_size) return KVRT_ESTATE;
+        for (int64_t q0 = 0; q0 < qn; q0 += 16) {
+            const int64_t kend = L - qn + std::min<int64_t>(qn, q0 + 16);
+            const int64_t kstart = s.window > 0 ? std::max<int64_t>(0, L - qn + q0 - s.window + 1) : 0;
+            tile_keys += (uint64_t)(kend - kstart);
+        }
+    }
+    PrefillArgs a{};
+    a.kv = make_view(c, layer);
+    a.len = make_len(c, layer);
+    a.q = static_cast<const uint16_t *>(q->data);
+    a.out = static_cast<uint16_t *>(out->data);
+    a.err = c->d_err;
+    a.n_items = n;
+    a.group = group;
+    a.qn = (int)qn;
+    a.window = s.window;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
+    c->counters.launches++;
+    if (launch_prefill(a, D, c->stream) != hipSuccess) return poison(c);
+    c->counters.attended_keys += tile_keys * hkv;
+    c->counters.attended_bytes += tile_keys * hkv * (uint64_t)D * 2 * 2;
+    return KVRT_OK;
 }
 
 int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,

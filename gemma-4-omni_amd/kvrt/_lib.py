@@ -39,6 +39,7 @@ CAP_FUSED_APPEND_ATTEND = 1 << 4
 CAP_GATHER = 1 << 5
 CAP_DEVICE_LENGTHS = 1 << 6
 CAP_TENSOR_ATTEND = 1 << 7
+CAP_PREFILL_MFMA = 1 << 8
 
 
 class KvrtTensor(ctypes.Structure):
@@ -121,6 +122,7 @@ SIGNATURES = [
     ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     ("kvrt_attend_decode_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_append_attend_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _T, _T, c_float]),
+    ("kvrt_attend_prefill_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_attend_tensors_async", c_int32, [_T, _T, _T, c_void_p, _T, c_float, c_int32, c_void_p]),
     ("kvrt_copy_rows_async", c_int32, [_T, _T, c_int64, c_void_p]),
     ("kvrt_session_state", c_int32, [c_void_p, c_int32, c_int32, _I32P]),

@@ -265,10 +265,21 @@ class KVRuntime:
         self._bind()
         _check(self.lib.kvrt_reset_slot_async(self._ctx, int(slot)), "kvrt_reset_slot_async")
 
+    # Query rows per kv head (g * Q) above which attention runs on the MFMA
+    # prefill kernel instead of the split-K decode kernel.
+    DECODE_MAX_ROWS = 16
+
     def attend(self, layer: int, q: torch.Tensor, slots: Sequence[int], scale: float,
                out: torch.Tensor | None = None) -> torch.Tensor:
-        """Decode attention of q [n, Hq, Q, D] over the last Q positions of each slot."""
+        """Attention of q [n, Hq, Q, D] over the last Q positions of each slot.
+
+        Decode shapes (g * Q <= 16 query rows per kv head) take the split-K
+        decode kernel; larger chunks (prefill, text appends) the MFMA kernel.
+        """
         require_cuda(q, "q")
+        spec = self.layers[self._owner(layer)]
+        if (q.shape[1] // max(1, spec.kv_heads)) * q.shape[2] > self.DECODE_MAX_ROWS:
+            return self.attend_prefill(layer, q, slots, scale, out=out)
         q = q.contiguous()
         out = torch.empty_like(q) if out is None else out
         self._bind()
@@ -277,6 +288,20 @@ class KVRuntime:
         _check(self.lib.kvrt_attend_decode_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(od),
                                                  float(scale)),
                "kvrt_attend_decode_async")
+        return out
+
+    def attend_prefill(self, layer: int, q: torch.Tensor, slots: Sequence[int], scale: float,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+        """Chunked-prefill attention (MFMA) of q [n, Hq, Q, D] over the last Q positions."""
+        require_cuda(q, "q")
+        q = q.contiguous()
+        out = torch.empty_like(q) if out is None else out
+        self._bind()
+        arr, n = self._slots(slots)
+        qd, od = tensor_desc(q), tensor_desc(out)
+        _check(self.lib.kvrt_attend_prefill_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(od),
+                                                  float(scale)),
+               "kvrt_attend_prefill_async")
         return out
 
     def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

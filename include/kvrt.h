@@ -65,6 +65,7 @@ extern "C" {
 #define KVRT_CAP_GATHER (1ull << 5)
 #define KVRT_CAP_DEVICE_LENGTHS (1ull << 6)
 #define KVRT_CAP_TENSOR_ATTEND (1ull << 7)
+#define KVRT_CAP_PREFILL_MFMA (1ull << 8)
 
 /* ---- enums ------------------------------------------------------------- */
 enum kvrt_layout {
@@ -110,7 +111,7 @@ typedef struct kvrt_config {
     int32_t capacity;     /* max logical tokens per slot                      */
     int32_t block_size;   /* PAGED: tokens per page (power of two, e.g. 16)   */
     int32_t pool_pages;   /* PAGED: pages in the shared pool                  */
-    int32_t max_q;        /* max rows per append / query rows per attend      */
+    int32_t max_q;        /* max rows per decode append / attend; RING rows >= W + max_q - 1 */
     int32_t reserved;
 } kvrt_config;
 
@@ -272,6 +273,20 @@ int kvrt_attend_decode_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
 int kvrt_append_attend_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
                              const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
                              const kvrt_tensor *out, float scale);
+
+/* Chunked-prefill attention on MFMA: q [n, Hq, Q, D] bf16 contiguous holds
+ * the queries of the last Q positions of each slot (append the chunk's K/V
+ * first, e.g. with kvrt_append_async); out likewise. Same visibility, scale
+ * and GQA head map as kvrt_attend_decode_async, for any Q <= length. P
+ * enters the P.V product as a sum of two bf16 terms (~2^-17 relative);
+ * scores, softmax and both products accumulate in fp32. bf16 layers only; Hq / kv_heads <= 16 (<= 8 for
+ * head_dim >= 256). RING layers need ring_rows >= Q + window - 1, PAGED
+ * layers the pages of the oldest visible key (KVRT_ESTATE otherwise).
+ * Replaces kernel_prefill_sdpa_bf16 (native/gemma4_listener_microbatch/
+ * gemma4_listener_kernels.cuh:692-790) and the Q3..Q8 text-append attention
+ * of the listener batch API (gemma4_listener_microbatch_impl.inc:3476-3586). */
+int kvrt_attend_prefill_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                              const kvrt_tensor *q, const kvrt_tensor *out, float scale);
 
 /* ---- context-free tensor kernels ------------------------------------------ */
 /* Decode attention over caller-owned HF-shaped K/V: k, v [n, kv_heads, Lmax, D]

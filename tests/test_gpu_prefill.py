@@ -1,0 +1,112 @@
+"""GPU parity of the chunked-prefill MFMA attention (kvrt_attend_prefill_async)
+against the fp64 oracle: Gemma sliding layers at the reference's canonical
+prefill length (Q = 291 with a 512 window, ring of 802 rows), Gemma full
+layers (D = 512), talker prefill (16 q / 8 kv heads), Q3..Q8 text appends, paged
+storage and ragged streams. Tolerance max-abs 1e-2 on bf16 outputs."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from tests.helpers import randn_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+ATOL = 1e-2
+
+
+def _setup(hq, hkv, d, window, layout, prefix_lens, qn, seed):
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(seed)
+    kw = {}
+    if layout == "ring":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="ring", window=window, ring_rows=window + qn - 1)
+    elif layout == "paged":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="paged", window=window)
+        kw = dict(block_size=16, pool_pages=512)
+    else:
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, window=window)
+    n = len(prefix_lens)
+    rt = KVRuntime([spec], n, max(prefix_lens) + qn + 8, max_q=qn, device="cuda", **kw)
+    orc = O.OracleCache([O.OracleLayer(hkv, d, window)], n)
+    for s, p in enumerate(prefix_lens):
+        if p:
+            k, v = randn_bf16(gen, (1, hkv, p, d)), randn_bf16(gen, (1, hkv, p, d))
+            rt.import_(s, 0, k.cuda(), v.cuda())
+            orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    # the chunk's own K/V rows go in first (prefill-length append), then attention
+    k, v = randn_bf16(gen, (n, hkv, qn, d)), randn_bf16(gen, (n, hkv, qn, d))
+    rt.append(0, k.cuda(), v.cuda(), list(range(n)))
+    for s in range(n):
+        orc.append(s, 0, to_np(k[s]), to_np(v[s]))
+    q = randn_bf16(gen, (n, hq, qn, d), 0.5)
+    return rt, orc, q
+
+
+def _check(rt, orc, q, scale, prefill=True):
+    n = q.shape[0]
+    fn = rt.attend_prefill if prefill else rt.attend
+    out = fn(0, q.cuda(), list(range(n)), scale)
+    torch.cuda.synchronize()
+    assert rt.health() == 0
+    worst = 0.0
+    for s in range(n):
+        ref = orc.attend(s, 0, to_np(q[s]), scale)
+        worst = max(worst, float(np.abs(to_np(out[s]) - ref).max()))
+    assert worst <= ATOL, worst
+    return out
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,d,window,layout,prefix,qn",
+    [
+        (8, 1, 256, 512, "ring", [0], 291),          # Gemma sliding, canonical prefill target
+        (8, 1, 256, 512, "ring", [700], 291),        # ... over a ring that has wrapped
+        (8, 1, 512, 0, "contig", [0, 130], 291),     # Gemma full layers, D = 512
+        (16, 8, 128, 0, "contig", [37, 0, 400], 100),  # talker prefill, ragged prefixes
+        (8, 1, 256, 512, "ring", [1500, 20], 8),     # Q8 text append (64 rows per kv head)
+        (8, 1, 256, 0, "contig", [300], 3),          # Q3 text append
+        (4, 4, 64, 0, "paged", [45, 300], 37),       # paged pool
+        (4, 2, 128, 24, "paged", [200], 50),         # paged + window
+    ],
+)
+def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):
+    rt, orc, q = _setup(hq, hkv, d, window, layout, prefix, qn, seed=hq * 7 + d + qn)
+    _check(rt, orc, q, 1.0 / math.sqrt(d))
+
+
+def test_prefill_single_query_and_decode_dispatch():
+    """Q = 1 through the MFMA kernel; g * Q above 16 rows dispatches to it from attend()."""
+    rt, orc, q = _setup(2, 1, 128, 0, "contig", [77], 1, seed=5)
+    _check(rt, orc, q, 0.1)
+    rt, orc, q = _setup(8, 1, 256, 512, "ring", [900], 4, seed=6)  # 32 rows per kv head
+    _check(rt, orc, q, 1.0 / 16, prefill=False)
+
+
+def test_prefill_and_decode_agree_where_both_apply():
+    rt, orc, q = _setup(4, 2, 128, 0, "contig", [500, 123], 4, seed=7)
+    a = rt.attend_prefill(0, q.cuda(), [0, 1], 0.09)
+    b = rt.attend(0, q.cuda(), [0, 1], 0.09)  # 8 rows per kv head: decode kernel
+    torch.cuda.synchronize()
+    assert float((a.float() - b.float()).abs().max()) <= ATOL
+
+
+def test_prefill_rejects_what_it_cannot_see():
+    from kvrt import KVRTError, KVRuntime, LayerSpec
+
+    rt = KVRuntime([LayerSpec(kv_heads=1, head_dim=256, layout="ring", window=64, ring_rows=64 + 8 - 1)], 1, 4096,
+                   max_q=8, device="cuda")
+    x = torch.zeros((1, 1, 1000, 256), dtype=torch.bfloat16, device="cuda")
+    rt.import_(0, 0, x, x)
+    q = torch.zeros((1, 8, 16, 256), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(KVRTError) as e:  # 16 queries need 16 + 63 resident rows, the ring keeps 71
+        rt.attend_prefill(0, q, [0], 0.1)
+    assert e.value.code == -2
+    q = torch.zeros((1, 8, 1001, 256), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(KVRTError):  # more queries than positions
+        rt.attend_prefill(0, q, [0], 0.1)
+    assert rt.health() == 0

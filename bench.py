@@ -60,6 +60,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
+    p.add_argument("--mode", choices=("step", "prefill"), default="step",
+                   help="step: the north-star decode step (default); prefill: the MFMA chunked-prefill "
+                        "attention at thinker/talker shapes (one JSON line of per-case TFLOP/s)")
     return p.parse_args()
 
 
@@ -269,6 +272,64 @@ def cpu_baseline(args) -> dict | None:
     }
 
 
+PREFILL_CASES = [
+    # name, streams, Hq, Hkv, D, Q, prefix, window
+    ("thinker_sliding_q291", 4, 8, 1, 256, 291, 2048, 512),
+    ("thinker_full_d512_q291", 4, 8, 1, 512, 291, 2048, 0),
+    ("talker_prefill_q512", 4, 16, 8, 128, 512, 0, 0),
+    ("thinker_prefill_q2048", 1, 8, 1, 256, 2048, 0, 0),
+    ("thinker_full_d512_q2048", 4, 8, 1, 512, 2048, 2048, 0),
+]
+MFMA_BF16_PEAK = 2.5e15  # FLOP/s, MI355X dense bf16
+
+
+def run_prefill(args) -> int:
+    """Chunked-prefill attention (kvrt_attend_prefill_async) at thinker/talker
+    shapes: algorithmic FLOPs = 4 * D per visible (query, key, q head)."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    results = []
+    for name, n, hq, hkv, d, qn, prefix, window in PREFILL_CASES:
+        layout = "ring" if window else "contig"
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window,
+                         ring_rows=window + qn - 1 if window else 0)
+        rt = KVRuntime([spec], n, prefix + qn + 8, max_q=qn, device="cuda")
+        for s in range(n):
+            kv = torch.randn((1, hkv, prefix + qn, d), generator=gen, device="cuda").to(torch.bfloat16)
+            rt.import_(s, 0, kv, kv)
+        q = torch.randn((n, hq, qn, d), generator=gen, device="cuda").to(torch.bfloat16)
+        o = torch.empty_like(q)
+        L = prefix + qn
+        vis = sum(min(L - qn + i + 1, window) if window else L - qn + i + 1 for i in range(qn))
+        flops = 4.0 * d * vis * hq * n
+        times = []
+        for _ in range(args.warmup + args.steps):
+            torch.cuda._sleep(1_000_000)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            rt.attend_prefill(0, q, list(range(n)), 1.0 / math.sqrt(d), out=o)
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e-3)
+        if rt.health() != 0:
+            raise RuntimeError(f"kvrt health check failed in prefill case {name}")
+        t = sorted(times[args.warmup:])[len(times[args.warmup:]) // 2]  # median
+        results.append({"case": name, "streams": n, "hq": hq, "hkv": hkv, "head_dim": d, "q": qn,
+                        "prefix": prefix, "window": window, "us": round(t * 1e6, 2),
+                        "tflops": round(flops / t / 1e12, 1), "mfma_frac": round(flops / t / MFMA_BF16_PEAK, 4)})
+        rt.close()
+    best = max(results, key=lambda r: r["tflops"])
+    print(json.dumps({
+        "metric": "chunked-prefill attention TFLOP/s (MFMA bf16), 1 MI355X", "value": best["tflops"],
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic",
+        "roofline": {"bound": "mfma", "achieved": best["tflops"], "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": best["mfma_frac"], "kernel": f"kvrt::prefill_kernel ({best['case']})"},
+        "cases": results}))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -279,6 +340,8 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    if args.mode == "prefill":
+        return run_prefill(args)
     gen = torch.Generator(device="cuda").manual_seed(1)
     margin = args.warmup + args.steps + args.kernel_reps + 8
     capacity = args.ctx + margin

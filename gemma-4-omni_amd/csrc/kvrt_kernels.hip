@@ -629,6 +629,7 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
 
     for (int t0 = kstart; t0 < kend; t0 += kPfKeys) {
         __syncthreads();  // the previous tile has been consumed
+        // K: row copies, consecutive threads on consecutive 16 B of a row.
         for (int c = threadIdx.x; c < kPfKeys * (D / 8); c += blockDim.x) {
             const int kr = c / (D / 8), seg = c % (D / 8);
             const int key = t0 + kr;
@@ -638,9 +639,17 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
                 bad |= off < 0;
                 off = off < 0 ? 0 : off;
             }
-            const uint4 kx = *reinterpret_cast<const uint4 *>(kg + off + 8 * seg);
+            *reinterpret_cast<uint4 *>(&sk[kr * KP + 8 * seg]) = *reinterpret_cast<const uint4 *>(kg + off + 8 * seg);
+        }
+        // V transposed: consecutive threads on consecutive keys of one 8-dim
+        // segment, so each 2-byte LDS store of a wave covers adjacent words.
+        for (int c = threadIdx.x; c < kPfKeys * (D / 8); c += blockDim.x) {
+            const int kr = c % kPfKeys, seg = c / kPfKeys;
+            const int key = t0 + kr;
+            const int kc = key < kend ? key : kstart;
+            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) off = off < 0 ? 0 : off;
             const uint4 vx = *reinterpret_cast<const uint4 *>(vg + off + 8 * seg);
-            *reinterpret_cast<uint4 *>(&sk[kr * KP + 8 * seg]) = kx;
             const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {

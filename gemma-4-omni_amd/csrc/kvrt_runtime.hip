@@ -13,6 +13,7 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <random>
 #include <vector>
 
 #include "kvrt_internal.h"
@@ -427,6 +428,10 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
             return fail(KVRT_EDEVICE);
         c->free_pages.reserve(cfg->pool_pages);
         for (int p = cfg->pool_pages - 1; p >= 0; --p) c->free_pages.push_back(p);
+        if (cfg->pool_seed != 0) {
+            std::mt19937 rng((uint32_t)cfg->pool_seed);
+            std::shuffle(c->free_pages.begin(), c->free_pages.end(), rng);
+        }
         c->first_live.assign(cfg->n_slots, 0);
     }
     c->ws_bytes = 0;

@@ -74,7 +74,7 @@ class KvrtConfig(ctypes.Structure):
         ("block_size", c_int32),
         ("pool_pages", c_int32),
         ("max_q", c_int32),
-        ("reserved", c_int32),
+        ("pool_seed", c_int32),
     ]
 
 

@@ -111,6 +111,7 @@ class KVRuntime:
         max_q: int = 2,
         block_size: int = 16,
         pool_pages: int = 0,
+        pool_seed: int = 0,
         device: torch.device | str | None = None,
     ) -> None:
         self.lib = L.load()
@@ -134,7 +135,7 @@ class KVRuntime:
         cfg.block_size = self.block_size
         cfg.pool_pages = self.pool_pages
         cfg.max_q = self.max_q
-        cfg.reserved = 0
+        cfg.pool_seed = int(pool_seed)
         self._cfg = cfg
         specs = (L.KvrtLayerSpec * len(self.layers))(*[s.to_c() for s in self.layers])
         self._specs = specs

@@ -112,7 +112,8 @@ typedef struct kvrt_config {
     int32_t block_size;   /* PAGED: tokens per page (power of two, e.g. 16)   */
     int32_t pool_pages;   /* PAGED: pages in the shared pool                  */
     int32_t max_q;        /* max rows per decode append / attend; RING rows >= W + max_q - 1 */
-    int32_t reserved;
+    int32_t pool_seed;    /* PAGED: nonzero = hand out pool pages in an order
+                             shuffled with this seed (0 = ascending)          */
 } kvrt_config;
 
 /* Optional caller-owned storage for one layer (kvrt_create_with_storage).

@@ -193,6 +193,30 @@ class OracleLayer:
     int8: bool = False
 
 
+class _Rows:
+    """Rows [H, n, ...] with amortised O(1) append (capacity doubling)."""
+
+    def __init__(self, heads: int, tail: tuple, dtype) -> None:
+        self.buf = np.zeros((heads, 16) + tail, dtype=dtype)
+        self.n = 0
+
+    def view(self) -> np.ndarray:
+        return self.buf[:, :self.n]
+
+    def append(self, x: np.ndarray) -> None:
+        q = x.shape[1]
+        if self.n + q > self.buf.shape[1]:
+            grown = np.zeros((self.buf.shape[0], max(2 * self.buf.shape[1], self.n + q)) + self.buf.shape[2:],
+                             dtype=self.buf.dtype)
+            grown[:, :self.n] = self.buf[:, :self.n]
+            self.buf = grown
+        self.buf[:, self.n:self.n + q] = x
+        self.n += q
+
+    def truncate(self, n: int) -> None:
+        self.n = min(self.n, int(n))
+
+
 @dataclass
 class OracleCache:
     """Logical KV of n_slots sessions: per (slot, layer) full-history rows.
@@ -203,50 +227,44 @@ class OracleCache:
 
     layers: list
     n_slots: int
-    k: dict = field(default_factory=dict)
-    v: dict = field(default_factory=dict)
-    ks: dict = field(default_factory=dict)
-    vs: dict = field(default_factory=dict)
+    rows: dict = field(default_factory=dict)
 
     def _get(self, slot, layer):
         key = (slot, layer)
-        if key not in self.k:
+        if key not in self.rows:
             spec = self.layers[layer]
             dt = np.int8 if spec.int8 else np.float32
-            self.k[key] = np.zeros((spec.kv_heads, 0, spec.head_dim), dtype=dt)
-            self.v[key] = np.zeros((spec.kv_heads, 0, spec.head_dim), dtype=dt)
-            self.ks[key] = np.zeros((spec.kv_heads, 0), dtype=np.float32)
-            self.vs[key] = np.zeros((spec.kv_heads, 0), dtype=np.float32)
-        return key
+            self.rows[key] = (_Rows(spec.kv_heads, (spec.head_dim,), dt), _Rows(spec.kv_heads, (spec.head_dim,), dt),
+                              _Rows(spec.kv_heads, (), np.float32), _Rows(spec.kv_heads, (), np.float32))
+        return self.rows[key]
 
     def length(self, slot: int, layer: int) -> int:
-        return self.k[self._get(slot, layer)].shape[1]
+        return self._get(slot, layer)[0].n
 
     def append(self, slot: int, layer: int, k: np.ndarray, v: np.ndarray) -> None:
         """k, v [Hkv, Q, D] float32 (bf16 values): concatenate along positions."""
-        key = self._get(slot, layer)
+        kr, vr, ks, vs = self._get(slot, layer)
         if self.layers[layer].int8:
             kq, ksc = quantize_int8(k)
             vq, vsc = quantize_int8(v)
-            self.k[key] = np.concatenate([self.k[key], kq], axis=1)
-            self.v[key] = np.concatenate([self.v[key], vq], axis=1)
-            self.ks[key] = np.concatenate([self.ks[key], ksc], axis=1)
-            self.vs[key] = np.concatenate([self.vs[key], vsc], axis=1)
+            kr.append(kq)
+            vr.append(vq)
+            ks.append(ksc)
+            vs.append(vsc)
         else:
-            self.k[key] = np.concatenate([self.k[key], np.asarray(k, np.float32)], axis=1)
-            self.v[key] = np.concatenate([self.v[key], np.asarray(v, np.float32)], axis=1)
+            kr.append(np.asarray(k, np.float32))
+            vr.append(np.asarray(v, np.float32))
 
     def truncate(self, slot: int, layer: int, keep_len: int) -> None:
-        key = self._get(slot, layer)
-        for d in (self.k, self.v, self.ks, self.vs):
-            d[key] = d[key][:, :keep_len]
+        for r in self._get(slot, layer):
+            r.truncate(keep_len)
 
     def values(self, slot: int, layer: int) -> tuple[np.ndarray, np.ndarray]:
         """Dequantised float32 K, V [Hkv, L, D]."""
-        key = self._get(slot, layer)
+        kr, vr, ks, vs = self._get(slot, layer)
         if self.layers[layer].int8:
-            return dequantize_int8(self.k[key], self.ks[key]), dequantize_int8(self.v[key], self.vs[key])
-        return self.k[key], self.v[key]
+            return dequantize_int8(kr.view(), ks.view()), dequantize_int8(vr.view(), vs.view())
+        return kr.view(), vr.view()
 
     def gather(self, layer: int, slots: list[int], lmax: int, start: list[int] | None = None):
         """Padded [n, Hkv, lmax, D] float32 K, V and bool mask [n, lmax]."""
@@ -269,8 +287,11 @@ class OracleCache:
         kk, vv = self.values(slot, layer)
         n_keys = kk.shape[1]
         qn = q.shape[1]
+        window = self.layers[layer].window
+        lo = 0 if window <= 0 else max(0, n_keys - qn - window + 1)
         pos = np.arange(n_keys - qn, n_keys)
-        return attend(q, kk, vv, pos, scale, self.layers[layer].window)
+        # keys below the first query's window are never visible: skip them
+        return attend(q, kk[:, lo:], vv[:, lo:], pos, scale, window, key_positions=np.arange(lo, n_keys))
 
 
 def sliding_retained(length: int, window: int) -> tuple[int, int]:

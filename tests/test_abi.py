@@ -69,7 +69,7 @@ int main(void) {
   F(kvrt_layer_spec, window); F(kvrt_layer_spec, ring_rows); F(kvrt_layer_spec, shared_src);
   F(kvrt_layer_spec, reserved);
   F(kvrt_config, struct_size); F(kvrt_config, n_layers); F(kvrt_config, n_slots); F(kvrt_config, capacity);
-  F(kvrt_config, block_size); F(kvrt_config, pool_pages); F(kvrt_config, max_q); F(kvrt_config, reserved);
+  F(kvrt_config, block_size); F(kvrt_config, pool_pages); F(kvrt_config, max_q); F(kvrt_config, pool_seed);
   F(kvrt_storage, k); F(kvrt_storage, v); F(kvrt_storage, k_scale); F(kvrt_storage, v_scale);
   F(kvrt_counters, launches); F(kvrt_counters, appended_rows); F(kvrt_counters, appended_bytes);
   F(kvrt_counters, attended_keys); F(kvrt_counters, attended_bytes); F(kvrt_counters, gathered_bytes);

@@ -119,6 +119,27 @@ struct DecodeArgs {
     int32_t slots[kMaxItems];
 };
 
+// Talker visibility of one item (host-validated: 0 <= prefix_start <=
+// prefix_pos < audio_start <= audio_pos < length). Query row i of the item is
+// the audio query when i == Q - 1, the prefix query otherwise (Q = 2).
+//   prefix query: keys [0, max(prefix_pos, prefix_start - 1)]
+//   audio query:  keys [0, prefix_start) U [prefix_start, prefix_pos] (mode != 1)
+//                      U [audio_start, audio_pos]
+// and in mode 2 the audio query's score of a key in [prefix_start, prefix_pos]
+// gets gate_log2 added (log2 domain).
+struct TalkerItem {
+    int32_t prefix_start;
+    int32_t prefix_pos;
+    int32_t audio_start;
+    int32_t audio_pos;
+    int32_t mode;
+    float gate_log2;
+};
+
+struct TalkerArgs : DecodeArgs {
+    TalkerItem talk[kMaxItems];
+};
+
 struct PrefillArgs {
     KVView kv;
     Lengths len;
@@ -154,6 +175,8 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
 // Split-K attention over the view, then the merge kernel.
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head,
                          hipStream_t s);
+// The same split-K decode under the talker visibility (bf16 CONTIG layers).
+hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s);
 // Chunked-prefill attention on MFMA (bf16 CONTIG / RING / PAGED layers).
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
 // Largest GQA group (waves per workgroup) of the prefill kernel for a head dim.

@@ -13,6 +13,8 @@
 //
 // Every memory-bound loop moves 16 B per lane with consecutive lanes on
 // consecutive addresses (one 1 KiB transaction per wave instruction).
+#include <type_traits>
+
 #include "kvrt_device.h"
 #include "kvrt_internal.h"
 
@@ -226,8 +228,12 @@ struct DecodeLds {
 // 16 B each) and KPW = 64/LPR key rows are in flight per load instruction.
 // The R rows of a kv head are its g q heads x Q query positions
 // (row r = j*Q + i for q head kvh*g + j, query i).
-template <int D, int R, int KDT, int LAYOUT>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+// Args is DecodeArgs (causal / sliding-window visibility) or TalkerArgs (the
+// talker's per-item prefix / audio ranges, bf16 CONTIG layers only).
+template <int D, int R, int KDT, int LAYOUT, class Args = DecodeArgs>
+__global__ __launch_bounds__(256) void decode_kernel(Args a) {
+    constexpr bool TALK = !std::is_same<Args, DecodeArgs>::value;
+    static_assert(!TALK || (KDT == KVRT_BF16 && LAYOUT == KVRT_LAYOUT_CONTIG), "talker: bf16 CONTIG");
     constexpr int VEC = (KDT == KVRT_INT8) ? 16 : 8;
     constexpr int LPR = D / VEC;
     constexpr int KPW = 64 / LPR;
@@ -249,6 +255,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     const int rows = a.group * Qn;
     const bool fused = (KDT == KVRT_BF16) && a.k_new != nullptr;
     int kend = fused ? len + Qn : len;
+    if constexpr (TALK) kend = min(kend, a.talk[item].audio_pos + 1);
     if (LAYOUT == KVRT_LAYOUT_CONTIG && kend > a.kv.rows) {
         // a length beyond the rows of the view (caller-provided lengths):
         // clamp the reads and raise the device flag
@@ -307,13 +314,35 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             for (int t = 0; t < QW; ++t) qw[r][t] = 0u;
         }
     }
-    // Per-row visibility bounds: key in [lo_r, hi_r].
-    int hi[R], lo[R];
+    // Per-row visibility: key in [lo_r, hi_r]; talker rows add the audio
+    // range [alo_r, ahi_r] and the gate gb_r over [blo, bhi].
+    int hi[R], lo[R], alo[R], ahi[R];
+    float gb[R];
+    int blo = 0, bhi = -1;
+    if constexpr (TALK) {
+        const TalkerItem t = a.talk[item];
+        blo = t.prefix_start;
+        bhi = t.prefix_pos;
+        const int base_hi = max(t.prefix_pos, t.prefix_start - 1);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int p = p0 + (r % Qn);
-        hi[r] = r < rows ? p : -1;
-        lo[r] = a.window > 0 ? p - a.window + 1 : 0;
+        for (int r = 0; r < R; ++r) {
+            const bool audio = (r % Qn) == Qn - 1;
+            lo[r] = 0;
+            hi[r] = r >= rows ? -1 : (audio && t.mode == 1 ? t.prefix_start - 1 : base_hi);
+            alo[r] = r < rows && audio ? t.audio_start : 0x7fffffff;
+            ahi[r] = r < rows && audio ? t.audio_pos : -1;
+            gb[r] = audio && t.mode == 2 ? t.gate_log2 : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int p = p0 + (r % Qn);
+            hi[r] = r < rows ? p : -1;
+            lo[r] = a.window > 0 ? p - a.window + 1 : 0;
+            alo[r] = 0x7fffffff;
+            ahi[r] = -1;
+            gb[r] = 0.f;
+        }
     }
 
     float m_run[R], l_run[R], acc[R][VEC];
@@ -392,8 +421,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
                 }
                 d = group_sum<LPR>(d);
                 if constexpr (KDT == KVRT_INT8) d *= ksc[u];
-                const bool vis = key[u] <= hi[r] && key[u] >= lo[r];
-                s[u][r] = vis ? d * a.scale_log2 : -INFINITY;
+                if constexpr (TALK) {
+                    const bool vis = key[u] <= hi[r] || (key[u] >= alo[r] && key[u] <= ahi[r]);
+                    const bool gated = key[u] >= blo && key[u] <= bhi;
+                    s[u][r] = vis ? fmaf(d, a.scale_log2, gated ? gb[r] : 0.f) : -INFINITY;
+                } else {
+                    const bool vis = key[u] <= hi[r] && key[u] >= lo[r];
+                    s[u][r] = vis ? d * a.scale_log2 : -INFINITY;
+                }
             }
         }
         // online softmax, one rescale per block of U keys
@@ -842,6 +877,32 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_
         case 4: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 4>(a, dtype, s)); break;
         case 8: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 8>(a, dtype, s)); break;
         case 16: KVRT_DISPATCH_D(head_dim, return launch_decode_rt<HD, 16>(a, dtype, s)); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int HD, int RT>
+static hipError_t launch_talker_rt(const TalkerArgs &a, hipStream_t s) {
+    dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
+    hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, KVRT_LAYOUT_CONTIG, TalkerArgs>), grid, block, 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const DecodeArgs &m = a;
+    const int chunks = (a.group * a.qn * HD + 255) / 256;
+    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items, chunks), dim3(256), 0, s, m);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s) {
+    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.kv.layout != KVRT_LAYOUT_CONTIG || a.advance != 0)
+        return hipErrorInvalidValue;
+    switch (rows_tile(rows_per_head)) {
+        case 1: KVRT_DISPATCH_D(head_dim, return launch_talker_rt<HD, 1>(a, s)); break;
+        case 2: KVRT_DISPATCH_D(head_dim, return launch_talker_rt<HD, 2>(a, s)); break;
+        case 4: KVRT_DISPATCH_D(head_dim, return launch_talker_rt<HD, 4>(a, s)); break;
+        case 8: KVRT_DISPATCH_D(head_dim, return launch_talker_rt<HD, 8>(a, s)); break;
+        case 16: KVRT_DISPATCH_D(head_dim, return launch_talker_rt<HD, 16>(a, s)); break;
         default: return hipErrorInvalidValue;
     }
     return hipErrorInvalidValue;

@@ -441,11 +441,49 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     return KVRT_OK;
 }
 
-// Launch the split-K decode for n slots of one layer (fused when k/v given).
+// bf16 round-to-nearest-even of a finite float, back as a float.
+float round_bf16(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+
+// Validate the talker visibility of n items against the host lengths and
+// lower it to the kernel's form; the key count of item i is audio_position + 1.
+int talker_items(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_talker_mask *m,
+                 TalkerItem *out) {
+    for (int i = 0; i < n; ++i) {
+        const kvrt_talker_mask &t = m[i];
+        if (t.prefix_attention_mode < 0 || t.prefix_attention_mode > 2 || !std::isfinite(t.prefix_log_gate) ||
+            (t.prefix_attention_mode == 2 && t.visible_prefix_count <= 0))
+            return KVRT_EINVAL;
+        if (t.prefix_start < 0 || t.prefix_position < t.prefix_start || t.audio_start <= t.prefix_position ||
+            t.audio_position < t.audio_start)
+            return KVRT_EINVAL;
+        if (t.audio_position >= c->len_at(slots[i], layer)) return KVRT_ESTATE;
+        // the additive mask value of the reference: fp32 gate - logf(count), stored as bf16
+        float g = 0.f;
+        if (t.prefix_attention_mode == 2) {
+            g = round_bf16(t.prefix_log_gate - logf((float)t.visible_prefix_count));
+            if (!std::isfinite(g)) return KVRT_EINVAL;
+        }
+        out[i] = TalkerItem{t.prefix_start, t.prefix_position, t.audio_start, t.audio_position,
+                            t.prefix_attention_mode, g * 1.4426950408889634f};
+    }
+    return KVRT_OK;
+}
+
+// Launch the split-K decode for n slots of one layer (fused when k/v given;
+// under the talker visibility when masks is given).
 int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_tensor *q,
-                const kvrt_tensor *k, const kvrt_tensor *v, const kvrt_tensor *out, float scale) {
+                const kvrt_tensor *k, const kvrt_tensor *v, const kvrt_tensor *out, float scale,
+                const kvrt_talker_mask *masks = nullptr) {
     const kvrt_layer_spec &s = c->layers[layer].spec;
     const bool fused = k != nullptr;
+    const bool talker = masks != nullptr;
     const int D = s.head_dim, hkv = s.kv_heads;
     if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
         return KVRT_EINVAL;
@@ -459,6 +497,13 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     if (rows_tile(rows) == 0) return KVRT_EINVAL;
     if (s.dtype == KVRT_INT8 && rows_tile(rows) > kMaxInt8Rows) return KVRT_EINVAL;
     if (!std::isfinite(scale)) return KVRT_EINVAL;
+    TalkerItem titems[kMaxItems];
+    if (talker) {
+        if (fused || s.dtype != KVRT_BF16 || s.layout != KVRT_LAYOUT_CONTIG || s.window != 0 || qn > 2)
+            return KVRT_EINVAL;
+        const int rc = talker_items(c, layer, n, slots, masks, titems);
+        if (rc != KVRT_OK) return rc;
+    }
     if (fused) {
         if (s.dtype != KVRT_BF16) return KVRT_EINVAL;
         if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4) || !is_contiguous(k) || !is_contiguous(v))
@@ -479,7 +524,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         if (s.layout == KVRT_LAYOUT_PAGED && Lnew - (int)qn - s.window + 1 < c->first_live[slots[i]] * c->cfg.block_size &&
             (s.window == 0 || c->first_live[slots[i]] > 0))
             return KVRT_ESTATE;  // the window would read evicted pages
-        max_keys = std::max<int64_t>(max_keys, visible_keys(s, Lnew, (int)qn));
+        max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
     }
     const int R = rows_tile(rows);
     const int n_split = choose_splits(n, hkv, max_keys, keys_per_iteration(D, R, s.dtype));
@@ -512,6 +557,18 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches += 2;
+    if (talker) {
+        TalkerArgs t{};
+        static_cast<DecodeArgs &>(t) = a;
+        for (int i = 0; i < n; ++i) t.talk[i] = titems[i];
+        if (launch_decode_talker(t, D, rows, c->stream) != hipSuccess) return poison(c);
+        for (int i = 0; i < n; ++i) {
+            const uint64_t keys = (uint64_t)titems[i].audio_pos + 1;
+            c->counters.attended_keys += keys * hkv;
+            c->counters.attended_bytes += keys * hkv * (uint64_t)D * 2 * 2;
+        }
+        return KVRT_OK;
+    }
     if (launch_decode(a, D, s.dtype, rows, c->stream) != hipSuccess) return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
     for (int i = 0; i < n; ++i) {
@@ -627,7 +684,8 @@ uint32_t kvrt_abi_version(void) { return KVRT_ABI_VERSION; }
 
 uint64_t kvrt_capabilities(void) {
     return KVRT_CAP_CONTIG | KVRT_CAP_RING | KVRT_CAP_PAGED | KVRT_CAP_INT8 | KVRT_CAP_FUSED_APPEND_ATTEND |
-           KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND | KVRT_CAP_PREFILL_MFMA;
+           KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND | KVRT_CAP_PREFILL_MFMA |
+           KVRT_CAP_TALKER_MASK;
 }
 
 const char *kvrt_strerror(int code) {
@@ -1029,6 +1087,14 @@ int kvrt_attend_decode_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_
     if (rc) return rc;
     if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
     return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
+}
+
+int kvrt_attend_talker_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *q,
+                             const kvrt_tensor *out, float scale, const kvrt_talker_mask *masks) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !masks) return KVRT_EINVAL;
+    return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale, masks);
 }
 
 int kvrt_append_attend_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *q,

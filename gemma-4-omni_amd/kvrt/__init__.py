@@ -10,7 +10,7 @@ behind the C ABI of include/kvrt.h (libkvrt.so, built in-tree).
 * ``kvrt.talker`` — HF talker cache import and the Q1 position counter.
 """
 from .cache import KVRTCache, KVRTCacheLayer, append_attend, attend, attend_padded, gather
-from .runtime import KVRTError, KVRuntime, LayerSpec, attend_tensors, copy_rows
+from .runtime import KVRTError, KVRuntime, LayerSpec, TalkerMask, attend_tensors, copy_rows
 
-__all__ = ["KVRTCache", "KVRTCacheLayer", "KVRTError", "KVRuntime", "LayerSpec", "append_attend", "attend",
+__all__ = ["KVRTCache", "KVRTCacheLayer", "KVRTError", "KVRuntime", "LayerSpec", "TalkerMask", "append_attend", "attend",
            "attend_padded", "attend_tensors", "copy_rows", "gather"]

@@ -40,6 +40,7 @@ CAP_GATHER = 1 << 5
 CAP_DEVICE_LENGTHS = 1 << 6
 CAP_TENSOR_ATTEND = 1 << 7
 CAP_PREFILL_MFMA = 1 << 8
+CAP_TALKER_MASK = 1 << 9
 
 
 class KvrtTensor(ctypes.Structure):
@@ -97,6 +98,18 @@ class KvrtCounters(ctypes.Structure):
     ]
 
 
+class KvrtTalkerMask(ctypes.Structure):
+    _fields_ = [
+        ("prefix_start", c_int32),
+        ("audio_start", c_int32),
+        ("prefix_position", c_int32),
+        ("audio_position", c_int32),
+        ("prefix_attention_mode", c_int32),
+        ("visible_prefix_count", c_int32),
+        ("prefix_log_gate", c_float),
+    ]
+
+
 # (name, restype, argtypes) of every symbol declared in include/kvrt.h.
 _T = POINTER(KvrtTensor)
 _I32P = POINTER(c_int32)
@@ -123,6 +136,8 @@ SIGNATURES = [
     ("kvrt_attend_decode_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_append_attend_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _T, _T, c_float]),
     ("kvrt_attend_prefill_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
+    ("kvrt_attend_talker_async", c_int32,
+     [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float, POINTER(KvrtTalkerMask)]),
     ("kvrt_attend_tensors_async", c_int32, [_T, _T, _T, c_void_p, _T, c_float, c_int32, c_void_p]),
     ("kvrt_copy_rows_async", c_int32, [_T, _T, c_int64, c_void_p]),
     ("kvrt_session_state", c_int32, [c_void_p, c_int32, c_int32, _I32P]),

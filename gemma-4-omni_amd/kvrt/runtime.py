@@ -99,6 +99,53 @@ class LayerSpec:
         return s
 
 
+@dataclass(frozen=True)
+class TalkerMask:
+    """Talker visibility of one slot (absolute cache positions).
+
+    ``[0, prefix_start)`` is the stable text, ``[prefix_start, audio_start)``
+    the reserved prefix frames of which ``[prefix_start, prefix_position]``
+    are visible, ``[audio_start, audio_position]`` the audio frames so far.
+    With Q = 2 query rows (JOINT step) row 0 is the prefix query at
+    ``prefix_position`` and row 1 the audio query; with Q = 1 the single row
+    is the audio query (terminal / audio-only step, ``prefix_position`` =
+    the last visible prefix frame). ``prefix_attention_mode``: 0 audio
+    queries see the visible prefix, 1 they do not, 2 they see it with
+    ``prefix_log_gate - log(visible_prefix_count)`` (bf16) added to the
+    score. Mirrors the arguments of qwen_build_joint_mask /
+    qwen_build_audio_only_mask (native/qwen_talker/qwen_talker_kernels.cu:759-807)
+    and their checks in duplex_kernel/native_qwen_talker.py:1211-1214.
+    """
+
+    prefix_start: int
+    audio_start: int
+    prefix_position: int
+    audio_position: int
+    prefix_attention_mode: int = 0
+    visible_prefix_count: int = 0
+    prefix_log_gate: float = -8.0
+
+    def __post_init__(self) -> None:
+        if self.prefix_attention_mode not in (0, 1, 2) or not math.isfinite(float(self.prefix_log_gate)):
+            raise ValueError("invalid talker prefix gate: mode must be 0, 1 or 2 and the gate finite")
+        if self.prefix_attention_mode == 2 and int(self.visible_prefix_count) <= 0:
+            raise ValueError("the gated prefix mode needs visible_prefix_count > 0")
+        if not (0 <= self.prefix_start <= self.prefix_position < self.audio_start <= self.audio_position):
+            raise ValueError("talker positions must satisfy 0 <= prefix_start <= prefix_position < "
+                             "audio_start <= audio_position")
+
+    def to_c(self) -> L.KvrtTalkerMask:
+        m = L.KvrtTalkerMask()
+        m.prefix_start = int(self.prefix_start)
+        m.audio_start = int(self.audio_start)
+        m.prefix_position = int(self.prefix_position)
+        m.audio_position = int(self.audio_position)
+        m.prefix_attention_mode = int(self.prefix_attention_mode)
+        m.visible_prefix_count = int(self.visible_prefix_count)
+        m.prefix_log_gate = float(self.prefix_log_gate)
+        return m
+
+
 class KVRuntime:
     """One kvrt context: the KV state of ``n_slots`` sessions over ``layers``."""
 
@@ -303,6 +350,26 @@ class KVRuntime:
         _check(self.lib.kvrt_attend_prefill_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(od),
                                                   float(scale)),
                "kvrt_attend_prefill_async")
+        return out
+
+    def attend_talker(self, layer: int, q: torch.Tensor, slots: Sequence[int], scale: float,
+                      masks: Sequence["TalkerMask"], out: torch.Tensor | None = None) -> torch.Tensor:
+        """Talker attention of q [n, Hq, Q, D] (Q = 2: prefix then audio query;
+        Q = 1: audio query) under one :class:`TalkerMask` per slot."""
+        require_cuda(q, "q")
+        q = q.contiguous()
+        out = torch.empty_like(q) if out is None else out
+        self._bind()
+        arr, n = self._slots(slots)
+        if len(masks) != n:
+            raise ValueError(f"{len(masks)} talker masks for {n} slots")
+        marr = (L.KvrtTalkerMask * max(1, n))()
+        for i, m in enumerate(masks):
+            marr[i] = m.to_c()
+        qd, od = tensor_desc(q), tensor_desc(out)
+        _check(self.lib.kvrt_attend_talker_async(self._ctx, layer, n, arr, ctypes.byref(qd), ctypes.byref(od),
+                                                 float(scale), marr),
+               "kvrt_attend_talker_async")
         return out
 
     def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

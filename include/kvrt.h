@@ -66,6 +66,7 @@ extern "C" {
 #define KVRT_CAP_DEVICE_LENGTHS (1ull << 6)
 #define KVRT_CAP_TENSOR_ATTEND (1ull << 7)
 #define KVRT_CAP_PREFILL_MFMA (1ull << 8)
+#define KVRT_CAP_TALKER_MASK (1ull << 9)
 
 /* ---- enums ------------------------------------------------------------- */
 enum kvrt_layout {
@@ -288,6 +289,44 @@ int kvrt_append_attend_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
  * of the listener batch API (gemma4_listener_microbatch_impl.inc:3476-3586). */
 int kvrt_attend_prefill_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
                               const kvrt_tensor *q, const kvrt_tensor *out, float scale);
+
+/* Talker visibility of one slot for kvrt_attend_talker_async. Positions are
+ * absolute cache rows: [0, prefix_start) is the stable text, [prefix_start,
+ * audio_start) the reserved prefix frames of which [prefix_start,
+ * prefix_position] are visible, [audio_start, audio_position] the audio
+ * frames so far. prefix_attention_mode: 0 audio queries see the visible
+ * prefix, 1 they do not, 2 they see it with prefix_log_gate -
+ * log(visible_prefix_count) (rounded to bf16) added to those scores. */
+typedef struct kvrt_talker_mask {
+    int32_t prefix_start;
+    int32_t audio_start;
+    int32_t prefix_position;
+    int32_t audio_position;
+    int32_t prefix_attention_mode;
+    int32_t visible_prefix_count;
+    float prefix_log_gate;
+} kvrt_talker_mask;
+
+/* Talker attention for n slots of one CONTIG bf16 layer with window 0:
+ * q, out [n, Hq, Q, D] bf16 contiguous with Q = 2 (JOINT step: row 0 the
+ * prefix query at prefix_position, row 1 the audio query at audio_position)
+ * or Q = 1 (audio-only query at audio_position, prefix_position being the
+ * last visible prefix frame). Key k is visible to
+ *   the prefix query: k < prefix_start or prefix_start <= k <= prefix_position
+ *   an audio query:   k < prefix_start, prefix_start <= k <= prefix_position
+ *                     unless mode 1, or audio_start <= k <= audio_position
+ * masks[i] describes slot i; write the step's K/V rows first (e.g. with
+ * kvrt_write_positions_async). Requires 0 <= prefix_start <= prefix_position
+ * < audio_start <= audio_position < length(slot, layer), mode <= 2, a finite
+ * gate and visible_prefix_count > 0 in mode 2 (KVRT_EINVAL / KVRT_ESTATE
+ * otherwise). Scores, softmax and accumulation in fp32, out bf16 (RNE).
+ * Replaces build_joint_mask_kernel / build_audio_only_mask_kernel and their
+ * launchers (native/qwen_talker/qwen_talker_kernels.cu:296-347, :759-807)
+ * with the repeat_kv + masked SDPA they feed (qwen_talker.cu:718-756,
+ * qwen_talker_aten_attention.cpp:150-160). */
+int kvrt_attend_talker_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                             const kvrt_tensor *q, const kvrt_tensor *out, float scale,
+                             const kvrt_talker_mask *masks);
 
 /* ---- context-free tensor kernels ------------------------------------------ */
 /* Decode attention over caller-owned HF-shaped K/V: k, v [n, kv_heads, Lmax, D]

@@ -30,6 +30,9 @@ tree; HF = transformers.cache_utils, a third-party dependency pinned at
   cache ``base - W + 1`` (gemma4_listener_cache.cu:448-452).
 * window range — gemma4_q4_range_from_position
   (gemma4_listener_kernels.cuh:23-49).
+* talker masks — build_joint_mask_kernel / build_audio_only_mask_kernel
+  (native/qwen_talker/qwen_talker_kernels.cu:296-347, launchers :759-807):
+  ``talker_mask`` and ``attend_masked``.
 * int8 KV (no reference implementation; closed form): per (token, head)
   scale = amax / 127 (fp32), q = clamp(round_half_even(x / scale), -127, 127),
   dequant = q * scale (fp32); amax == 0 gives scale 0 and q = 0.
@@ -154,6 +157,78 @@ def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_positions: np.ndarray,
             p = np.exp(row)
             p /= p.sum()
             out[h, i] = p @ v[kh]
+    return out.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# talker masks (JOINT Q = 2 and audio-only Q = 1)
+# ---------------------------------------------------------------------------
+
+MASKED_BF16 = float(bf16_bits_to_f32(np.array([0xFF7F], dtype=np.uint16))[0])  # -3.3895313892515355e38
+
+
+def talker_gate(mode: int, visible_prefix_count: int, prefix_log_gate: float) -> float:
+    """Additive value of a gated prefix key: fp32 ``gate - logf(count)`` stored
+    as bf16 (qwen_talker_kernels.cu:774-777 computes it, :318-320 / :344-346
+    write it through ``__float2bfloat16``); 0 outside mode 2."""
+    if mode != 2:
+        return 0.0
+    logc = np.float32(np.log(float(visible_prefix_count)))  # correctly rounded logf
+    g = np.float32(np.float32(prefix_log_gate) - logc)
+    return float(round_bf16(np.array([g], dtype=np.float32))[0])
+
+
+def talker_mask(rows: int, key_len: int, prefix_start: int, audio_start: int, prefix_position: int,
+                audio_position: int, mode: int, visible_prefix_count: int = 0,
+                prefix_log_gate: float = -8.0) -> np.ndarray:
+    """Additive mask [rows, key_len] (float32 holding bf16 values).
+
+    rows = 2 restates build_joint_mask_kernel (native/qwen_talker/
+    qwen_talker_kernels.cu:296-321: row 0 the prefix query, row 1 the audio
+    query); rows = 1 restates build_audio_only_mask_kernel (:323-347, with
+    prefix_position = visible_prefix_position). Per key position p:
+    stable = p < prefix_start; visible_prefix = prefix_start <= p <=
+    prefix_position; audio = audio_start <= p <= audio_position; allowed =
+    stable or (visible_prefix and (prefix row or mode != 1)) or (audio row and
+    audio); value 0 if allowed else bf16 finfo.min, replaced by the gate for
+    an audio row on a visible-prefix key in mode 2.
+    """
+    if rows not in (1, 2):
+        raise ValueError("talker masks have 1 (audio-only) or 2 (joint) query rows")
+    p = np.arange(key_len)
+    stable = p < prefix_start
+    vis_prefix = (p >= prefix_start) & (p <= prefix_position)
+    audio = (p >= audio_start) & (p <= audio_position)
+    gate = talker_gate(mode, visible_prefix_count, prefix_log_gate)
+    out = np.empty((rows, key_len), dtype=np.float32)
+    for r in range(rows):
+        audio_row = rows == 1 or r == 1
+        allowed = stable | (vis_prefix & (not audio_row or mode != 1)) | (audio & audio_row)
+        val = np.where(allowed, np.float32(0.0), np.float32(MASKED_BF16))
+        if audio_row and mode == 2:
+            val = np.where(vis_prefix, np.float32(gate), val)
+        out[r] = val
+    return out
+
+
+def attend_masked(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarray, scale: float) -> np.ndarray:
+    """softmax(q.k * scale + mask) v per q head, float64; GQA by repeat_kv.
+
+    q [Hq, Q, D]; k, v [Hkv, L, D]; mask [Q, L] additive (broadcast over
+    heads), as the talker's masked SDPA (qwen_talker_aten_attention.cpp:150-160).
+    Returns float32 [Hq, Q, D].
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    hq, qn, _ = q.shape
+    g = hq // k.shape[0]
+    out = np.zeros(q.shape, dtype=np.float64)
+    for h in range(hq):
+        s = (q[h] @ k[h // g].T) * float(scale) + np.asarray(mask, dtype=np.float64)
+        s = s - s.max(axis=1, keepdims=True)
+        w = np.exp(s)
+        out[h] = (w / w.sum(axis=1, keepdims=True)) @ v[h // g]
     return out.astype(np.float32)
 
 

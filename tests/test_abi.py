@@ -49,7 +49,7 @@ def test_version_capabilities_and_error_strings():
     assert lib.kvrt_abi_version() == 1
     caps = lib.kvrt_capabilities()
     for bit in (L.CAP_CONTIG, L.CAP_RING, L.CAP_PAGED, L.CAP_INT8, L.CAP_FUSED_APPEND_ATTEND, L.CAP_GATHER,
-                L.CAP_DEVICE_LENGTHS, L.CAP_TENSOR_ATTEND):
+                L.CAP_DEVICE_LENGTHS, L.CAP_TENSOR_ATTEND, L.CAP_PREFILL_MFMA, L.CAP_TALKER_MASK):
         assert caps & bit
     assert L.strerror(0) == "ok"
     for code in range(-1, -7, -1):
@@ -75,10 +75,14 @@ int main(void) {
   F(kvrt_counters, attended_keys); F(kvrt_counters, attended_bytes); F(kvrt_counters, gathered_bytes);
   F(kvrt_counters, truncations); F(kvrt_counters, truncated_rows); F(kvrt_counters, pages_in_use);
   F(kvrt_counters, pages_evicted);
+  F(kvrt_talker_mask, prefix_start); F(kvrt_talker_mask, audio_start); F(kvrt_talker_mask, prefix_position);
+  F(kvrt_talker_mask, audio_position); F(kvrt_talker_mask, prefix_attention_mode);
+  F(kvrt_talker_mask, visible_prefix_count); F(kvrt_talker_mask, prefix_log_gate);
   printf("\"sizeof.kvrt_tensor\": [%zu, 0], \"sizeof.kvrt_layer_spec\": [%zu, 0], \"sizeof.kvrt_config\": [%zu, 0],"
-         " \"sizeof.kvrt_storage\": [%zu, 0], \"sizeof.kvrt_counters\": [%zu, 0]\n}\n",
+         " \"sizeof.kvrt_storage\": [%zu, 0], \"sizeof.kvrt_counters\": [%zu, 0],"
+         " \"sizeof.kvrt_talker_mask\": [%zu, 0]\n}\n",
          sizeof(kvrt_tensor), sizeof(kvrt_layer_spec), sizeof(kvrt_config), sizeof(kvrt_storage),
-         sizeof(kvrt_counters));
+         sizeof(kvrt_counters), sizeof(kvrt_talker_mask));
   return 0;
 }
 """
@@ -95,7 +99,7 @@ def test_ctypes_structs_match_the_c_header_layout(tmp_path):
     subprocess.run([gcc, "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
     layout = json.loads(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
     structs = {"kvrt_tensor": L.KvrtTensor, "kvrt_layer_spec": L.KvrtLayerSpec, "kvrt_config": L.KvrtConfig,
-               "kvrt_storage": L.KvrtStorage, "kvrt_counters": L.KvrtCounters}
+               "kvrt_storage": L.KvrtStorage, "kvrt_counters": L.KvrtCounters, "kvrt_talker_mask": L.KvrtTalkerMask}
     for key, (off, size) in layout.items():
         sname, field = key.split(".")
         if sname == "sizeof":
@@ -164,6 +168,7 @@ def test_null_context_calls_fail_with_einval():
     assert lib.kvrt_health(None) == L.KVRT_EINVAL
     assert lib.kvrt_destroy(None) == L.KVRT_EINVAL
     assert lib.kvrt_attend_tensors_async(None, None, None, None, None, 1.0, 0, None) == L.KVRT_EINVAL
+    assert lib.kvrt_attend_talker_async(None, 0, 1, slots, None, None, 1.0, None) == L.KVRT_EINVAL
 
 
 def test_runtime_refuses_to_start_without_a_gpu():

@@ -255,3 +255,27 @@ def test_audio_q1_counter_advances_then_fails_closed():
         advance_audio_q1_position(pos, limit)
     with pytest.raises(RuntimeError):
         advance_audio_q1_position(-1, 5)
+
+
+@pytest.mark.parametrize("kwargs,ok", [
+    (dict(prefix_attention_mode=3), False),                                   # native_qwen_talker.py:1211
+    (dict(prefix_log_gate=float("inf")), False),
+    (dict(prefix_attention_mode=2, visible_prefix_count=0), False),           # :1213
+    (dict(prefix_attention_mode=2, visible_prefix_count=3), True),
+    (dict(prefix_position=8), False),                                         # inside the audio region
+    (dict(prefix_position=1), False),                                         # before the prefix start
+    (dict(audio_position=7), False),
+    (dict(), True),
+])
+def test_talker_mask_validation(kwargs, ok):
+    from kvrt import TalkerMask
+
+    args = dict(prefix_start=2, audio_start=8, prefix_position=4, audio_position=10)
+    args.update(kwargs)
+    if ok:
+        c = TalkerMask(**args).to_c()
+        assert (c.prefix_start, c.audio_start, c.prefix_position, c.audio_position) == (
+            args["prefix_start"], args["audio_start"], args["prefix_position"], args["audio_position"])
+    else:
+        with pytest.raises(ValueError):
+            TalkerMask(**args)

@@ -161,6 +161,38 @@ struct SetLenArgs {
     int32_t val[kPtUpdates];
 };
 
+// Static description of one layer, kept in device memory by the context
+// (uploaded at create and when a RoPE table is set); read by the
+// slot-lifecycle kernels, which may span every layer of a context.
+struct LayerDesc {
+    KVView kv;
+    int32_t head_dim;
+    int32_t dtype;
+    float rope_scaling;
+    int32_t rope_pairs;       // entries of inv_freq (head_dim / 2), 0 = keys not rotated
+    const float *inv_freq;    // device [head_dim / 2] or null
+};
+
+constexpr int kMaxMoveLayers = 64;   // layer entries per slot-move launch
+constexpr int kMaxRebaseRows = 128;  // rows one rebase workgroup holds in registers
+
+// Row moves between slots (and contexts) of identically shaped layers:
+// entry e moves rows[e] positions of every kv head of layer[e] from
+// (src_slot, src_pos0[e] + r) to (dst_slot, dst_pos0[e] + r).
+struct SlotMoveArgs {
+    const LayerDesc *src;     // device table of the source context
+    const LayerDesc *dst;     // device table of the destination context
+    int32_t *err;
+    int32_t src_slot;
+    int32_t dst_slot;
+    int32_t n_entries;
+    int32_t rope_delta;       // rebase: moved keys rotate by this many positions
+    int32_t layer[kMaxMoveLayers];
+    int32_t src_pos0[kMaxMoveLayers];
+    int32_t dst_pos0[kMaxMoveLayers];
+    int32_t rows[kMaxMoveLayers];
+};
+
 struct CopyRowsArgs {
     const uint8_t *src;
     uint8_t *dst;
@@ -185,6 +217,11 @@ hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
 hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,
                             hipStream_t s);
 hipError_t launch_copy_rows(const CopyRowsArgs &a, hipStream_t s);
+// Copy between two slots (any layout, bf16 or int8 with scales); ranges must not overlap.
+hipError_t launch_slot_copy(const SlotMoveArgs &a, int64_t max_units, hipStream_t s);
+// In-place move of <= kMaxRebaseRows rows per entry within one slot, keys
+// rotated by rope_delta positions where the layer has a RoPE table (bf16).
+hipError_t launch_slot_rebase(const SlotMoveArgs &a, int max_heads, hipStream_t s);
 hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s);
 
 // Smallest instantiated row tile >= rows (1, 2, 4, 8, 16); 0 if too large.

@@ -9,7 +9,7 @@
 //   merge_kernel    log-sum-exp merge of the partials in fixed order
 //                   (deterministic) -> bf16, then the fused length advance
 //   set_i32_kernel  length / page-table edits carried in the kernarg block
-//   copy_rows_kernel, zero_kernel
+//   copy_rows_kernel, zero_kernel, slot_copy_kernel, slot_rebase_kernel
 //
 // Every memory-bound loop moves 16 B per lane with consecutive lanes on
 // consecutive addresses (one 1 KiB transaction per wave instruction).
@@ -779,6 +779,143 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyRowsArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// slot lifecycle: clone / cross-context copy / rollover rebase
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t row_offset_any(const KVView &v, int slot, int head, int pos, int D) {
+    if (v.layout == KVRT_LAYOUT_CONTIG) return row_offset<KVRT_LAYOUT_CONTIG>(v, slot, head, pos, D);
+    if (v.layout == KVRT_LAYOUT_RING) return row_offset<KVRT_LAYOUT_RING>(v, slot, head, pos, D);
+    return row_offset<KVRT_LAYOUT_PAGED>(v, slot, head, pos, D);
+}
+
+// grid (chunks, n_entries), 256 threads: every thread step copies 16 B of K
+// and of V of one (head, row); int8 layers also copy the row's two scales.
+// Source and destination rows must not overlap (different slots).
+__global__ __launch_bounds__(256) void slot_copy_kernel(SlotMoveArgs a) {
+    const int e = blockIdx.y;
+    const LayerDesc S = a.src[a.layer[e]];
+    const LayerDesc T = a.dst[a.layer[e]];
+    const int D = S.head_dim;
+    const int eb = S.dtype == KVRT_INT8 ? 1 : 2;
+    const int units = D * eb / 16;
+    const int rows = a.rows[e];
+    const int64_t total = (int64_t)S.kv.kv_heads * rows * units;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int u = (int)(i % units);
+        const int64_t t = i / units;
+        const int r = (int)(t % rows);
+        const int h = (int)(t / rows);
+        const int64_t so = row_offset_any(S.kv, a.src_slot, h, a.src_pos0[e] + r, D);
+        const int64_t to = row_offset_any(T.kv, a.dst_slot, h, a.dst_pos0[e] + r, D);
+        if (so < 0 || to < 0) {
+            a.err[0] = 1;
+            continue;
+        }
+        const int64_t sb = so * eb + u * 16, tb = to * eb + u * 16;
+        const uint4 kx = *reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(S.kv.k) + sb);
+        const uint4 vx = *reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(S.kv.v) + sb);
+        *reinterpret_cast<uint4 *>(static_cast<uint8_t *>(T.kv.k) + tb) = kx;
+        *reinterpret_cast<uint4 *>(static_cast<uint8_t *>(T.kv.v) + tb) = vx;
+        if (eb == 1 && u == 0) {
+            T.kv.ks[to / D] = S.kv.ks[so / D];
+            T.kv.vs[to / D] = S.kv.vs[so / D];
+        }
+    }
+}
+
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
+
+// grid (n_entries, max kv heads), 1024 threads: workgroup (e, h) moves the
+// rows[e] <= kMaxRebaseRows rows of kv head h of layer[e] from src_pos0 to
+// dst_pos0 within src_slot (bf16 layers). Every thread loads its units (row,
+// 8-pair segment: dims [8g, 8g+8) and [D/2 + 8g, D/2 + 8g + 8)) of K and V,
+// waits for them, and the workgroup synchronises before the first store, so
+// overlapping ranges move correctly. Keys of layers with a RoPE table rotate
+// by rope_delta positions: per pair i, with f = fp32(delta * inv_freq[i]),
+// c = bf16(cos(f) * scaling), s = bf16(sin(f) * scaling) (cos / sin of the
+// fp32 argument rounded from double), x1' = bf16(bf16(x1 c) - bf16(x2 s)),
+// x2' = bf16(bf16(x2 c) + bf16(x1 s)).
+__global__ __launch_bounds__(1024) void slot_rebase_kernel(SlotMoveArgs a) {
+    constexpr int kPer = 4;  // units per thread: 128 rows x 32 segments (D = 512) / 1024
+    __shared__ float2 cs[256];
+    const int e = blockIdx.x, h = blockIdx.y;
+    const LayerDesc L = a.src[a.layer[e]];
+    if (h >= L.kv.kv_heads) return;  // the whole workgroup leaves together
+    const int D = L.head_dim, half = D / 2;
+    const bool rope = L.inv_freq != nullptr;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        float c = 1.f, sn = 0.f;
+        if (rope) {
+            const float f = (float)a.rope_delta * L.inv_freq[i];
+            c = bf16_round((float)cos((double)f) * L.rope_scaling);
+            sn = bf16_round((float)sin((double)f) * L.rope_scaling);
+        }
+        cs[i] = make_float2(c, sn);
+    }
+    const int segs = half / 8;
+    const int units = a.rows[e] * segs;
+    uint4 k1[kPer], k2[kPer], v1[kPer], v2[kPer];
+    int64_t dst[kPer];
+    int seg[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int idx = threadIdx.x + j * (int)blockDim.x;
+        const bool ok = idx < units;
+        const int r = ok ? idx / segs : 0;
+        seg[j] = ok ? idx % segs : 0;
+        const int64_t so = ok ? row_offset_any(L.kv, a.src_slot, h, a.src_pos0[e] + r, D) : -1;
+        const int64_t to = ok ? row_offset_any(L.kv, a.src_slot, h, a.dst_pos0[e] + r, D) : -1;
+        if (ok && (so < 0 || to < 0)) a.err[0] = 1;
+        dst[j] = (so >= 0 && to >= 0) ? to + 8 * seg[j] : -1;
+        k1[j] = k2[j] = v1[j] = v2[j] = make_uint4(0, 0, 0, 0);
+        if (dst[j] >= 0) {
+            const uint16_t *kp = static_cast<const uint16_t *>(L.kv.k) + so + 8 * seg[j];
+            const uint16_t *vp = static_cast<const uint16_t *>(L.kv.v) + so + 8 * seg[j];
+            k1[j] = *reinterpret_cast<const uint4 *>(kp);
+            k2[j] = *reinterpret_cast<const uint4 *>(kp + half);
+            v1[j] = *reinterpret_cast<const uint4 *>(vp);
+            v2[j] = *reinterpret_cast<const uint4 *>(vp + half);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every load of this thread has returned
+    __syncthreads();                // ... and of every thread of the workgroup
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        if (dst[j] < 0) continue;
+        uint4 n1 = k1[j], n2 = k2[j];
+        if (rope) {
+            const uint32_t a1[4] = {k1[j].x, k1[j].y, k1[j].z, k1[j].w};
+            const uint32_t a2[4] = {k2[j].x, k2[j].y, k2[j].z, k2[j].w};
+            uint32_t o1[4], o2[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t lo1 = 0, lo2 = 0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const float x1 = hh ? bf16_hi(a1[w]) : bf16_lo(a1[w]);
+                    const float x2 = hh ? bf16_hi(a2[w]) : bf16_lo(a2[w]);
+                    const float2 t = cs[8 * seg[j] + 2 * w + hh];
+                    const float y1 = bf16_round(x1 * t.x) - bf16_round(x2 * t.y);
+                    const float y2 = bf16_round(x2 * t.x) + bf16_round(x1 * t.y);
+                    lo1 |= (uint32_t)f32_to_bf16(y1) << (16 * hh);
+                    lo2 |= (uint32_t)f32_to_bf16(y2) << (16 * hh);
+                }
+                o1[w] = lo1;
+                o2[w] = lo2;
+            }
+            n1 = make_uint4(o1[0], o1[1], o1[2], o1[3]);
+            n2 = make_uint4(o2[0], o2[1], o2[2], o2[3]);
+        }
+        uint16_t *kp = static_cast<uint16_t *>(L.kv.k) + dst[j];
+        uint16_t *vp = static_cast<uint16_t *>(L.kv.v) + dst[j];
+        *reinterpret_cast<uint4 *>(kp) = n1;
+        *reinterpret_cast<uint4 *>(kp + half) = n2;
+        *reinterpret_cast<uint4 *>(vp) = v1[j];
+        *reinterpret_cast<uint4 *>(vp + half) = v2[j];
+    }
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
          i += (uint64_t)gridDim.x * blockDim.x)
@@ -943,6 +1080,22 @@ hipError_t launch_copy_rows(const CopyRowsArgs &a, hipStream_t s) {
     int64_t g = (total + 255) / 256;
     if (g > 8192) g = 8192;
     hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)g), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_slot_copy(const SlotMoveArgs &a, int64_t max_units, hipStream_t s) {
+    if (a.n_entries <= 0 || max_units <= 0) return hipSuccess;
+    if (a.n_entries > kMaxMoveLayers) return hipErrorInvalidValue;
+    int64_t g = (max_units + 255) / 256;
+    if (g > 2048) g = 2048;
+    hipLaunchKernelGGL(slot_copy_kernel, dim3((unsigned)g, a.n_entries), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_slot_rebase(const SlotMoveArgs &a, int max_heads, hipStream_t s) {
+    if (a.n_entries <= 0) return hipSuccess;
+    if (a.n_entries > kMaxMoveLayers || max_heads <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(slot_rebase_kernel, dim3(a.n_entries, max_heads), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 

@@ -29,6 +29,8 @@ struct Layer {
     float *ks = nullptr, *vs = nullptr;
     bool owned = false;
     uint64_t kv_bytes = 0, scale_bytes = 0;
+    float *inv_freq = nullptr;  // device RoPE table [head_dim / 2] (kvrt_set_layer_rope)
+    float rope_scaling = 1.f;
 };
 
 bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -73,6 +75,7 @@ struct kvrt_ctx {
     float *ws = nullptr;
     size_t ws_bytes = 0;
     std::vector<float *> retired_ws;  // kept until destroy: captured graphs may reference them
+    LayerDesc *d_desc = nullptr;      // device [n_layers] layer descriptions
     kvrt_counters counters{};
 
     int len_at(int slot, int layer) const { return len[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
@@ -132,6 +135,25 @@ KVView make_view(kvrt_ctx *c, int layer) {
     v.head_stride = (int64_t)v.rows * s.head_dim;
     v.slot_stride = v.head_stride * s.kv_heads;
     return v;
+}
+
+// Upload the device layer descriptions (views, head dims, RoPE tables).
+int upload_desc(kvrt_ctx *c) {
+    std::vector<LayerDesc> h(c->cfg.n_layers);
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        const Layer &L = c->layers[c->layers[l].owner];
+        h[l].kv = make_view(c, l);
+        h[l].head_dim = L.spec.head_dim;
+        h[l].dtype = L.spec.dtype;
+        h[l].rope_scaling = L.rope_scaling;
+        h[l].rope_pairs = L.inv_freq ? L.spec.head_dim / 2 : 0;
+        h[l].inv_freq = L.inv_freq;
+    }
+    if (!c->d_desc && hipMalloc((void **)&c->d_desc, h.size() * sizeof(LayerDesc)) != hipSuccess)
+        return KVRT_EDEVICE;
+    if (hipMemcpy(c->d_desc, h.data(), h.size() * sizeof(LayerDesc), hipMemcpyHostToDevice) != hipSuccess)
+        return KVRT_EDEVICE;
+    return KVRT_OK;
 }
 
 Lengths make_len(kvrt_ctx *c, int layer) {
@@ -436,6 +458,7 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     }
     c->ws_bytes = 0;
     if (ensure_workspace(c, workspace_bound(c)) != KVRT_OK) return fail(KVRT_EDEVICE);
+    if (upload_desc(c) != KVRT_OK) return fail(KVRT_EDEVICE);
     if (hipDeviceSynchronize() != hipSuccess) return fail(KVRT_EDEVICE);
     *out = c;
     return KVRT_OK;
@@ -737,6 +760,9 @@ int kvrt_destroy(kvrt_ctx *c) {
         if (L.ks) (void)hipFree(L.ks);
         if (L.vs) (void)hipFree(L.vs);
     }
+    for (Layer &L : c->layers)
+        if (L.inv_freq) (void)hipFree(L.inv_freq);
+    if (c->d_desc) (void)hipFree(c->d_desc);
     if (c->d_len) (void)hipFree(c->d_len);
     if (c->d_err) (void)hipFree(c->d_err);
     if (c->d_pt) (void)hipFree(c->d_pt);
@@ -1040,44 +1066,210 @@ int kvrt_evict(kvrt_ctx *c, int32_t slot, int32_t keep_from) {
     return KVRT_OK;
 }
 
+namespace {
+
+// Positions [lo, n) of (slot, layer) that a copy of the first n tokens
+// carries: CONTIG all of them, RING those still in the ring, PAGED those on
+// live pages. KVRT_ESTATE when a key the next query (position n) can see is
+// not resident.
+int copy_range(const kvrt_ctx *c, int slot, int l, int n, int &lo) {
+    const kvrt_layer_spec &s = c->layers[l].spec;
+    const int L = c->len_at(slot, l);
+    if (n > L) return KVRT_ESTATE;
+    const int need = s.window > 0 ? std::max(0, n - s.window + 1) : 0;
+    lo = 0;
+    if (s.layout == KVRT_LAYOUT_RING) lo = std::max(0, std::max(n - s.ring_rows, L - s.ring_rows));
+    else if (s.layout == KVRT_LAYOUT_PAGED) lo = std::min(n, c->first_live[slot] * c->cfg.block_size);
+    return lo > need ? KVRT_ESTATE : KVRT_OK;
+}
+
+bool same_topology(const kvrt_ctx *a, const kvrt_ctx *b) {
+    if (a->cfg.n_layers != b->cfg.n_layers || a->device != b->device) return false;
+    if (a->paged != b->paged || (a->paged && a->cfg.block_size != b->cfg.block_size)) return false;
+    for (int l = 0; l < a->cfg.n_layers; ++l) {
+        const kvrt_layer_spec &x = a->layers[l].spec, &y = b->layers[l].spec;
+        if (x.layout != y.layout || x.dtype != y.dtype || x.kv_heads != y.kv_heads || x.head_dim != y.head_dim ||
+            x.window != y.window || x.ring_rows != y.ring_rows || a->layers[l].owner != b->layers[l].owner)
+            return false;
+    }
+    return true;
+}
+
+// Copy the first n tokens of every owned layer of (src, src_slot) into
+// (dst, dst_slot), on dst's stream; dst lengths become n.
+int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int n) {
+    const int nl = src->cfg.n_layers;
+    std::vector<int> lo(nl, 0);
+    int page_lo = n;
+    for (int l = 0; l < nl; ++l) {
+        if (src->layers[l].owner != l) continue;
+        const kvrt_layer_spec &s = src->layers[l].spec;
+        if (s.layout == KVRT_LAYOUT_CONTIG && n > dst->cfg.capacity) return KVRT_ESTATE;
+        const int rc = copy_range(src, src_slot, l, n, lo[l]);
+        if (rc != KVRT_OK) return rc;
+        if (s.layout == KVRT_LAYOUT_PAGED) page_lo = std::min(page_lo, lo[l]);
+    }
+    // destination pages: release what the slot holds (host bookkeeping only:
+    // the device table is read only inside mapped, live ranges), then map the
+    // copied range; only the new mappings are enqueued, each index once
+    std::vector<int32_t> pidx, pval;
+    if (dst->paged) {
+        const int bs = dst->cfg.block_size;
+        const int need = n > 0 ? (n - 1) / bs - page_lo / bs + 1 : 0;
+        if ((n - 1) / bs >= dst->pt_stride) return KVRT_ESTATE;
+        int held = 0;
+        for (int p = 0; p < dst->pt_stride; ++p) held += dst->pt[(size_t)dst_slot * dst->pt_stride + p] >= 0;
+        if (need > (int)dst->free_pages.size() + held) return KVRT_ENOMEM;  // nothing changed
+        for (int p = 0; p < dst->pt_stride; ++p) {
+            int32_t &e = dst->pt[(size_t)dst_slot * dst->pt_stride + p];
+            if (e >= 0) {
+                dst->free_pages.push_back(e);
+                e = -1;
+                dst->counters.pages_in_use--;
+            }
+        }
+        const int from = (page_lo / bs) * bs;
+        if (map_pages(dst, dst_slot, from, n, pidx, pval) != KVRT_OK) return poison(dst);  // counted above
+        dst->first_live[dst_slot] = from / bs;
+    }
+    int rc = enqueue_pages(dst, pidx, pval);
+    if (rc != KVRT_OK) return rc;
+    SlotMoveArgs a{};
+    a.src = src->d_desc;
+    a.dst = dst->d_desc;
+    a.err = dst->d_err;
+    a.src_slot = src_slot;
+    a.dst_slot = dst_slot;
+    int64_t max_units = 0;
+    uint64_t bytes = 0;
+    auto flush = [&]() -> int {
+        if (a.n_entries == 0) return KVRT_OK;
+        dst->counters.launches++;
+        if (launch_slot_copy(a, max_units, dst->stream) != hipSuccess) return poison(dst);
+        a.n_entries = 0;
+        max_units = 0;
+        return KVRT_OK;
+    };
+    std::vector<int32_t> idx;
+    for (int l = 0; l < nl; ++l) {
+        if (src->layers[l].owner != l) continue;
+        const kvrt_layer_spec &s = src->layers[l].spec;
+        const int rows = n - lo[l];
+        if (rows > 0) {
+            const int e = a.n_entries++;
+            a.layer[e] = l;
+            a.src_pos0[e] = a.dst_pos0[e] = lo[l];
+            a.rows[e] = rows;
+            const int eb = s.dtype == KVRT_INT8 ? 1 : 2;
+            max_units = std::max<int64_t>(max_units, (int64_t)s.kv_heads * rows * (s.head_dim * eb / 16));
+            bytes += (uint64_t)rows * s.kv_heads * (s.head_dim * eb + (eb == 1 ? 8 : 0)) * 2;
+            if (a.n_entries == kMaxMoveLayers && (rc = flush()) != KVRT_OK) return rc;
+        }
+        dst->len_ref(dst_slot, l) = n;
+        idx.push_back((int32_t)((size_t)dst_slot * nl + l));
+    }
+    if ((rc = flush()) != KVRT_OK) return rc;
+    dst->counters.gathered_bytes += bytes;
+    return set_device_lens(dst, idx);
+}
+
+}  // namespace
+
 int kvrt_copy_prefix_async(kvrt_ctx *c, int32_t src_slot, int32_t dst_slot, int32_t n_tokens) {
     int rc = begin(c);
     if (rc) return rc;
     if (!valid_slot(c, src_slot) || !valid_slot(c, dst_slot) || src_slot == dst_slot || n_tokens < 0)
         return KVRT_EINVAL;
+    return copy_slot_impl(c, dst_slot, c, src_slot, n_tokens);
+}
+
+int kvrt_copy_session_async(kvrt_ctx *dst, int32_t dst_slot, kvrt_ctx *src, int32_t src_slot, int32_t n_tokens) {
+    if (!dst || !src || dst == src) return KVRT_EINVAL;
+    if (src->poisoned) return KVRT_EPOISONED;
+    int rc = begin(dst);
+    if (rc) return rc;
+    if (!valid_slot(dst, dst_slot) || !valid_slot(src, src_slot) || n_tokens < 0) return KVRT_EINVAL;
+    if (!same_topology(dst, src)) return KVRT_EINVAL;
+    return copy_slot_impl(dst, dst_slot, src, src_slot, n_tokens);
+}
+
+int kvrt_set_layer_rope(kvrt_ctx *c, int32_t layer, const float *inv_freq, int32_t n_freq, float scaling) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || c->layers[layer].owner != layer) return KVRT_EINVAL;
+    Layer &L = c->layers[layer];
+    if (L.spec.dtype != KVRT_BF16 || !std::isfinite(scaling)) return KVRT_EINVAL;
+    if (inv_freq == nullptr) {
+        if (n_freq != 0) return KVRT_EINVAL;
+    } else {
+        if (n_freq != L.spec.head_dim / 2) return KVRT_EINVAL;
+        for (int i = 0; i < n_freq; ++i)
+            if (!std::isfinite(inv_freq[i])) return KVRT_EINVAL;
+    }
+    // pending work may read the current table
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    if (inv_freq == nullptr) {
+        if (L.inv_freq) (void)hipFree(L.inv_freq);
+        L.inv_freq = nullptr;
+    } else {
+        if (!L.inv_freq && hipMalloc((void **)&L.inv_freq, (size_t)n_freq * sizeof(float)) != hipSuccess)
+            return poison(c);
+        if (hipMemcpy(L.inv_freq, inv_freq, (size_t)n_freq * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return poison(c);
+    }
+    L.rope_scaling = scaling;
+    return upload_desc(c) == KVRT_OK ? KVRT_OK : poison(c);
+}
+
+int kvrt_rollover_async(kvrt_ctx *c, int32_t slot, int32_t prefix_len, int32_t retained_rows) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, slot) || prefix_len <= 0 || retained_rows <= 0 || retained_rows > KVRT_MAX_ROLLOVER_ROWS)
+        return KVRT_EINVAL;
+    int L = -1, max_heads = 0;
     for (int l = 0; l < c->cfg.n_layers; ++l) {
         if (c->layers[l].owner != l) continue;
         const kvrt_layer_spec &s = c->layers[l].spec;
-        if (s.layout == KVRT_LAYOUT_PAGED) return KVRT_EINVAL;
-        const int L = c->len_at(src_slot, l);
-        if (n_tokens > L) return KVRT_ESTATE;
-        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && n_tokens - s.window + 1 < L - s.ring_rows)
-            return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING || s.dtype != KVRT_BF16) return KVRT_EINVAL;
+        const int Ll = c->len_at(slot, l);
+        if (L >= 0 && Ll != L) return KVRT_ESTATE;
+        L = Ll;
+        max_heads = std::max(max_heads, s.kv_heads);
     }
+    if (L < 0) return KVRT_EINVAL;
+    if ((int64_t)L <= (int64_t)prefix_len + retained_rows) return KVRT_ESTATE;
+    if (c->paged && c->first_live[slot] > 0) return KVRT_ESTATE;  // the prefix pages are gone
+    SlotMoveArgs a{};
+    a.src = a.dst = c->d_desc;
+    a.err = c->d_err;
+    a.src_slot = a.dst_slot = slot;
+    a.rope_delta = prefix_len - (L - retained_rows);
     std::vector<int32_t> idx;
+    uint64_t bytes = 0;
     for (int l = 0; l < c->cfg.n_layers; ++l) {
         if (c->layers[l].owner != l) continue;
         const kvrt_layer_spec &s = c->layers[l].spec;
-        const KVView vw = make_view(c, l);
-        const int rows = s.layout == KVRT_LAYOUT_RING ? std::min(s.ring_rows, c->len_at(src_slot, l)) : n_tokens;
-        for (int kv = 0; kv < 2; ++kv) {
-            uint8_t *base = static_cast<uint8_t *>(kv == 0 ? vw.k : vw.v);
-            CopyRowsArgs a{};
-            a.src = base + (int64_t)src_slot * vw.slot_stride * 2;
-            a.dst = base + (int64_t)dst_slot * vw.slot_stride * 2;
-            a.d0 = 1;
-            a.d1 = s.kv_heads;
-            a.rows = rows;
-            a.row_bytes = (int64_t)s.head_dim * 2;
-            a.s0 = a.t0 = vw.slot_stride * 2;
-            a.s1 = a.t1 = vw.head_stride * 2;
-            a.sr = a.tr = vw.row_stride * 2;
+        const int e = a.n_entries++;
+        a.layer[e] = l;
+        a.src_pos0[e] = L - retained_rows;
+        a.dst_pos0[e] = prefix_len;
+        a.rows[e] = retained_rows;
+        bytes += (uint64_t)retained_rows * s.kv_heads * s.head_dim * 2 * 2;
+        if (a.n_entries == kMaxMoveLayers) {
             c->counters.launches++;
-            if (launch_copy_rows(a, c->stream) != hipSuccess) return poison(c);
+            if (launch_slot_rebase(a, max_heads, c->stream) != hipSuccess) return poison(c);
+            a.n_entries = 0;
         }
-        c->len_ref(dst_slot, l) = n_tokens;
-        idx.push_back((int32_t)((size_t)dst_slot * c->cfg.n_layers + l));
+        c->len_ref(slot, l) = prefix_len + retained_rows;
+        idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
     }
+    if (a.n_entries) {
+        c->counters.launches++;
+        if (launch_slot_rebase(a, max_heads, c->stream) != hipSuccess) return poison(c);
+    }
+    c->counters.truncations++;
+    c->counters.truncated_rows += (uint64_t)(L - prefix_len - retained_rows) * idx.size();
+    c->counters.gathered_bytes += bytes;
     return set_device_lens(c, idx);
 }
 

@@ -11,6 +11,7 @@ from ctypes import POINTER, c_float, c_int32, c_int64, c_uint32, c_uint64, c_voi
 from ._build import LIB_PATH
 
 KVRT_MAX_RANK = 4
+KVRT_MAX_ROLLOVER_ROWS = 128
 KVRT_MAX_ITEMS = 64
 
 KVRT_OK = 0
@@ -133,6 +134,9 @@ SIGNATURES = [
     ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),
     ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
+    ("kvrt_copy_session_async", c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32]),
+    ("kvrt_set_layer_rope", c_int32, [c_void_p, c_int32, POINTER(c_float), c_int32, c_float]),
+    ("kvrt_rollover_async", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     ("kvrt_attend_decode_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_append_attend_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _T, _T, c_float]),
     ("kvrt_attend_prefill_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),

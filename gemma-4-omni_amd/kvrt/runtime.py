@@ -433,9 +433,34 @@ class KVRuntime:
         _check(self.lib.kvrt_evict(self._ctx, slot, int(keep_from)), "kvrt_evict")
 
     def copy_prefix(self, src_slot: int, dst_slot: int, n_tokens: int) -> None:
+        """Clone the first n_tokens positions of src_slot into dst_slot (all layers, one launch)."""
         self._bind()
         _check(self.lib.kvrt_copy_prefix_async(self._ctx, src_slot, dst_slot, int(n_tokens)),
                "kvrt_copy_prefix_async")
+
+    def copy_session(self, dst_slot: int, src: "KVRuntime", src_slot: int, n_tokens: int) -> None:
+        """Copy the first n_tokens positions of ``src``'s src_slot into dst_slot of this
+        runtime (identical topology), on this runtime's current stream."""
+        self._bind()
+        _check(self.lib.kvrt_copy_session_async(self._ctx, int(dst_slot), src._ctx, int(src_slot), int(n_tokens)),
+               "kvrt_copy_session_async")
+
+    def set_layer_rope(self, layer: int, inv_freq: Sequence[float] | None, scaling: float = 1.0) -> None:
+        """RoPE inverse frequencies (head_dim / 2 fp32 values) of a layer for rollover."""
+        self._bind()
+        if inv_freq is None:
+            _check(self.lib.kvrt_set_layer_rope(self._ctx, layer, None, 0, float(scaling)), "kvrt_set_layer_rope")
+            return
+        vals = [float(x) for x in inv_freq]
+        arr = (ctypes.c_float * max(1, len(vals)))(*vals)
+        _check(self.lib.kvrt_set_layer_rope(self._ctx, layer, arr, len(vals), float(scaling)), "kvrt_set_layer_rope")
+
+    def rollover(self, slot: int, prefix_len: int, retained_rows: int) -> None:
+        """Keep the prefix, move the newest retained_rows rows behind it and
+        rotate their keys by the position shift (layers with a RoPE table)."""
+        self._bind()
+        _check(self.lib.kvrt_rollover_async(self._ctx, int(slot), int(prefix_len), int(retained_rows)),
+               "kvrt_rollover_async")
 
     # ---- state -----------------------------------------------------------------
     def seq_length(self, slot: int, layer: int = 0) -> int:

@@ -46,6 +46,7 @@ extern "C" {
 #define KVRT_MAX_RANK 4
 #define KVRT_MAX_ITEMS 64      /* slots per batched call                 */
 #define KVRT_MAX_POSITIONS 128 /* rows per kvrt_write_positions_async call */
+#define KVRT_MAX_ROLLOVER_ROWS 128 /* rows kept by one kvrt_rollover_async    */
 
 /* ---- return codes ------------------------------------------------------ */
 #define KVRT_OK 0
@@ -245,11 +246,52 @@ int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len);
  * the reference (paged KV is absent there); bounded-memory decode. */
 int kvrt_evict(kvrt_ctx *ctx, int32_t slot, int32_t keep_from);
 
-/* Copy the first n_tokens rows of every non-shared layer from src_slot to
- * dst_slot (CONTIG layers; dst lengths become n_tokens). Replaces
- * copy_static_cache_prefix (duplex_kernel/thinker_cache.py:83-190) and
- * gemma4_cache_copy_async (gemma4_listener_cache.cu:306-345). */
+/* Copy the first n_tokens positions of every non-shared layer from src_slot
+ * to dst_slot in one launch (dst lengths become n_tokens). CONTIG layers copy
+ * all n_tokens rows; RING layers the rows still in the ring; PAGED layers
+ * (bf16 or int8 with scales) the rows on live pages, into freshly mapped
+ * pages of dst_slot (its previous pages are released first). KVRT_ESTATE if
+ * a key the next query would see is no longer resident in src_slot,
+ * KVRT_ENOMEM (nothing changed) if the pool cannot hold the copy.
+ * Replaces copy_static_cache_prefix (duplex_kernel/thinker_cache.py:83-190),
+ * gemma4_cache_copy_async (gemma4_listener_cache.cu:306-345) and the KV part
+ * of gemma4_listener_batch_clone_session_slot_async
+ * (gemma4_listener_microbatch_impl.inc:4046-4119). */
 int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, int32_t n_tokens);
+
+/* The same copy between two contexts of identical topology (layer specs,
+ * aliasing, block size, device), enqueued on dst's stream; work on src's
+ * stream that produced the rows must be ordered before it by the caller.
+ * Replaces the KV part of gemma4_listener_batch_copy_session_cache_async
+ * (gemma4_listener_microbatch_impl.inc:4121-4172). */
+int kvrt_copy_session_async(kvrt_ctx *dst, int32_t dst_slot, kvrt_ctx *src, int32_t src_slot,
+                            int32_t n_tokens);
+
+/* RoPE table of one non-shared bf16 layer for kvrt_rollover_async:
+ * inv_freq[head_dim / 2] (host, fp32; 0 leaves a pair unrotated) and the
+ * cos/sin scaling; inv_freq = NULL with n_freq = 0 removes the table.
+ * Synchronous: waits for the bound stream, then uploads.
+ * Replaces the d_inv_freq_sliding / d_inv_freq_full tables of the listener
+ * (native/gemma4_listener_microbatch/gemma4_listener.cu:1840-1880). */
+int kvrt_set_layer_rope(kvrt_ctx *ctx, int32_t layer, const float *inv_freq, int32_t n_freq, float scaling);
+
+/* Rollover of one slot: every non-shared layer keeps positions
+ * [0, prefix_len) and moves its newest retained_rows rows, positions
+ * [L - retained_rows, L), to [prefix_len, prefix_len + retained_rows) (one
+ * launch, overlapping ranges allowed); keys of layers with a RoPE table are
+ * rotated by delta = prefix_len - (L - retained_rows) positions:
+ *   c = bf16(cos(f) * scaling), s = bf16(sin(f) * scaling), f = fp32(delta * inv_freq[i]),
+ *   x1' = bf16(bf16(x1 c) - bf16(x2 s)), x2' = bf16(bf16(x2 c) + bf16(x1 s))
+ * for the pair (x1, x2) = (dim i, dim i + D/2). Lengths become prefix_len +
+ * retained_rows. Requires CONTIG or PAGED bf16 layers (a RING drops the prefix
+ * rows the next window needs), equal lengths L over the slot's layers,
+ * L > prefix_len + retained_rows, 0 < retained_rows <= KVRT_MAX_ROLLOVER_ROWS
+ * and, for PAGED, no evicted page.
+ * Replaces gemma4_cache_rebase_async (native/gemma4_listener/
+ * gemma4_listener_cache.cu:303-351) and the per-layer kernel_rope_rebase_bf16
+ * launches of gemma4_listener_batch_rollover_async
+ * (gemma4_listener_microbatch_impl.inc:3835-3895). */
+int kvrt_rollover_async(kvrt_ctx *ctx, int32_t slot, int32_t prefix_len, int32_t retained_rows);
 
 /* GQA decode attention over the last Q positions of n slots of one layer:
  * q [n, Hq, Q, D] bf16 contiguous, out [n, Hq, Q, D] bf16 contiguous.

@@ -30,6 +30,10 @@ tree; HF = transformers.cache_utils, a third-party dependency pinned at
   cache ``base - W + 1`` (gemma4_listener_cache.cu:448-452).
 * window range — gemma4_q4_range_from_position
   (gemma4_listener_kernels.cuh:23-49).
+* RoPE rebase — kernel_rope_rebase_bf16 / kernel_rope_bf16
+  (native/gemma4_listener_microbatch/gemma4_listener_kernels.cuh:294-360),
+  rollover compaction gemma4_cache_rebase_async (gemma4_listener_cache.cu:
+  303-351): ``rope_rebase``, ``OracleCache.rollover``.
 * talker masks — build_joint_mask_kernel / build_audio_only_mask_kernel
   (native/qwen_talker/qwen_talker_kernels.cu:296-347, launchers :759-807):
   ``talker_mask`` and ``attend_masked``.
@@ -232,6 +236,56 @@ def attend_masked(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarray,
     return out.astype(np.float32)
 
 
+# ---------------------------------------------------------------------------
+# RoPE (forward and rebase of cached keys)
+# ---------------------------------------------------------------------------
+
+
+def rope_cos_sin(delta_or_pos: float, inv_freq: np.ndarray, scaling: float = 1.0) -> tuple[np.ndarray, np.ndarray]:
+    """bf16 (cos, sin) per pair: f = fp32(p * inv_freq[i]); bf16(fp32(cos f) * scaling).
+
+    Restates the angle step of kernel_rope_bf16 / kernel_rope_rebase_bf16
+    (native/gemma4_listener_microbatch/gemma4_listener_kernels.cuh:294-360)
+    with cos / sin of the fp32 argument correctly rounded to fp32.
+    """
+    f = (np.float32(delta_or_pos) * np.asarray(inv_freq, np.float32)).astype(np.float32)
+    c = np.cos(f.astype(np.float64)).astype(np.float32) * np.float32(scaling)
+    s = np.sin(f.astype(np.float64)).astype(np.float32) * np.float32(scaling)
+    return round_bf16(c.astype(np.float32)), round_bf16(s.astype(np.float32))
+
+
+def rope_rotate(x: np.ndarray, cos_b: np.ndarray, sin_b: np.ndarray) -> np.ndarray:
+    """Rotate the (dim i, dim i + D/2) pairs of bf16 rows x [..., D] with bf16
+    pointwise products and bf16 add / subtract:
+    x1' = bf16(bf16(x1 c) - bf16(x2 s)), x2' = bf16(bf16(x2 c) + bf16(x1 s))
+    (gemma4_listener_kernels.cuh:323-330, :350-359)."""
+    x = np.asarray(x, np.float32)
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    x1c, x2s = round_bf16(x1 * cos_b), round_bf16(x2 * sin_b)
+    x2c, x1s = round_bf16(x2 * cos_b), round_bf16(x1 * sin_b)
+    return np.concatenate([round_bf16((x1c - x2s).astype(np.float32)),
+                           round_bf16((x2c + x1s).astype(np.float32))], axis=-1)
+
+
+def rope_rebase(x: np.ndarray, inv_freq: np.ndarray, delta: int, scaling: float = 1.0) -> np.ndarray:
+    """kernel_rope_rebase_bf16: rotate already-rotated keys by delta positions."""
+    c, s = rope_cos_sin(delta, inv_freq, scaling)
+    return rope_rotate(x, c, s)
+
+
+def gemma_inv_freq(head_dim: int, base: float, rotary_pairs: int | None = None) -> np.ndarray:
+    """fp32 inverse frequencies 1 / base^(2i / D), zero beyond rotary_pairs
+    (gemma4_listener.cu:1840-1880: sliding D 256 all 128 pairs; full D 512
+    proportional RoPE with 64 rotated pairs)."""
+    half = head_dim // 2
+    pairs = half if rotary_pairs is None else rotary_pairs
+    i = np.arange(half)
+    out = (1.0 / np.power(np.float64(base), (2.0 * i) / head_dim)).astype(np.float32)
+    out[pairs:] = 0.0
+    return out
+
+
 def attend_bruteforce(q, k, v, q_positions, scale, window=0):
     """Pure-Python-loop attention (tiny shapes only): golden-vector generator."""
     hq, qn, d = len(q), len(q[0]), len(q[0][0])
@@ -333,6 +387,37 @@ class OracleCache:
     def truncate(self, slot: int, layer: int, keep_len: int) -> None:
         for r in self._get(slot, layer):
             r.truncate(keep_len)
+
+    def copy_prefix(self, src: int, dst: int, layer: int, n: int) -> None:
+        """dst's rows of a layer become the first n rows of src's
+        (gemma4_cache_copy_async, gemma4_listener_cache.cu:306-345)."""
+        for a, b in zip(self._get(src, layer), self._get(dst, layer)):
+            b.truncate(0)
+            if n:
+                b.append(a.view()[:, :n].copy())
+
+    def rollover(self, slot: int, layer: int, prefix_len: int, retained: int,
+                 inv_freq: np.ndarray | None = None, scaling: float = 1.0) -> None:
+        """Keep [0, prefix_len), move the last `retained` rows behind it and
+        rotate their keys by prefix_len - (L - retained) positions
+        (gemma4_cache_rebase_async, gemma4_listener_cache.cu:303-351, then
+        kernel_rope_rebase_bf16 per layer, impl.inc:3835-3895)."""
+        if self.layers[layer].int8:
+            raise ValueError("rollover rotates bf16 keys only")
+        kr, vr, ks, vs = self._get(slot, layer)
+        L = kr.n
+        if not (0 < prefix_len and 0 < retained and L > prefix_len + retained):
+            raise ValueError("rollover needs L > prefix_len + retained > 0")
+        k, v = kr.view(), vr.view()
+        moved_k = k[:, L - retained:].copy()
+        if inv_freq is not None:
+            moved_k = rope_rebase(moved_k, inv_freq, prefix_len - (L - retained), scaling)
+        new_k = np.concatenate([k[:, :prefix_len], moved_k], axis=1)
+        new_v = np.concatenate([v[:, :prefix_len], v[:, L - retained:]], axis=1)
+        kr.truncate(0)
+        vr.truncate(0)
+        kr.append(new_k)
+        vr.append(new_v)
 
     def values(self, slot: int, layer: int) -> tuple[np.ndarray, np.ndarray]:
         """Dequantised float32 K, V [Hkv, L, D]."""

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 template <int D, int R>
 struct DecodeLds {
     static constexpr bool kWgMerge = R * D <= 4096;
-    static constexpr int kFloats = kWgMerge ? (kWaves - 1) * R * D : 1;
+    static constexpr int kFloats = kWgMerge ? kWaves * R * D : 1;
 };
 
 // grid (n_split / kWaves, kv_heads, n_items), 256 threads = kWaves waves.
@@ -386,12 +386,12 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                     kp = nw ? a.k_new + on : kp;
                     vp = nw ? a.v_new + on : vp;
                 }
-                kx[u] = *reinterpret_cast<const uint4 *>(kp);
-                vx[u] = *reinterpret_cast<const uint4 *>(vp);
+                kx[u] = load_stream16(kp);
+                vx[u] = load_stream16(vp);
                 ksc[u] = vsc[u] = 0.f;
             } else {
-                kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.k) + o + seg * VEC);
-                vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(a.kv.v) + o + seg * VEC);
+                kx[u] = load_stream16(static_cast<const int8_t *>(a.kv.k) + o + seg * VEC);
+                vx[u] = load_stream16(static_cast<const int8_t *>(a.kv.v) + o + seg * VEC);
                 ksc[u] = a.kv.ks[o / D];
                 vsc[u] = a.kv.vs[o / D];
             }
@@ -484,51 +484,49 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         }
     }
     using Lds = DecodeLds<D, R>;
-    __shared__ float lds[Lds::kFloats];
+    __shared__ __align__(16) float lds[Lds::kFloats];
     __shared__ float2 lds_ml[kWaves * R];
-    int part;
     if constexpr (Lds::kWgMerge) {
-        // Workgroup merge: waves 1..3 hand their partials to wave 0 in LDS.
-        part = blockIdx.x;
+        // Workgroup merge: every wave puts its partial in LDS; wave w then
+        // merges rows w, w + kWaves, ... over the kWaves partials (64 lanes
+        // across D) and writes the workgroup's partial of those rows.
         if (sub == 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (wave > 0) {
+                float4 *dst = reinterpret_cast<float4 *>(lds + (wave * R + r) * D + seg * VEC);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) lds[((wave - 1) * R + r) * D + seg * VEC + e] = acc[r][e];
-                }
+                for (int t = 0; t < VEC / 4; ++t)
+                    dst[t] = make_float4(acc[r][4 * t], acc[r][4 * t + 1], acc[r][4 * t + 2], acc[r][4 * t + 3]);
                 if (seg == 0) lds_ml[wave * R + r] = make_float2(m_run[r], l_run[r]);
             }
         }
         __syncthreads();
-        if (wave == 0) {
+        constexpr int EPL = D / 64;  // dims per lane
+        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + blockIdx.x) * R;
+        for (int r = wave; r < R && r < rows; r += kWaves) {
+            float M = kNegBig;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float M = m_run[r];
+            for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
+            float L = 0.f, o[EPL];
 #pragma unroll
-                for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
-                const float w0 = __builtin_amdgcn_exp2f(m_run[r] - M);
-                float L = l_run[r] * w0;
+            for (int e = 0; e < EPL; ++e) o[e] = 0.f;
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) acc[r][e] *= w0;
+            for (int w2 = 0; w2 < kWaves; ++w2) {
+                const float2 ml = lds_ml[w2 * R + r];
+                const float ww = __builtin_amdgcn_exp2f(ml.x - M);
+                L = fmaf(ml.y, ww, L);
+                const float *src = lds + (w2 * R + r) * D + lane * EPL;
 #pragma unroll
-                for (int w2 = 1; w2 < kWaves; ++w2) {
-                    const float2 ml = lds_ml[w2 * R + r];
-                    const float ww = __builtin_amdgcn_exp2f(ml.x - M);
-                    L = fmaf(ml.y, ww, L);
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e)
-                        acc[r][e] = fmaf(lds[((w2 - 1) * R + r) * D + seg * VEC + e], ww, acc[r][e]);
-                }
-                m_run[r] = M;
-                l_run[r] = L;
+                for (int e = 0; e < EPL; ++e) o[e] = fmaf(src[e], ww, o[e]);
             }
+            float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[e] = o[e];
+            if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
         }
-    } else {
-        part = split;
-    }
-    if (sub == 0 && (!Lds::kWgMerge || wave == 0)) {
-        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + part) * R;
+    } else if (sub == 0) {
+        // one partial per wave
+        const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + split) * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (r < rows) {
@@ -542,55 +540,65 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     }
 }
 
-// grid (kv_heads, n_items, chunks), 256 threads: thread t of chunk c merges
-// output 256c + t of the R*D outputs of one (item, kv head) from the partials
-// decode_kernel wrote. Runs after it in stream order, so every partial is
-// visible without device-scope fences (which on gfx950 write back and
-// invalidate the whole L2 of an XCD). Each thread issues the (m, l) pair and
-// the accumulator of 16 partials at once — one dependent memory round trip
-// per 16 partials — and merges them in index order (deterministic):
+// grid (kv_heads, n_items, chunks), 256 threads: G consecutive threads merge
+// one of the R*D outputs of an (item, kv head) from the partials
+// decode_kernel wrote; thread j of the G takes partials j, j + G, ... (at most
+// 16, all issued at once: one dependent memory round trip). Runs after the
+// decode in stream order, so every partial is visible without device-scope
+// fences (which on gfx950 write back and invalidate the whole L2 of an XCD).
+// Per thread, then across the G lanes in a fixed butterfly (deterministic):
 //   M = max m_s, L = sum l_s 2^(m_s - M), out = sum acc_s 2^(m_s - M) / L.
 // Chunk 0 of kv head 0 also advances the item's length after a fused append:
 // every decode workgroup has read the lengths by then.
-template <int D, int R>
+template <int D, int R, int G>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     constexpr int B = 16;
     const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
     const int n_parts = DecodeLds<D, R>::kWgMerge ? a.n_split / kWaves : a.n_split;
     const int Qn = a.qn;
     const int rows = a.group * Qn;
-    const int idx = blockIdx.z * 256 + threadIdx.x;
-    if (idx < rows * D) {
-        const int r = idx / D, d = idx % D;
-        const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
-        const float2 *ml = a.part_ml + pbase + r;
-        const float *acc = a.part_acc + (pbase + r) * D + d;
-        float M = kNegBig, L = 0.f, O = 0.f;
-        for (int s0 = 0; s0 < n_parts; s0 += B) {
-            float2 m[B];
-            float v[B];
+    const int t = blockIdx.z * 256 + threadIdx.x;
+    const int idx = t / G, j = t % G;
+    const bool live = idx < rows * D;
+    const int r = live ? idx / D : 0, d = live ? idx % D : 0;
+    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
+    const float2 *ml = a.part_ml + pbase + r;
+    const float *acc = a.part_acc + (pbase + r) * D + d;
+    float M = kNegBig, L = 0.f, O = 0.f;
+    for (int s0 = j; s0 < n_parts; s0 += B * G) {
+        float2 m[B];
+        float v[B];
 #pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const bool ok = s0 + u < n_parts;
-                m[u] = ok ? ml[(int64_t)(s0 + u) * R] : make_float2(kNegBig, 0.f);
-                v[u] = ok ? acc[(int64_t)(s0 + u) * R * D] : 0.f;
-            }
-            float bm = M;
-#pragma unroll
-            for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
-            const float c = __builtin_amdgcn_exp2f(M - bm);
-            L *= c;
-            O *= c;
-            M = bm;
-#pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const float w = __builtin_amdgcn_exp2f(m[u].x - M);
-                L = fmaf(m[u].y, w, L);
-                O = fmaf(v[u], w, O);
-            }
+        for (int u = 0; u < B; ++u) {
+            const int sp = s0 + u * G;
+            const bool ok = live && sp < n_parts;
+            m[u] = ok ? ml[(int64_t)sp * R] : make_float2(kNegBig, 0.f);
+            v[u] = ok ? acc[(int64_t)sp * R * D] : 0.f;
         }
-        const int j = r / Qn, i = r % Qn;
-        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + j) * Qn + i) * D + d] = f32_to_bf16(L > 0.f ? O / L : 0.f);
+        float bm = M;
+#pragma unroll
+        for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
+        const float c = __builtin_amdgcn_exp2f(M - bm);
+        L *= c;
+        O *= c;
+        M = bm;
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const float w = __builtin_amdgcn_exp2f(m[u].x - M);
+            L = fmaf(m[u].y, w, L);
+            O = fmaf(v[u], w, O);
+        }
+    }
+    if constexpr (G > 1) {
+        const float Mg = group_max<G>(M);
+        const float w = __builtin_amdgcn_exp2f(M - Mg);
+        L = group_sum<G>(L * w);
+        O = group_sum<G>(O * w);
+    }
+    if (live && j == 0) {
+        const int jh = r / Qn, i = r % Qn;
+        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
+            f32_to_bf16(L > 0.f ? O / L : 0.f);
     }
     if (a.advance && kvh == 0 && blockIdx.z == 0 && threadIdx.x == 0)
         a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += a.qn;
@@ -984,6 +992,26 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
     return hipGetLastError();
 }
 
+// The merge with G threads per output, G the smallest power of two that
+// leaves each thread at most 16 partials.
+template <int HD, int RT>
+static hipError_t launch_merge(const DecodeArgs &a, hipStream_t s) {
+    const int parts = DecodeLds<HD, RT>::kWgMerge ? a.n_split / kWaves : a.n_split;
+    const int outs = a.group * a.qn * HD;
+    auto go = [&](auto g) {
+        constexpr int G = decltype(g)::value;
+        const int chunks = (outs * G + 255) / 256;
+        hipLaunchKernelGGL((merge_kernel<HD, RT, G>), dim3(a.kv.kv_heads, a.n_items, chunks), dim3(256), 0, s, a);
+        return hipGetLastError();
+    };
+    if (parts <= 16) return go(std::integral_constant<int, 1>{});
+    if (parts <= 32) return go(std::integral_constant<int, 2>{});
+    if (parts <= 64) return go(std::integral_constant<int, 4>{});
+    if (parts <= 128) return go(std::integral_constant<int, 8>{});
+    if (parts <= 256) return go(std::integral_constant<int, 16>{});
+    return hipErrorInvalidValue;
+}
+
 template <int HD, int RT>
 static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s) {
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
@@ -1000,9 +1028,7 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int chunks = (a.group * a.qn * HD + 255) / 256;
-    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items, chunks), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return launch_merge<HD, RT>(a, s);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s) {
@@ -1025,10 +1051,7 @@ static hipError_t launch_talker_rt(const TalkerArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, KVRT_LAYOUT_CONTIG, TalkerArgs>), grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const DecodeArgs &m = a;
-    const int chunks = (a.group * a.qn * HD + 255) / 256;
-    hipLaunchKernelGGL((merge_kernel<HD, RT>), dim3(a.kv.kv_heads, a.n_items, chunks), dim3(256), 0, s, m);
-    return hipGetLastError();
+    return launch_merge<HD, RT>(a, s);
 }
 
 hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s) {

@@ -150,6 +150,7 @@ struct PrefillArgs {
     int32_t group;          // Hq / kv_heads (waves per workgroup)
     int32_t qn;             // Q (query rows per item)
     int32_t window;
+    int32_t heads_per_wg;   // q heads of the group served by one workgroup (divides group)
     float scale_log2;
     int32_t slots[kMaxItems];
 };
@@ -211,8 +212,9 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_
 hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s);
 // Chunked-prefill attention on MFMA (bf16 CONTIG / RING / PAGED layers).
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
-// Largest GQA group (waves per workgroup) of the prefill kernel for a head dim.
-constexpr int prefill_max_group(int head_dim) { return head_dim >= 256 ? 8 : 16; }
+// Most q heads one prefill workgroup computes (one wave each); a larger GQA
+// group is served by several workgroups.
+constexpr int kPfMaxHeads = 8;
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
 hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,
                             hipStream_t s);

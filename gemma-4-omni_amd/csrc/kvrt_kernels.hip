@@ -607,13 +607,17 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // chunked-prefill attention (MFMA)
 // ---------------------------------------------------------------------------
-// grid (ceil(Q / 16), kv_heads, n_items), 64 * g threads: wave j is q head
-// kvh * g + j over the 16 query rows of block x; the g waves share each
-// 32-key K/V tile staged in LDS (K row-major, V transposed). Per tile and
+// grid (ceil(Q / 16), kv_heads * g / hw, n_items), 64 * NW threads with NW =
+// 4 or 8 >= hw: workgroup (x, y) serves the hw q heads
+// kvh*g + (y % (g/hw))*hw + j (wave j < hw) over the 16 query rows of block x;
+// all NW waves stage each 32-key K/V tile into LDS (K row-major, V
+// transposed) and the hw computing waves share it. With PF the next tile's
+// global loads are issued into registers before the current tile is
+// computed, so their latency hides behind the MFMAs. Per tile and computing
 // wave:
 //   S^T (32 keys x 16 queries) = K Q^T      2 * D/32  v_mfma_f32_16x16x32_bf16
 //   online softmax per query column (fp32, exp2 domain)
-//   O^T (D x 16) += V^T P^T                 D/16      v_mfma_f32_16x16x32_bf16
+//   O^T (D x 16) += V^T P^T                 2 * D/16  v_mfma_f32_16x16x32_bf16
 // with P split into two bf16 terms for the second product and everything
 // accumulated in fp32. MFMA lane layouts (16x16x32): A[row l%16][k 8(l/16)+j],
 // B[k 8(l/16)+j][col l%16], D[row 4(l/16)+v][col l%16].
@@ -632,23 +636,120 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
                                                    c, 0, 0, 0);
 }
 
+// Calls f(integral_constant<int, u>) for u = U .. N-1: register arrays
+// indexed by u stay in registers.
+template <int U, int N>
+struct StaticFor {
+    template <class F>
+    __device__ __forceinline__ static void run(F &&f) {
+        if constexpr (U < N) {
+            f(std::integral_constant<int, U>{});
+            StaticFor<U + 1, N>::run(f);
+        }
+    }
+};
+
+// Tile units: K unit c = (row c / (D/8), 16 B segment c % (D/8)); V unit
+// c = (row c % 32, segment c / 32), so that consecutive threads write
+// adjacent words of a V^T row. Keys at or past kend read row kstart (masked
+// in the softmax).
 template <int D, int LAYOUT>
-__global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillArgs a) {
+__device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend, int c,
+                                              u32x4_t &kx, u32x4_t &vx, bool &bad) {
+    constexpr int UNITS = kPfKeys * (D / 8);
+    const uint16_t *kg = static_cast<const uint16_t *>(kv.k);
+    const uint16_t *vg = static_cast<const uint16_t *>(kv.v);
+    const int cc = c < UNITS ? c : 0;
+    const int kr = cc / (D / 8), ks = cc % (D / 8);
+    const int key = t0 + kr;
+    const int vr = cc % kPfKeys, vs = cc / kPfKeys;
+    const int vkey = t0 + vr;
+    int64_t off, voff;
+    if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
+        // one multiply-add per row from the (slot, head) base
+        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
+        off = base + (int64_t)(key < kend ? key : kstart) * D;
+        voff = base + (int64_t)(vkey < kend ? vkey : kstart) * D;
+    } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
+        // t0 % rows once per tile: rows of the tile wrap at most once
+        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
+        const int r0 = t0 % kv.rows, rs = kstart % kv.rows;
+        int rk = r0 + kr, rv = r0 + vr;
+        rk = rk >= kv.rows ? rk - kv.rows : rk;
+        rv = rv >= kv.rows ? rv - kv.rows : rv;
+        off = base + (int64_t)(key < kend ? rk : rs) * D;
+        voff = base + (int64_t)(vkey < kend ? rv : rs) * D;
+    } else {
+        off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kstart, D);
+        voff = row_offset<LAYOUT>(kv, slot, kvh, vkey < kend ? vkey : kstart, D);
+    }
+    if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+        bad |= off < 0;
+        off = off < 0 ? 0 : off;
+        voff = voff < 0 ? 0 : voff;
+    }
+    kx = *reinterpret_cast<const u32x4_t *>(kg + off + 8 * ks);
+    vx = *reinterpret_cast<const u32x4_t *>(vg + voff + 8 * vs);
+}
+
+template <int D>
+__device__ __forceinline__ void pf_stage_unit(uint16_t *sk, uint16_t *sv, int c, const u32x4_t &kx, const u32x4_t &vx) {
+    constexpr int UNITS = kPfKeys * (D / 8);
+    constexpr int KP = D + 8, VP = kPfKeys + 8;
+    if (c < UNITS) {
+        const int kr = c / (D / 8), ks = c % (D / 8);
+        *reinterpret_cast<u32x4_t *>(&sk[kr * KP + 8 * ks]) = kx;
+        const int vr = c % kPfKeys, vs = c / kPfKeys;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sv[(8 * vs + 2 * e) * VP + vr] = (uint16_t)(vx[e] & 0xffffu);
+            sv[(8 * vs + 2 * e + 1) * VP + vr] = (uint16_t)(vx[e] >> 16);
+        }
+    }
+}
+
+// A whole tile of KU units per thread: unit u of thread t is c = t + u * blockDim.
+template <int D, int LAYOUT, int KU>
+__device__ __forceinline__ void pf_fetch(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend,
+                                         u32x4_t (&kreg)[KU], u32x4_t (&vreg)[KU], bool &bad) {
+    StaticFor<0, KU>::run([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        pf_fetch_unit<D, LAYOUT>(kv, slot, kvh, t0, kstart, kend, threadIdx.x + u * (int)blockDim.x, kreg[u], vreg[u],
+                                 bad);
+    });
+}
+
+template <int D, int KU>
+__device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4_t (&kreg)[KU], const u32x4_t (&vreg)[KU]) {
+    StaticFor<0, KU>::run([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        pf_stage_unit<D>(sk, sv, threadIdx.x + u * (int)blockDim.x, kreg[u], vreg[u]);
+    });
+}
+
+template <int D, int LAYOUT, int NW, bool PF>
+__global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = D + 8;        // K tile row pitch (bf16): 16 B of padding per row
     constexpr int VP = kPfKeys + 8;  // V^T tile row pitch (bf16)
+    constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
+    constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
+    constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
     __shared__ __align__(16) uint16_t sk[kPfKeys * KP];
     __shared__ __align__(16) uint16_t sv[D * VP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int item = blockIdx.z, kvh = blockIdx.y, hkv = gridDim.y;
-    const int g = a.group, hq = hkv * g, head = kvh * g + wave;
+    const int hw = a.heads_per_wg, nhb = a.group / hw;
+    const int item = blockIdx.z, kvh = blockIdx.y / nhb, hkv = gridDim.y / nhb;
+    const int g = a.group, hq = hkv * g;
+    const bool computes = wave < hw;
+    const int head = kvh * g + (blockIdx.y % nhb) * hw + (computes ? wave : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     const int Qn = a.qn;
     const int qrow0 = blockIdx.x * 16;
     const int base_pos = L - Qn;               // position of query row 0
     const int qr = qrow0 + col;                // this lane's query row (S^T / O^T column)
-    const bool qvalid = qr < Qn;
+    const bool qvalid = computes && qr < Qn;
     const int pq = base_pos + qr;
     const int lo_q = a.window > 0 ? pq - a.window + 1 : 0;
     const int kend = base_pos + min(Qn, qrow0 + 16);  // keys < kend: up to the block's last query
@@ -667,40 +768,14 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
 #pragma unroll
     for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool bad = false;
-    const uint16_t *kg = static_cast<const uint16_t *>(a.kv.k);
-    const uint16_t *vg = static_cast<const uint16_t *>(a.kv.v);
 
-    for (int t0 = kstart; t0 < kend; t0 += kPfKeys) {
-        __syncthreads();  // the previous tile has been consumed
-        // K: row copies, consecutive threads on consecutive 16 B of a row.
-        for (int c = threadIdx.x; c < kPfKeys * (D / 8); c += blockDim.x) {
-            const int kr = c / (D / 8), seg = c % (D / 8);
-            const int key = t0 + kr;
-            const int kc = key < kend ? key : kstart;  // readable row; masked below
-            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
-            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
-                bad |= off < 0;
-                off = off < 0 ? 0 : off;
-            }
-            *reinterpret_cast<uint4 *>(&sk[kr * KP + 8 * seg]) = *reinterpret_cast<const uint4 *>(kg + off + 8 * seg);
-        }
-        // V transposed: consecutive threads on consecutive keys of one 8-dim
-        // segment, so each 2-byte LDS store of a wave covers adjacent words.
-        for (int c = threadIdx.x; c < kPfKeys * (D / 8); c += blockDim.x) {
-            const int kr = c % kPfKeys, seg = c / kPfKeys;
-            const int key = t0 + kr;
-            const int kc = key < kend ? key : kstart;
-            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
-            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) off = off < 0 ? 0 : off;
-            const uint4 vx = *reinterpret_cast<const uint4 *>(vg + off + 8 * seg);
-            const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                sv[(8 * seg + 2 * e) * VP + kr] = (uint16_t)(vw[e] & 0xffffu);
-                sv[(8 * seg + 2 * e + 1) * VP + kr] = (uint16_t)(vw[e] >> 16);
-            }
-        }
-        __syncthreads();
+    // The MFMA work on the tile staged in LDS, keys t0 .. t0 + 31.
+    auto compute_tile = [&](int t0) __attribute__((always_inline)) {
+        // every key of the tile visible to all 16 queries of the block (the
+        // block's first query sees up to its own position, the last one's
+        // window starts at or before t0): no per-key mask
+        const bool all_visible = qrow0 + 16 <= Qn && t0 + kPfKeys - 1 <= base_pos + qrow0 &&
+                                 (a.window == 0 || t0 >= base_pos + qrow0 + 15 - a.window + 1);
         // S^T blocks: rows = keys pf_key(b, i), cols = queries
         f32x4_t s[2];
 #pragma unroll
@@ -717,7 +792,7 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
         for (int j = 0; j < 8; ++j) {
             const int key = t0 + 8 * grp + j;
             const float raw = j < 4 ? s[0][j] : s[1][j - 4];
-            const bool vis = qvalid && key < kend && key <= pq && key >= lo_q;
+            const bool vis = all_visible || (qvalid && key < kend && key <= pq && key >= lo_q);
             sc[j] = vis ? raw * a.scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, sc[j]);
         }
@@ -726,8 +801,10 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
         const float corr = __builtin_amdgcn_exp2f(m - mn);
         m = mn;
         l *= corr;
+        if (__any(corr != 1.0f)) {
 #pragma unroll
-        for (int b = 0; b < D / 16; ++b) o[b] *= corr;
+            for (int b = 0; b < D / 16; ++b) o[b] *= corr;
+        }
         // P = P_hi + P_lo, both bf16 (P_lo = the rounding error of P_hi): the
         // two products keep P to ~2^-17 relative, where one bf16 P (2^-9)
         // would be visible in bf16 outputs of few-key rows.
@@ -737,9 +814,8 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
             const float p0 = __builtin_amdgcn_exp2f(sc[2 * j] - m);
             const float p1 = __builtin_amdgcn_exp2f(sc[2 * j + 1] - m);
             l += p0 + p1;
-            const uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
-            ph[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-            pl[j] = (uint32_t)f32_to_bf16(p0 - bf16_to_f32(h0)) | ((uint32_t)f32_to_bf16(p1 - bf16_to_f32(h1)) << 16);
+            ph[j] = pack_bf16x2(p0, p1);
+            pl[j] = pack_bf16x2(p0 - bf16_lo(ph[j]), p1 - bf16_hi(ph[j]));
         }
         const uint4 pop_hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
         const uint4 pop_lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
@@ -749,8 +825,47 @@ __global__ __launch_bounds__(D >= 256 ? 512 : 1024) void prefill_kernel(PrefillA
             const uint4 va = *reinterpret_cast<const uint4 *>(&sv[(16 * b + col) * VP + 8 * grp]);
             o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
         }
+    };
+    // Q is in registers before the first prefetch is issued: inside the loop
+    // the compiler then waits only for each tile's own loads, not for the
+    // prefetches behind it (vmcnt counts in order).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if constexpr (PF) {
+        // PD tiles in flight in registers: the loop runs PD tiles per pass,
+        // phase p staging ring entry p and refilling it with the tile PD
+        // ahead (keys past kend read row kstart: in bounds, never visible).
+        u32x4_t kreg[PD][KU], vreg[PD][KU];
+        StaticFor<0, PD>::run([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, kstart + p * kPfKeys, kstart, kend, kreg[p], vreg[p], bad);
+        });
+        for (int t0 = kstart; t0 < kend; t0 += PD * kPfKeys) {
+            StaticFor<0, PD>::run([&](auto pc) {
+                constexpr int p = decltype(pc)::value;
+                const int tt = t0 + p * kPfKeys;
+                if (tt < kend) {
+                    __syncthreads();  // the previous tile has been consumed
+                    pf_stage<D, KU>(sk, sv, kreg[p], vreg[p]);
+                    __syncthreads();
+                    pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, tt + PD * kPfKeys, kstart, kend, kreg[p], vreg[p], bad);
+                    if (computes) compute_tile(tt);
+                }
+            });
+        }
+    } else {
+        for (int t0 = kstart; t0 < kend; t0 += kPfKeys) {
+            __syncthreads();  // the previous tile has been consumed
+            for (int c = threadIdx.x; c < UNITS; c += blockDim.x) {  // one unit in registers at a time
+                u32x4_t kx, vx;
+                pf_fetch_unit<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, c, kx, vx, bad);
+                pf_stage_unit<D>(sk, sv, c, kx, vx);
+            }
+            __syncthreads();
+            if (computes) compute_tile(t0);
+        }
     }
     if (bad) a.err[0] = 1;
+    if (!computes) return;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));
     if (!qvalid) return;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
@@ -1069,9 +1184,17 @@ hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_
 }
 
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
-    dim3 grid((a.qn + 15) / 16, a.kv.kv_heads, a.n_items), block(64 * a.group);
-    KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
-        hipLaunchKernelGGL((prefill_kernel<HD, LY>), grid, block, 0, s, a)));
+    const int hw = a.heads_per_wg;
+    if (hw <= 0 || a.group % hw != 0 || hw > kPfMaxHeads) return hipErrorInvalidValue;
+    dim3 grid((a.qn + 15) / 16, a.kv.kv_heads * (a.group / hw), a.n_items);
+    // 4 or 8 waves; D = 512 keeps no tile in flight across the MFMAs (registers)
+    if (hw > 4) {
+        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
+            hipLaunchKernelGGL((prefill_kernel<HD, LY, 8, (HD < 512)>), grid, dim3(512), 0, s, a)));
+    } else {
+        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
+            hipLaunchKernelGGL((prefill_kernel<HD, LY, 4, (HD < 512)>), grid, dim3(256), 0, s, a)));
+    }
     return hipGetLastError();
 }
 

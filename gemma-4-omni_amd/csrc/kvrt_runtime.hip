@@ -1320,7 +1320,7 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     for (int i = 0; i < 4; ++i)
         if (out->dims[i] != q->dims[i]) return KVRT_EINVAL;
     const int group = (int)(hq / hkv);
-    if (group > prefill_max_group(D) || !std::isfinite(scale)) return KVRT_EINVAL;
+    if (!std::isfinite(scale)) return KVRT_EINVAL;
     uint64_t tile_keys = 0;
     for (int i = 0; i < n; ++i) {
         const int L = c->len_at(slots[i], layer);
@@ -1345,6 +1345,12 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     a.group = group;
     a.qn = (int)qn;
     a.window = s.window;
+    // q heads per workgroup: the largest divisor of the group a workgroup
+    // can hold (each further part of the group stages the K/V tiles again)
+    int hw = 1;
+    for (int d = 1; d <= std::min(group, kPfMaxHeads); ++d)
+        if (group % d == 0) hw = d;
+    a.heads_per_wg = hw;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches++;

@@ -57,6 +57,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--one-stream", action="store_true",
                    help="run every launch on the caller's stream (default: one stream per model and group)")
     p.add_argument("--kernel-reps", type=int, default=50, help="event-timed launches of the dominant kernel")
+    p.add_argument("--talker-wgs", type=int, default=192,
+                   help="split-K decode workgroups per talker launch (kvrt_config.decode_wgs)")
+    p.add_argument("--thinker-wgs", type=int, default=192,
+                   help="split-K decode workgroups per thinker launch (kvrt_config.decode_wgs)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
@@ -81,8 +85,10 @@ def build_runtimes(args, capacity: int, n_slots: int):
             th_specs.append(LayerSpec(kv_heads=THINKER["hkv"], head_dim=THINKER["d"], layout="ring",
                                       window=THINKER["window"], ring_rows=THINKER["window"]))
     tk_specs = [LayerSpec(kv_heads=TALKER["hkv"], head_dim=TALKER["d"]) for _ in range(TALKER["layers"])]
-    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, device="cuda")
-    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, device="cuda")
+    th_wgs = getattr(args, "thinker_wgs", 0) if args is not None else 0
+    tk_wgs = getattr(args, "talker_wgs", 0) if args is not None else 0
+    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, decode_wgs=th_wgs, device="cuda")
+    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, decode_wgs=tk_wgs, device="cuda")
     return thinker, talker
 
 
@@ -432,6 +438,7 @@ def main() -> int:
             "hip_graph": graph is not None,
             "hip_streams": 1 if args.one_stream else 2 * args.groups,
             "tokens_per_step": tokens_per_step,
+            "decode_wgs": {"talker": args.talker_wgs, "thinker": args.thinker_wgs},
         },
         "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
         "step_hbm_frac": round(total_bytes / elapsed / HBM_PEAK, 4),

@@ -204,9 +204,9 @@ bool is_contiguous(const kvrt_tensor *t) {
 
 constexpr int kMaxWgPerHead = 64;
 
-int target_wgs() {
+int target_wgs(const kvrt_config &cfg) {
     static const int v = env_int("KVRT_TARGET_WGS", 512);
-    return v;
+    return cfg.decode_wgs > 0 ? cfg.decode_wgs : v;
 }
 // Keys a wave must own at least: one main-loop iteration of the kernel
 // variant (8..32 keys), unless KVRT_MIN_KEYS_PER_WAVE asks for more.
@@ -217,11 +217,11 @@ int min_keys_per_wave(int keys_per_iter) {
 
 // Number of wave splits per (item, kv head): enough workgroups to fill the
 // chip, but at least min_keys keys per wave. n_items * kv_heads * (splits /
-// kWaves) <= target_wgs + n_items * kv_heads, which bounds the workspace.
-int choose_splits(int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
+// kWaves) <= target + n_items * kv_heads, which bounds the workspace.
+int choose_splits(int target, int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
     const int per_head = n_items * kv_heads;
     const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave(keys_per_iter);
-    int wg = (target_wgs() + per_head - 1) / per_head;
+    int wg = (target + per_head - 1) / per_head;
     const int64_t cap = std::max<int64_t>(1, (max_keys + per_wg - 1) / per_wg);
     if (wg > cap) wg = (int)cap;
     if (wg > kMaxWgPerHead) wg = kMaxWgPerHead;  // fix-up merges <= 256 wave partials
@@ -242,7 +242,7 @@ size_t workspace_bound(const kvrt_ctx *c) {
     size_t best = 0;
     for (const Layer &L : c->layers) {
         const int hkv = L.spec.kv_heads;
-        const int total_wgs = std::min(target_wgs() + n * hkv, n * hkv * kMaxWgPerHead);
+        const int total_wgs = std::min(target_wgs(c->cfg) + n * hkv, n * hkv * kMaxWgPerHead);
         const size_t parts = (size_t)total_wgs * kWaves * 16;
         best = std::max(best, ((parts * L.spec.head_dim + 63) / 64) * 64 * 4 + parts * 8 + 256);
     }
@@ -362,7 +362,8 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     *out = nullptr;
     if (cfg->struct_size != sizeof(kvrt_config)) return KVRT_EINVAL;
     if (cfg->n_layers <= 0 || cfg->n_layers > 4096 || cfg->n_slots <= 0 || cfg->n_slots > (1 << 20) ||
-        cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 65536)
+        cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 65536 || cfg->decode_wgs < 0 ||
+        cfg->decode_wgs > 65536)
         return KVRT_EINVAL;
     bool any_paged = false;
     for (int i = 0; i < cfg->n_layers; ++i) {
@@ -550,7 +551,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
     }
     const int R = rows_tile(rows);
-    const int n_split = choose_splits(n, hkv, max_keys, keys_per_iteration(D, R, s.dtype));
+    const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys, keys_per_iteration(D, R, s.dtype));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
     if (rc != KVRT_OK) return rc;
@@ -1398,7 +1399,8 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.group = group;
     a.qn = (int)qn;
     a.window = window;
-    a.n_split = choose_splits((int)n, (int)hkv, window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
+    a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv,
+                              window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
                               keys_per_iteration((int)D, rows_tile(rows), KVRT_BF16));
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = i;

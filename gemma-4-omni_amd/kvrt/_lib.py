@@ -77,6 +77,7 @@ class KvrtConfig(ctypes.Structure):
         ("pool_pages", c_int32),
         ("max_q", c_int32),
         ("pool_seed", c_int32),
+        ("decode_wgs", c_int32),
     ]
 
 

@@ -159,6 +159,7 @@ class KVRuntime:
         block_size: int = 16,
         pool_pages: int = 0,
         pool_seed: int = 0,
+        decode_wgs: int = 0,
         device: torch.device | str | None = None,
     ) -> None:
         self.lib = L.load()
@@ -183,6 +184,7 @@ class KVRuntime:
         cfg.pool_pages = self.pool_pages
         cfg.max_q = self.max_q
         cfg.pool_seed = int(pool_seed)
+        cfg.decode_wgs = int(decode_wgs)
         self._cfg = cfg
         specs = (L.KvrtLayerSpec * len(self.layers))(*[s.to_c() for s in self.layers])
         self._specs = specs

@@ -116,6 +116,10 @@ typedef struct kvrt_config {
     int32_t max_q;        /* max rows per decode append / attend; RING rows >= W + max_q - 1 */
     int32_t pool_seed;    /* PAGED: nonzero = hand out pool pages in an order
                              shuffled with this seed (0 = ascending)          */
+    int32_t decode_wgs;   /* split-K decode: target workgroups per launch
+                             (0 = 512, or KVRT_TARGET_WGS). Contexts whose
+                             launches run beside another model's on a second
+                             stream do better with fewer (e.g. 192)          */
 } kvrt_config;
 
 /* Optional caller-owned storage for one layer (kvrt_create_with_storage).

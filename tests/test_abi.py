@@ -70,6 +70,7 @@ int main(void) {
   F(kvrt_layer_spec, reserved);
   F(kvrt_config, struct_size); F(kvrt_config, n_layers); F(kvrt_config, n_slots); F(kvrt_config, capacity);
   F(kvrt_config, block_size); F(kvrt_config, pool_pages); F(kvrt_config, max_q); F(kvrt_config, pool_seed);
+  F(kvrt_config, decode_wgs);
   F(kvrt_storage, k); F(kvrt_storage, v); F(kvrt_storage, k_scale); F(kvrt_storage, v_scale);
   F(kvrt_counters, launches); F(kvrt_counters, appended_rows); F(kvrt_counters, appended_bytes);
   F(kvrt_counters, attended_keys); F(kvrt_counters, attended_bytes); F(kvrt_counters, gathered_bytes);
@@ -144,6 +145,7 @@ def test_layer_storage_bytes_per_layout():
     dict(cfg=dict(struct_size=4)),
     dict(cfg=dict(n_slots=0)),
     dict(cfg=dict(max_q=0)),
+    dict(cfg=dict(decode_wgs=-1)),
     dict(spec=dict(head_dim=96)),
     dict(spec=dict(kv_heads=0)),
     dict(spec=dict(dtype=1)),                                   # int8 needs PAGED

@@ -327,8 +327,8 @@ int kvrt_append_attend_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
  * first, e.g. with kvrt_append_async); out likewise. Same visibility, scale
  * and GQA head map as kvrt_attend_decode_async, for any Q <= length. P
  * enters the P.V product as a sum of two bf16 terms (~2^-17 relative);
- * scores, softmax and both products accumulate in fp32. bf16 layers only; Hq / kv_heads <= 16 (<= 8 for
- * head_dim >= 256). RING layers need ring_rows >= Q + window - 1, PAGED
+ * scores, softmax and both products accumulate in fp32. bf16 layers only;
+ * any Hq / kv_heads. RING layers need ring_rows >= Q + window - 1, PAGED
  * layers the pages of the oldest visible key (KVRT_ESTATE otherwise).
  * Replaces kernel_prefill_sdpa_bf16 (native/gemma4_listener_microbatch/
  * gemma4_listener_kernels.cuh:692-790) and the Q3..Q8 text-append attention

@@ -649,10 +649,9 @@ struct StaticFor {
     }
 };
 
-// Tile units: K unit c = (row c / (D/8), 16 B segment c % (D/8)); V unit
-// c = (row c % 32, segment c / 32), so that consecutive threads write
-// adjacent words of a V^T row. Keys at or past kend read row kstart (masked
-// in the softmax).
+// Tile units: unit c = (row c / (D/8), 16 B segment c % (D/8)) of both the
+// K and the V tile, both staged row-major. Keys at or past kend read row
+// kstart (masked in the softmax).
 template <int D, int LAYOUT>
 __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend, int c,
                                               u32x4_t &kx, u32x4_t &vx, bool &bad) {
@@ -662,49 +661,35 @@ __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kv
     const int cc = c < UNITS ? c : 0;
     const int kr = cc / (D / 8), ks = cc % (D / 8);
     const int key = t0 + kr;
-    const int vr = cc % kPfKeys, vs = cc / kPfKeys;
-    const int vkey = t0 + vr;
-    int64_t off, voff;
+    int64_t off;
     if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
         // one multiply-add per row from the (slot, head) base
         const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
         off = base + (int64_t)(key < kend ? key : kstart) * D;
-        voff = base + (int64_t)(vkey < kend ? vkey : kstart) * D;
     } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
         // t0 % rows once per tile: rows of the tile wrap at most once
         const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
         const int r0 = t0 % kv.rows, rs = kstart % kv.rows;
-        int rk = r0 + kr, rv = r0 + vr;
+        int rk = r0 + kr;
         rk = rk >= kv.rows ? rk - kv.rows : rk;
-        rv = rv >= kv.rows ? rv - kv.rows : rv;
         off = base + (int64_t)(key < kend ? rk : rs) * D;
-        voff = base + (int64_t)(vkey < kend ? rv : rs) * D;
     } else {
         off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kstart, D);
-        voff = row_offset<LAYOUT>(kv, slot, kvh, vkey < kend ? vkey : kstart, D);
-    }
-    if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
         bad |= off < 0;
         off = off < 0 ? 0 : off;
-        voff = voff < 0 ? 0 : voff;
     }
     kx = *reinterpret_cast<const u32x4_t *>(kg + off + 8 * ks);
-    vx = *reinterpret_cast<const u32x4_t *>(vg + voff + 8 * vs);
+    vx = *reinterpret_cast<const u32x4_t *>(vg + off + 8 * ks);
 }
 
 template <int D>
 __device__ __forceinline__ void pf_stage_unit(uint16_t *sk, uint16_t *sv, int c, const u32x4_t &kx, const u32x4_t &vx) {
     constexpr int UNITS = kPfKeys * (D / 8);
-    constexpr int KP = D + 8, VP = kPfKeys + 8;
+    constexpr int KP = D + 8;
     if (c < UNITS) {
         const int kr = c / (D / 8), ks = c % (D / 8);
         *reinterpret_cast<u32x4_t *>(&sk[kr * KP + 8 * ks]) = kx;
-        const int vr = c % kPfKeys, vs = c / kPfKeys;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            sv[(8 * vs + 2 * e) * VP + vr] = (uint16_t)(vx[e] & 0xffffu);
-            sv[(8 * vs + 2 * e + 1) * VP + vr] = (uint16_t)(vx[e] >> 16);
-        }
+        *reinterpret_cast<u32x4_t *>(&sv[kr * KP + 8 * ks]) = vx;
     }
 }
 
@@ -730,12 +715,11 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
 template <int D, int LAYOUT, int NW, bool PF>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = D + 8;        // K tile row pitch (bf16): 16 B of padding per row
-    constexpr int VP = kPfKeys + 8;  // V^T tile row pitch (bf16)
     constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
     constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
     constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
     __shared__ __align__(16) uint16_t sk[kPfKeys * KP];
-    __shared__ __align__(16) uint16_t sv[D * VP];
+    __shared__ __align__(16) uint16_t sv[kPfKeys * KP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
@@ -770,6 +754,20 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     bool bad = false;
 
     // The MFMA work on the tile staged in LDS, keys t0 .. t0 + 31.
+    // V^T operand rows through gfx950's LDS transpose read: in each group of
+    // 16 lanes, lane s points at key row 8*grp + s/4 (+4 for the second
+    // read), dims 4*(s%4) .. +3 of the 16-dim block; lane t = 4a + e then
+    // receives dim 4a + e of key rows 8*grp + j, j = 0..3, i.e. A[d][k].
+    const uint16_t *sv_lane = &sv[(8 * grp + (col >> 2)) * KP + 4 * (col & 3)];
+    auto read_vt = [&](const uint16_t *p) __attribute__((always_inline)) {
+        typedef short v4s_t __attribute__((ext_vector_type(4)));
+        const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (v4s_t __attribute__((address_space(3))) *)(p));
+        const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (v4s_t __attribute__((address_space(3))) *)(p + 4 * KP));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        return make_uint4(l2.x, l2.y, h2.x, h2.y);
+    };
     auto compute_tile = [&](int t0) __attribute__((always_inline)) {
         // every key of the tile visible to all 16 queries of the block (the
         // block's first query sees up to its own position, the last one's
@@ -822,7 +820,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // O^T += V^T P^T: A row i = d (16b + col), k = keys 8grp .. +7
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) {
-            const uint4 va = *reinterpret_cast<const uint4 *>(&sv[(16 * b + col) * VP + 8 * grp]);
+            const uint4 va = read_vt(sv_lane + 16 * b);
             o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
         }
     };

@@ -110,3 +110,39 @@ def test_prefill_rejects_what_it_cannot_see():
     with pytest.raises(KVRTError):  # more queries than positions
         rt.attend_prefill(0, q, [0], 0.1)
     assert rt.health() == 0
+
+
+@pytest.mark.parametrize("logical_q", [3, 5, 7])
+def test_even_physical_q_with_pad_row_truncation_equals_the_logical_q(logical_q):
+    """The reference's variable-Q text step runs an even physical Q (logical
+    + 1 pad row for odd logical Q), then truncates the cursor to the logical
+    end (gemma4_listener_microbatch_impl.inc:3476-3586,
+    native_listener_microbatch.py:1640-1655). kvrt takes any Q directly; both
+    routes must give the same logical rows, cache and next decode."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(logical_q)
+    hq, hkv, d = 8, 1, 256
+    prefix = randn_bf16(gen, (1, hkv, 300, d))
+    k = randn_bf16(gen, (1, hkv, logical_q + 1, d))
+    v = randn_bf16(gen, (1, hkv, logical_q + 1, d))
+    q = randn_bf16(gen, (1, hq, logical_q + 1, d), 0.5)
+    outs, rts = [], []
+    for physical in (logical_q, logical_q + 1):
+        rt = KVRuntime([LayerSpec(kv_heads=hkv, head_dim=d, window=512)], 1, 512, max_q=8, device="cuda")
+        rt.import_(0, 0, prefix.cuda(), prefix.cuda())
+        rt.append(0, k[:, :, :physical].contiguous().cuda(), v[:, :, :physical].contiguous().cuda(), [0])
+        outs.append(rt.attend_prefill(0, q[:, :, :physical].contiguous().cuda(), [0], 1 / 16))
+        rt.truncate(0, 300 + logical_q)
+        rts.append(rt)
+    torch.cuda.synchronize()
+    direct, padded = outs
+    assert float((direct.float() - padded[:, :, :logical_q].float()).abs().max()) <= 1e-6
+    assert rts[0].seq_length(0) == rts[1].seq_length(0) == 300 + logical_q
+    qd = randn_bf16(gen, (1, hq, 1, d), 0.5).cuda()
+    kd = randn_bf16(gen, (1, hkv, 1, d)).cuda()
+    a = rts[0].append_attend(0, qd, kd, kd, [0], 1 / 16)
+    b = rts[1].append_attend(0, qd, kd, kd, [0], 1 / 16)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert rts[0].health() == 0 and rts[1].health() == 0

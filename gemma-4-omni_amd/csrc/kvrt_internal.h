@@ -115,9 +115,17 @@ struct DecodeArgs {
     int32_t window;
     int32_t n_split;        // wave splits per (item, kv head) = gridDim.x * kWaves
     int32_t advance;        // the merge kernel adds qn to each item's length
+    int32_t n_parts;        // partials per (item, kv head) the merge kernel combines
     float scale_log2;       // softmax scale * log2(e)
     int32_t slots[kMaxItems];
 };
+
+// The split-K decode merges its 4 waves' partials in LDS (one partial per
+// workgroup) when R * D floats per wave fit.
+constexpr bool decode_wg_merge(int head_dim, int rows_tile) { return rows_tile * head_dim <= 4096; }
+// Row tiles that run on the MFMA decode kernel (bf16, causal / window visibility).
+constexpr int kMfmaDecodeMinRows = 8;
+constexpr int kMfmaDecodeKeys = 16;  // keys per MFMA decode tile
 
 // Talker visibility of one item (host-validated: 0 <= prefix_start <=
 // prefix_pos < audio_start <= audio_pos < length). Query row i of the item is
@@ -208,6 +216,9 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
 // Split-K attention over the view, then the merge kernel.
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head,
                          hipStream_t s);
+// The same decode with S and P.V on MFMA (bf16, row tiles 8 and 16), one
+// partial per workgroup; then the merge kernel.
+hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s);
 // The same split-K decode under the talker visibility (bf16 CONTIG layers).
 hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s);
 // Chunked-prefill attention on MFMA (bf16 CONTIG / RING / PAGED layers).

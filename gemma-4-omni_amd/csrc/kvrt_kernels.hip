@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 // of waves 1..3, when R * D is small enough to stage them.
 template <int D, int R>
 struct DecodeLds {
-    static constexpr bool kWgMerge = R * D <= 4096;
+    static constexpr bool kWgMerge = decode_wg_merge(D, R);
     static constexpr int kFloats = kWgMerge ? kWaves * R * D : 1;
 };
 
@@ -540,6 +540,226 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     }
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16k16(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
+                                                     c, 0, 0, 0);
+}
+// gfx950 LDS transpose read: in each group of 16 lanes, lane s gives the
+// address of 4 consecutive bf16; lane t = 4a + e receives element e of the
+// chunks of lanes a, a + 4, a + 8, a + 12.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+    const s16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4_t __attribute__((address_space(3))) *)(p));
+    return __builtin_bit_cast(uint2, x);
+}
+
+// Split-K decode on MFMA for R = g*Q in {8, 16} query rows per kv head
+// (bf16): same grid, key splits, visibility and partial format as
+// decode_kernel, one partial per workgroup. Per 16-key tile a wave computes
+//   S^T (16 keys x 16 rows) = K Q^T   D/32 v_mfma_f32_16x16x32_bf16, K read
+//                                     straight from HBM as the A operand
+//   O^T (D x 16) += V^T P^T           2 * D/16 v_mfma_f32_16x16x16_bf16
+// with the V tile staged row-major in the wave's own LDS slice and read
+// transposed (ds_read_b64_tr_b16), and P as two bf16 terms. Lane layouts:
+// 16x16x32 A[i l%16][k 8(l/16)+j], 16x16x16 A[i l%16][k 4(l/16)+j],
+// B[k ..][n l%16], D[i 4(l/16)+v][n l%16]; column n is query row r.
+template <int D, int R, int LAYOUT>
+__global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
+    constexpr int T = kMfmaDecodeKeys;
+    constexpr int KP = D + 8;  // V tile row pitch (bf16)
+    static_assert(R == 8 || R == 16, "MFMA decode row tiles");
+    // the waves' V tiles while streaming, their partials for the merge after
+    constexpr int kTileBytes = kWaves * T * KP * 2, kPartBytes = kWaves * R * D * 4;
+    __shared__ __align__(16) uint8_t lds_raw[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
+    __shared__ float2 lds_ml[kWaves * R];
+    uint16_t *sv_all = reinterpret_cast<uint16_t *>(lds_raw);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int item = blockIdx.z, kvh = blockIdx.y, hkv = gridDim.y;
+    const int split = blockIdx.x * kWaves + wave;
+    const int slot = a.slots[item];
+    const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const bool fused = a.k_new != nullptr;
+    int kend = fused ? len + Qn : len;
+    if (LAYOUT == KVRT_LAYOUT_CONTIG && kend > a.kv.rows) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) a.err[0] = 1;
+        kend = a.kv.rows;
+    }
+    const int p0 = kend - Qn;
+    const int kstart = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int nk = max(0, kend - kstart);
+    int chunk = (nk + a.n_split - 1) / a.n_split;
+    chunk = (chunk + T - 1) / T * T;
+    const int ws = kstart + split * chunk;
+    const int we = min(kend, ws + chunk);
+
+    // Fused append: workgroup 0 of every (item, kv head) stores the new rows;
+    // no workgroup of this launch reads them from the cache.
+    if (fused && blockIdx.x == 0) {
+        for (int c = threadIdx.x; c < Qn * (D / 8); c += blockDim.x) {
+            const int r = c / (D / 8), sg = c % (D / 8);
+            const int pos = len + r;
+            bool ok = true;
+            if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) ok = pos < a.kv.rows;
+            const int64_t dst = ok ? row_offset<LAYOUT>(a.kv, slot, kvh, pos, D) : -1;
+            if (dst < 0) {
+                a.err[0] = 1;
+                continue;
+            }
+            const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 8;
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.k) + dst + sg * 8) =
+                *reinterpret_cast<const uint4 *>(a.k_new + src);
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.v) + dst + sg * 8) =
+                *reinterpret_cast<const uint4 *>(a.v_new + src);
+        }
+    }
+
+    // Q^T as the B operand: column col is row r = col (q head kvh*g + r/Qn,
+    // query r % Qn); lane (col, grp) holds dims 32c + 8grp .. +7.
+    const int hq = hkv * a.group;
+    const bool rvalid = col < rows;
+    uint4 qop[D / 32];
+    {
+        const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
+        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D + 8 * grp;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c)
+            qop[c] = rvalid ? *reinterpret_cast<const uint4 *>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
+    }
+    const int hi = rvalid ? p0 + col % Qn : -1;
+    const int lo = a.window > 0 ? p0 + col % Qn - a.window + 1 : 0;
+    float m = kNegBig, l = 0.f;  // running max (uniform per column) and this lane's partial sum
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint16_t *sv = sv_all + wave * (T * KP);
+    const uint16_t *sv_lane = sv + (4 * grp + (col >> 2)) * KP + 4 * (col & 3);
+    bool bad = false;
+    const int64_t new_base = ((int64_t)item * hkv + kvh) * Qn * D;
+    for (int t0 = ws; t0 < we; t0 += T) {
+        // K as the A operand (lane (col, grp): key t0 + col, dims 32c + 8grp)
+        // and the V tile (unit u = lane + 64i: key row u / (D/8), 16 B
+        // segment u % (D/8)); keys past we read row ws and are masked; the
+        // rows of a fused append come from k_new / v_new.
+        uint4 ka[D / 32], vt[D / 32];
+#pragma unroll
+        for (int i = -1; i < D / 32; ++i) {
+            const int kr = i < 0 ? col : (lane + 64 * i) / (D / 8);
+            const int kk = t0 + kr;
+            const int kc = kk < we ? kk : ws;
+            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+                bad |= kk < we && off < 0;
+                off = off < 0 ? 0 : off;
+            }
+            const uint16_t *kp = static_cast<const uint16_t *>(a.kv.k) + off;
+            const uint16_t *vp = static_cast<const uint16_t *>(a.kv.v) + off;
+            if (fused) {
+                const bool nw = kc >= len;
+                const int64_t on = new_base + (int64_t)(kc - len) * D;
+                kp = nw ? a.k_new + on : kp;
+                vp = nw ? a.v_new + on : vp;
+            }
+            if (i < 0) {
+#pragma unroll
+                for (int c = 0; c < D / 32; ++c) ka[c] = load_stream16(kp + 32 * c + 8 * grp);
+            } else {
+                vt[i] = load_stream16(vp + 8 * ((lane + 64 * i) % (D / 8)));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            const int u = lane + 64 * i;
+            *reinterpret_cast<uint4 *>(sv + (u / (D / 8)) * KP + 8 * (u % (D / 8))) = vt[i];
+        }
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) s = mfma16(ka[c], qop[c], s);
+        // this lane: keys t0 + 4grp + v of row col
+        float sc[4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int key = t0 + 4 * grp + v;
+            const bool vis = key < we && key <= hi && key >= lo;
+            sc[v] = vis ? s[v] * a.scale_log2 : -INFINITY;
+            tmax = fmaxf(tmax, sc[v]);
+        }
+        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+        const float mn = fmaxf(m, tmax);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        l *= corr;
+        if (__any(corr != 1.0f)) {
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b) o[b] *= corr;
+        }
+        float p[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
+            l += p[v];
+        }
+        // P = P_hi + P_lo in bf16 (as in the prefill kernel)
+        const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
+        const uint2 ph = make_uint2(h01, h23);
+        const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
+                                    pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) {
+            const uint2 va = lds_read_tr16(sv_lane + 16 * b);
+            o[b] = mfma16k16(va, pl, mfma16k16(va, ph, o[b]));
+        }
+    }
+    if (bad) a.err[0] = 1;
+    l = pair<OpSum, 32>(pair<OpSum, 16>(l));
+    // Workgroup merge: every wave puts its partial in LDS (over the tiles);
+    // wave w then merges rows w, w + kWaves, ... and writes the workgroup's
+    // partial of those rows (one partial per workgroup, as decode_kernel).
+    __syncthreads();  // every wave is done with its V tile
+    float *lds_part = reinterpret_cast<float *>(lds_raw);
+    if (rvalid) {  // columns >= rows (>= R when R = 8) hold no row of this wave
+        float *dst = lds_part + (wave * R + col) * D + 4 * grp;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b)
+            *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+        if (grp == 0) lds_ml[wave * R + col] = make_float2(m, l);
+    }
+    __syncthreads();
+    constexpr int EPL = D / 64;  // dims per lane
+    const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + blockIdx.x) * R;
+    for (int r = wave; r < R && r < rows; r += kWaves) {
+        float M = kNegBig;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
+        float L = 0.f, acc[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+            const float2 ml = lds_ml[w2 * R + r];
+            const float ww = __builtin_amdgcn_exp2f(ml.x - M);
+            L = fmaf(ml.y, ww, L);
+            const float *src = lds_part + (w2 * R + r) * D + lane * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[e] = fmaf(src[e], ww, acc[e]);
+        }
+        float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) dst[e] = acc[e];
+        if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+    }
+}
+
 // grid (kv_heads, n_items, chunks), 256 threads: G consecutive threads merge
 // one of the R*D outputs of an (item, kv head) from the partials
 // decode_kernel wrote; thread j of the G takes partials j, j + G, ... (at most
@@ -554,7 +774,7 @@ template <int D, int R, int G>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     constexpr int B = 16;
     const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
-    const int n_parts = DecodeLds<D, R>::kWgMerge ? a.n_split / kWaves : a.n_split;
+    const int n_parts = a.n_parts;
     const int Qn = a.qn;
     const int rows = a.group * Qn;
     const int t = blockIdx.z * 256 + threadIdx.x;
@@ -621,20 +841,12 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // with P split into two bf16 terms for the second product and everything
 // accumulated in fp32. MFMA lane layouts (16x16x32): A[row l%16][k 8(l/16)+j],
 // B[k 8(l/16)+j][col l%16], D[row 4(l/16)+v][col l%16].
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kPfKeys = 32;  // keys per LDS tile
 
 // Key (within a tile) of row i of S^T block b. Chosen so that lane group G
 // (lanes 16G..16G+15) ends up with the scores of keys 8G..8G+7 across the two
 // blocks, which are exactly the keys of its B operand in V^T P^T.
 __device__ __forceinline__ int pf_key(int b, int i) { return 8 * (i >> 2) + 4 * b + (i & 3); }
-
-__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-}
 
 // Calls f(integral_constant<int, u>) for u = U .. N-1: register arrays
 // indexed by u stay in registers.
@@ -1109,7 +1321,7 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
 // leaves each thread at most 16 partials.
 template <int HD, int RT>
 static hipError_t launch_merge(const DecodeArgs &a, hipStream_t s) {
-    const int parts = DecodeLds<HD, RT>::kWgMerge ? a.n_split / kWaves : a.n_split;
+    const int parts = a.n_parts;
     const int outs = a.group * a.qn * HD;
     auto go = [&](auto g) {
         constexpr int G = decltype(g)::value;
@@ -1142,6 +1354,26 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_merge<HD, RT>(a, s);
+}
+
+hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s) {
+    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves) return hipErrorInvalidValue;
+    dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
+    const int rt = rows_tile(rows_per_head);
+    auto go = [&](auto rc) -> hipError_t {
+        constexpr int RT = decltype(rc)::value;
+        KVRT_DISPATCH_D(head_dim, {
+            KVRT_DISPATCH_LAYOUT(a.kv.layout,
+                hipLaunchKernelGGL((decode_mfma_kernel<HD, RT, LY>), grid, block, 0, s, a));
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            return launch_merge<HD, RT>(a, s);
+        });
+        return hipErrorInvalidValue;
+    };
+    if (rt == 8) return go(std::integral_constant<int, 8>{});
+    if (rt == 16) return go(std::integral_constant<int, 16>{});
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s) {

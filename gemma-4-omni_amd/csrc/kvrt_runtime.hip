@@ -204,6 +204,16 @@ bool is_contiguous(const kvrt_tensor *t) {
 
 constexpr int kMaxWgPerHead = 64;
 
+// bf16 row tiles of 8 and 16 query rows per kv head take the MFMA decode
+// (KVRT_MFMA_DECODE=0 keeps them on the VALU kernel).
+bool use_mfma_decode(int dtype, int rows_tile_) {
+    static const bool enabled = [] {
+        const char *e = std::getenv("KVRT_MFMA_DECODE");
+        return !(e && e[0] == '0');
+    }();
+    return enabled && dtype == KVRT_BF16 && rows_tile_ >= kMfmaDecodeMinRows;
+}
+
 int target_wgs(const kvrt_config &cfg) {
     static const int v = env_int("KVRT_TARGET_WGS", 512);
     return cfg.decode_wgs > 0 ? cfg.decode_wgs : v;
@@ -551,7 +561,9 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
     }
     const int R = rows_tile(rows);
-    const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys, keys_per_iteration(D, R, s.dtype));
+    const bool mfma = !talker && use_mfma_decode(s.dtype, R);
+    const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys,
+                                      mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
     if (rc != KVRT_OK) return rc;
@@ -578,6 +590,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.window = s.window;
     a.n_split = n_split;
     a.advance = fused ? 1 : 0;
+    a.n_parts = (mfma || decode_wg_merge(D, R)) ? n_split / kWaves : n_split;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches += 2;
@@ -593,7 +606,9 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         }
         return KVRT_OK;
     }
-    if (launch_decode(a, D, s.dtype, rows, c->stream) != hipSuccess) return poison(c);
+    if ((mfma ? launch_decode_mfma(a, D, rows, c->stream) : launch_decode(a, D, s.dtype, rows, c->stream)) !=
+        hipSuccess)
+        return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
     for (int i = 0; i < n; ++i) {
         int &L = c->len_ref(slots[i], layer);
@@ -1399,12 +1414,14 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.group = group;
     a.qn = (int)qn;
     a.window = window;
+    const int R = rows_tile(rows);
+    const bool mfma = use_mfma_decode(KVRT_BF16, R);
     a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv,
                               window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
-                              keys_per_iteration((int)D, rows_tile(rows), KVRT_BF16));
+                              mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16));
+    a.n_parts = (mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = i;
-    const int R = rows_tile(rows);
     const size_t acc_elems = (size_t)n * hkv * a.n_split * R * D;
     const size_t bytes = (kTensorWsHead + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * R * 8;
     std::lock_guard<std::mutex> lock(g_tensor_ws.mu);
@@ -1428,7 +1445,8 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.err = reinterpret_cast<int32_t *>(g_tensor_ws.ptr);
     a.part_acc = g_tensor_ws.ptr + kTensorWsHead;
     a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + kTensorWsHead + ((acc_elems + 63) / 64) * 64);
-    if (launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream)) != hipSuccess)
+    if ((mfma ? launch_decode_mfma(a, (int)D, rows, static_cast<hipStream_t>(stream))
+              : launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream))) != hipSuccess)
         return KVRT_EDEVICE;
     return KVRT_OK;
 }

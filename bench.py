@@ -61,6 +61,8 @@ def parse() -> argparse.Namespace:
                    help="split-K decode workgroups per talker launch (kvrt_config.decode_wgs)")
     p.add_argument("--thinker-wgs", type=int, default=192,
                    help="split-K decode workgroups per thinker launch (kvrt_config.decode_wgs)")
+    p.add_argument("--decode-kernel", choices=("auto", "valu", "mfma"), default="auto",
+                   help="kernel for bf16 decodes of 8 or 16 query rows per kv head (kvrt_config.decode_kernel)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
@@ -87,8 +89,9 @@ def build_runtimes(args, capacity: int, n_slots: int):
     tk_specs = [LayerSpec(kv_heads=TALKER["hkv"], head_dim=TALKER["d"]) for _ in range(TALKER["layers"])]
     th_wgs = getattr(args, "thinker_wgs", 0) if args is not None else 0
     tk_wgs = getattr(args, "talker_wgs", 0) if args is not None else 0
-    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, decode_wgs=th_wgs, device="cuda")
-    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, decode_wgs=tk_wgs, device="cuda")
+    kern = getattr(args, "decode_kernel", "auto") if args is not None else "auto"
+    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, decode_wgs=th_wgs, decode_kernel=kern, device="cuda")
+    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, decode_wgs=tk_wgs, decode_kernel=kern, device="cuda")
     return thinker, talker
 
 
@@ -439,6 +442,7 @@ def main() -> int:
             "hip_streams": 1 if args.one_stream else 2 * args.groups,
             "tokens_per_step": tokens_per_step,
             "decode_wgs": {"talker": args.talker_wgs, "thinker": args.thinker_wgs},
+            "decode_kernel": args.decode_kernel,
         },
         "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
         "step_hbm_frac": round(total_bytes / elapsed / HBM_PEAK, 4),

@@ -204,14 +204,14 @@ bool is_contiguous(const kvrt_tensor *t) {
 
 constexpr int kMaxWgPerHead = 64;
 
-// bf16 row tiles of 8 and 16 query rows per kv head take the MFMA decode
-// (KVRT_MFMA_DECODE=0 keeps them on the VALU kernel).
-bool use_mfma_decode(int dtype, int rows_tile_) {
-    static const bool enabled = [] {
-        const char *e = std::getenv("KVRT_MFMA_DECODE");
-        return !(e && e[0] == '0');
-    }();
-    return enabled && dtype == KVRT_BF16 && rows_tile_ >= kMfmaDecodeMinRows;
+// Which bf16 decodes run on the MFMA kernel (kvrt_config.decode_kernel).
+// AUTO: 16 query rows per kv head (GQA group 8 with Q = 2), and 8 rows at
+// head_dim 512 — the shapes where the VALU kernel's dot products and P.V
+// products make it compute-bound. 8 rows at head_dim <= 256 stay on the VALU
+// kernel, which is as fast there and lighter on a concurrent stream.
+bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim) {
+    if (mode == KVRT_DECODE_VALU || dtype != KVRT_BF16 || rows_tile_ < kMfmaDecodeMinRows) return false;
+    return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512;
 }
 
 int target_wgs(const kvrt_config &cfg) {
@@ -373,7 +373,7 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     if (cfg->struct_size != sizeof(kvrt_config)) return KVRT_EINVAL;
     if (cfg->n_layers <= 0 || cfg->n_layers > 4096 || cfg->n_slots <= 0 || cfg->n_slots > (1 << 20) ||
         cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 65536 || cfg->decode_wgs < 0 ||
-        cfg->decode_wgs > 65536)
+        cfg->decode_wgs > 65536 || cfg->decode_kernel < KVRT_DECODE_AUTO || cfg->decode_kernel > KVRT_DECODE_MFMA)
         return KVRT_EINVAL;
     bool any_paged = false;
     for (int i = 0; i < cfg->n_layers; ++i) {
@@ -561,7 +561,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
     }
     const int R = rows_tile(rows);
-    const bool mfma = !talker && use_mfma_decode(s.dtype, R);
+    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D);
     const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
@@ -1415,7 +1415,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.qn = (int)qn;
     a.window = window;
     const int R = rows_tile(rows);
-    const bool mfma = use_mfma_decode(KVRT_BF16, R);
+    const bool mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D);
     a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv,
                               window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
                               mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16));

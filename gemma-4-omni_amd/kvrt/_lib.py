@@ -67,6 +67,11 @@ class KvrtLayerSpec(ctypes.Structure):
     ]
 
 
+# kvrt_config.decode_kernel (kvrt.h KVRT_DECODE_*)
+KVRT_DECODE_AUTO, KVRT_DECODE_VALU, KVRT_DECODE_MFMA = 0, 1, 2
+DECODE_KERNELS = {"auto": KVRT_DECODE_AUTO, "valu": KVRT_DECODE_VALU, "mfma": KVRT_DECODE_MFMA}
+
+
 class KvrtConfig(ctypes.Structure):
     _fields_ = [
         ("struct_size", c_uint32),
@@ -78,6 +83,7 @@ class KvrtConfig(ctypes.Structure):
         ("max_q", c_int32),
         ("pool_seed", c_int32),
         ("decode_wgs", c_int32),
+        ("decode_kernel", c_int32),
     ]
 
 

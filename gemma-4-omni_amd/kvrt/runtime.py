@@ -160,6 +160,7 @@ class KVRuntime:
         pool_pages: int = 0,
         pool_seed: int = 0,
         decode_wgs: int = 0,
+        decode_kernel: str = "auto",
         device: torch.device | str | None = None,
     ) -> None:
         self.lib = L.load()
@@ -185,6 +186,9 @@ class KVRuntime:
         cfg.max_q = self.max_q
         cfg.pool_seed = int(pool_seed)
         cfg.decode_wgs = int(decode_wgs)
+        if decode_kernel not in L.DECODE_KERNELS:
+            raise ValueError(f"decode_kernel must be one of {sorted(L.DECODE_KERNELS)}, got {decode_kernel!r}")
+        cfg.decode_kernel = L.DECODE_KERNELS[decode_kernel]
         self._cfg = cfg
         specs = (L.KvrtLayerSpec * len(self.layers))(*[s.to_c() for s in self.layers])
         self._specs = specs

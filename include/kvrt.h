@@ -120,7 +120,17 @@ typedef struct kvrt_config {
                              (0 = 512, or KVRT_TARGET_WGS). Contexts whose
                              launches run beside another model's on a second
                              stream do better with fewer (e.g. 192)          */
+    int32_t decode_kernel; /* KVRT_DECODE_*: which kernel runs bf16 decodes of
+                             8 or 16 query rows per kv head                   */
 } kvrt_config;
+
+/* kvrt_config.decode_kernel. AUTO: MFMA for 16 rows per kv head and for 8 rows
+ * at head_dim 512, the VALU kernel otherwise. VALU / MFMA force one kernel for
+ * every eligible decode (MFMA: bf16, 8 or 16 rows per kv head, not the talker
+ * masks; other decodes always run on the VALU kernel). */
+#define KVRT_DECODE_AUTO 0
+#define KVRT_DECODE_VALU 1
+#define KVRT_DECODE_MFMA 2
 
 /* Optional caller-owned storage for one layer (kvrt_create_with_storage).
  * Sizes must equal kvrt_layer_storage_bytes for that layer. */

@@ -108,21 +108,26 @@ def test_import_and_truncate_move_no_bytes():
     assert rt.counters()["truncations"] == 1
 
 
-@pytest.mark.parametrize(
-    "hq,hkv,d,qn,window,layout",
-    [
-        (16, 8, 128, 1, 0, "contig"),   # talker shape
-        (16, 8, 128, 2, 0, "contig"),
-        (8, 1, 256, 1, 0, "contig"),    # thinker global shape
-        (8, 1, 256, 2, 64, "ring"),     # thinker sliding shape, Q=2
-        (8, 1, 256, 1, 64, "ring"),
-        (8, 8, 128, 2, 0, "contig"),    # listener micro-batch shape (g=1)
-        (8, 1, 512, 2, 0, "contig"),    # real Gemma full layers (D=512)
-        (16, 8, 128, 1, 0, "paged"),
-        (4, 2, 64, 3, 0, "contig"),     # odd Q: rows tile padding
-    ],
-)
-def test_decode_attention_matches_oracle(hq, hkv, d, qn, window, layout):
+_DECODE_SHAPES = [
+    (16, 8, 128, 1, 0, "contig"),   # talker shape
+    (16, 8, 128, 2, 0, "contig"),
+    (8, 1, 256, 1, 0, "contig"),    # thinker global shape
+    (8, 1, 256, 2, 64, "ring"),     # thinker sliding shape, Q=2
+    (8, 1, 256, 1, 64, "ring"),
+    (8, 8, 128, 2, 0, "contig"),    # listener micro-batch shape (g=1)
+    (8, 1, 512, 2, 0, "contig"),    # real Gemma full layers (D=512)
+    (8, 1, 512, 1, 0, "contig"),
+    (16, 8, 128, 1, 0, "paged"),
+    (4, 2, 64, 3, 0, "contig"),     # odd Q: rows tile padding
+]
+# g * Q of 8 or 16 rows per kv head has two kernels (decode_kernel="auto"
+# picks one by shape): run those shapes on each, forced.
+_DECODE_CASES = [s + ("auto",) for s in _DECODE_SHAPES] + [
+    s + (kern,) for s in _DECODE_SHAPES if (s[0] // s[1]) * s[3] in (8, 16) for kern in ("valu", "mfma")]
+
+
+@pytest.mark.parametrize("hq,hkv,d,qn,window,layout,kernel", _DECODE_CASES)
+def test_decode_attention_matches_oracle(hq, hkv, d, qn, window, layout, kernel):
     from kvrt import LayerSpec
 
     gen = torch.Generator().manual_seed(hq * 131 + d + qn)
@@ -134,7 +139,7 @@ def test_decode_attention_matches_oracle(hq, hkv, d, qn, window, layout):
         kw = dict(block_size=16, pool_pages=256)
     else:
         spec = LayerSpec(kv_heads=hkv, head_dim=d, window=window)
-    rt = _rt([spec], n_slots=4, capacity=1024, max_q=4, **kw)
+    rt = _rt([spec], n_slots=4, capacity=1024, max_q=4, decode_kernel=kernel, **kw)
     orc = O.OracleCache(_oracle_layers([spec]), 4)
     slots = [3, 1, 0]
     lens = [517, 33, 200]
@@ -323,15 +328,16 @@ def test_error_paths_fail_closed_and_poison():
     assert rt.health() == -4
 
 
-@pytest.mark.parametrize("hq,hkv,d,length", [(16, 1, 512, 16000), (16, 8, 128, 16000), (8, 1, 256, 9000)])
-def test_many_splits_long_context(hq, hkv, d, length):
+@pytest.mark.parametrize("hq,hkv,d,length,kernel", [(16, 1, 512, 16000, "auto"), (16, 8, 128, 16000, "auto"),
+                                                   (8, 1, 256, 9000, "valu"), (8, 1, 256, 9000, "mfma")])
+def test_many_splits_long_context(hq, hkv, d, length, kernel):
     """One stream, long context: the split count hits its cap (64 workgroups
     per kv head; 256 wave partials when the workgroup merge is off)."""
     from kvrt import LayerSpec
 
     gen = torch.Generator().manual_seed(length + d)
     spec = LayerSpec(kv_heads=hkv, head_dim=d)
-    rt = _rt([spec], n_slots=1, capacity=length + 4, max_q=1)
+    rt = _rt([spec], n_slots=1, capacity=length + 4, max_q=1, decode_kernel=kernel)
     orc = O.OracleCache(_oracle_layers([spec]), 1)
     k = randn_bf16(gen, (1, hkv, length, d))
     v = randn_bf16(gen, (1, hkv, length, d))

@@ -25,6 +25,29 @@ constexpr int kMaxInt8Rows = 8;      // query rows per kv head of an INT8 decode
 // whose query rows and accumulators take the registers.
 constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
 
+// bf16 CONTIG / RING decodes of <= 4 rows per kv head stream K/V straight
+// into LDS (global_load_lds_dwordx4) through a ring of kDmaStages stages of
+// kDmaUnroll key groups per wave, so the next stages stay in flight while a
+// wave computes on the current one without holding registers for them.
+#ifndef KVRT_DMA_UNROLL
+#define KVRT_DMA_UNROLL 3
+#endif
+#ifndef KVRT_DMA_STAGES
+#define KVRT_DMA_STAGES 2
+#endif
+#ifndef KVRT_DECODE_DMA
+#define KVRT_DECODE_DMA 1
+#endif
+constexpr int kDmaUnroll = KVRT_DMA_UNROLL;
+constexpr int kDmaStages = KVRT_DMA_STAGES;
+constexpr bool decode_dma(int R, int dtype, int layout) {
+    return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= 4;
+}
+// Key groups per main-loop pass of decode_kernel.
+constexpr int decode_unroll(int R, int dtype, int layout) {
+    return decode_dma(R, dtype, layout) ? kDmaUnroll : keys_unroll(R);
+}
+
 // Where the rows of one layer live. Row (slot, head, pos) starts at element
 //   CONTIG: slot*slot_stride + head*head_stride + pos*row_stride
 //   RING:   slot*slot_stride + head*head_stride + (pos % rows)*row_stride
@@ -240,6 +263,6 @@ hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s);
 // Smallest instantiated row tile >= rows (1, 2, 4, 8, 16); 0 if too large.
 int rows_tile(int rows);
 // Keys one wave consumes per main-loop iteration of decode_kernel.
-int keys_per_iteration(int head_dim, int rows_tile, int dtype);
+int keys_per_iteration(int head_dim, int rows_tile, int dtype, int layout);
 
 }  // namespace kvrt

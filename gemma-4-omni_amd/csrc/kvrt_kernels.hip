@@ -214,6 +214,41 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 // ---------------------------------------------------------------------------
 // decode attention (split-K)
 // ---------------------------------------------------------------------------
+// LDS DMA: global_load_lds_dwordx4 moves lane l's 16 bytes at g to LDS byte
+// lds + 16 * l without passing through registers. It is issued from inline
+// assembly that sets M0 in the same statement, so the compiler neither tracks
+// these loads nor inserts its own (all-or-nothing) waits for them: the decode
+// waits with explicit vmcnt waits — vector loads complete in issue order, so
+// vmcnt(N) means every DMA but the N most recent has landed — and reads the
+// LDS back only after such a wait. The kernels using it set M0 nowhere else.
+__device__ __forceinline__ void dma_load16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most n * STEP vector memory operations are outstanding,
+// n in [0, NMAX] (wave-uniform).
+template <int STEP, int NMAX>
+__device__ __forceinline__ void wait_vmem_steps(int n) {
+    if constexpr (NMAX > 0) {
+        if (n >= NMAX) {
+            wait_vmem<NMAX * STEP>();
+            return;
+        }
+        wait_vmem_steps<STEP, NMAX - 1>(n);
+    } else {
+        wait_vmem<0>();
+    }
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class T>
+__device__ __forceinline__ uint32_t lds_addr(const T *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T *)p;
+}
+
 // LDS floats a decode workgroup needs for its cross-wave merge: the partials
 // of waves 1..3, when R * D is small enough to stage them.
 template <int D, int R>
@@ -230,6 +265,14 @@ struct DecodeLds {
 // (row r = j*Q + i for q head kvh*g + j, query i).
 // Args is DecodeArgs (causal / sliding-window visibility) or TalkerArgs (the
 // talker's per-item prefix / audio ranges, bf16 CONTIG layers only).
+//
+// K/V reach the waves in one of two ways. DMA (bf16 CONTIG / RING, R <= 4):
+// every wave streams its key range through its own LDS ring of kDmaStages
+// stages x U key groups (K and V, 1 KiB each per group) plus its q rows; at
+// pass p it waits for stage p, reads it into registers, refills it with pass
+// p + kDmaStages and computes, so kDmaStages - 1 stages stay in flight during
+// the arithmetic. Otherwise (int8, PAGED, more rows): a pass loads its U
+// groups straight into registers, all before the first is used.
 template <int D, int R, int KDT, int LAYOUT, class Args = DecodeArgs>
 __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     constexpr bool TALK = !std::is_same<Args, DecodeArgs>::value;
@@ -237,9 +280,15 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     constexpr int VEC = (KDT == KVRT_INT8) ? 16 : 8;
     constexpr int LPR = D / VEC;
     constexpr int KPW = 64 / LPR;
-    constexpr int U = keys_unroll(R);
+    constexpr bool DMA = decode_dma(R, KDT, LAYOUT);
+    constexpr int U = decode_unroll(R, KDT, LAYOUT);
     constexpr int QW = VEC / 2;  // packed bf16 pairs of q per lane and row
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad head_dim");
+    constexpr int STG = kDmaStages;
+    constexpr int QI = (R * LPR + 63) / 64;                  // q DMA instructions per wave
+    constexpr int WAVE_BYTES = DMA ? (STG * U * 2 + QI) * 1024 : 16;
+    static_assert(!DMA || (STG >= 1 && 2 * U * STG < 64), "DMA ring: outstanding loads fit vmcnt");
+    static_assert(!DMA || R * D * 4 <= WAVE_BYTES, "DMA ring holds the wave's partial");
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -300,6 +349,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int hq = hkv * a.group;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+        if constexpr (DMA) break;  // staged through LDS below
         if (r < rows) {
             const int j = r / Qn, i = r % Qn;
             const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + seg * VEC;
@@ -356,15 +406,83 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
 
     const int64_t new_base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * VEC;
     bool bad = false;  // a visible key on an unmapped page (PAGED)
-    for (int base = ws; base < we; base += KPW * U) {
+    const int npass = we > ws ? (we - ws + KPW * U - 1) / (KPW * U) : 0;
+    __shared__ __align__(16) u32x4_t dma_lds[DMA ? kWaves * WAVE_BYTES / 16 : 1];
+    // this wave's LDS: q rows (QI KiB), then STG stages of U x (K, V) KiB
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t ring = lds_addr(dma_lds) + wave_u * WAVE_BYTES;
+    const u32x4_t *ring_v = dma_lds + wave_u * (WAVE_BYTES / 16);
+    // DMA of the U key groups of pass p into stage st (same addressing and
+    // clamping as the register load below; CONTIG / RING rows always exist).
+    auto dma_pass = [&](int p, int st) __attribute__((always_inline)) {
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(ring + (QI + st * U * 2) * 1024);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kk = ws + p * KPW * U + u * KPW + sub;
+            const int kc = kk < we ? kk : ws;
+            const int64_t o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            const uint16_t *kp = static_cast<const uint16_t *>(a.kv.k) + o + seg * VEC;
+            const uint16_t *vp = static_cast<const uint16_t *>(a.kv.v) + o + seg * VEC;
+            if (fused) {
+                const bool nw = kc >= len;
+                const int64_t on = new_base + (int64_t)(kc - len) * D;
+                kp = nw ? a.k_new + on : kp;
+                vp = nw ? a.v_new + on : vp;
+            }
+            dma_load16(kp, dst + u * 2048);
+            dma_load16(vp, dst + u * 2048 + 1024);
+        }
+    };
+    if constexpr (DMA) {
+        // q first (row r = e / LPR of element chunk e = t*64 + lane; rows past
+        // the tile's real rows read row 0), then the first STG passes.
+#pragma unroll
+        for (int t = 0; t < QI; ++t) {
+            const int e = t * 64 + lane;
+            int r = e / LPR;
+            r = r < rows ? r : 0;
+            const int j = r / Qn, i = r % Qn;
+            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + (e % LPR) * VEC;
+            dma_load16(qp, __builtin_amdgcn_readfirstlane(ring + t * 1024));
+        }
+        const int pro = min(STG, npass);
+        for (int p = 0; p < pro; ++p) dma_pass(p, p);
+        wait_vmem_steps<2 * U, STG>(pro);  // q has landed
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4_t x = ring_v[r * LPR + seg];
+            qw[r][0] = x[0]; qw[r][1] = x[1]; qw[r][2] = x[2]; qw[r][3] = x[3];
+            if (r >= rows) qw[r][0] = qw[r][1] = qw[r][2] = qw[r][3] = 0u;
+        }
+    }
+    for (int p = 0; p < npass; ++p) {
+        const int base = ws + p * KPW * U;
+        uint4 kx[U], vx[U];
+        float ksc[U], vsc[U];
+        int key[U];
+        if constexpr (DMA) {
+            // stage p: wait for it (the later passes stay in flight), read it,
+            // then refill the stage with pass p + STG before computing
+            const int st = p % STG;
+            wait_vmem_steps<2 * U, STG - 1>(min(STG - 1, npass - 1 - p));
+            const u32x4_t *sv = ring_v + (QI * 1024 + st * U * 2048) / 16;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const u32x4_t x = sv[u * 128 + lane], y = sv[u * 128 + 64 + lane];
+                kx[u] = make_uint4(x[0], x[1], x[2], x[3]);
+                vx[u] = make_uint4(y[0], y[1], y[2], y[3]);
+                const int kk = base + u * KPW + sub;
+                key[u] = kk < we ? kk : 0x7fffffff;
+                ksc[u] = vsc[u] = 0.f;
+            }
+            wait_lds();
+            if (p + STG < npass) dma_pass(p + STG, st);
+        } else {
         // Load phase, branch-free so that all 2U loads issue back to back:
         // a key past the wave's range (or on an unmapped page) reads a valid
         // row instead (the wave's first key / pool page 0) and is masked out
         // of the softmax; fused rows >= len come from the new K/V by an
         // address select.
-        uint4 kx[U], vx[U];
-        float ksc[U], vsc[U];
-        int key[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kk = base + u * KPW + sub;
@@ -395,6 +513,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 ksc[u] = a.kv.ks[o / D];
                 vsc[u] = a.kv.vs[o / D];
             }
+        }
         }
         // scores (log2 domain)
         float s[U][R];
@@ -469,6 +588,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         }
     }
 
+    if constexpr (DMA) wait_vmem<0>();  // every DMA of this wave has landed (q too)
     if (bad) a.err[0] = 1;
 
     // merge the KPW key sub-groups of the wave (lanes LPR apart)
@@ -484,8 +604,12 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         }
     }
     using Lds = DecodeLds<D, R>;
-    __shared__ __align__(16) float lds[Lds::kFloats];
+    __shared__ __align__(16) float lds_own[DMA ? 1 : Lds::kFloats];
     __shared__ float2 lds_ml[kWaves * R];
+    // a wave's partial: its own slice of lds_own, or (DMA) its own ring, which
+    // it no longer reads or loads into
+    float *lds = DMA ? reinterpret_cast<float *>(dma_lds) : lds_own;
+    constexpr int PST = DMA ? WAVE_BYTES / 4 : R * D;  // floats between waves' partials
     if constexpr (Lds::kWgMerge) {
         // Workgroup merge: every wave puts its partial in LDS; wave w then
         // merges rows w, w + kWaves, ... over the kWaves partials (64 lanes
@@ -493,7 +617,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         if (sub == 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float4 *dst = reinterpret_cast<float4 *>(lds + (wave * R + r) * D + seg * VEC);
+                float4 *dst = reinterpret_cast<float4 *>(lds + wave * PST + r * D + seg * VEC);
 #pragma unroll
                 for (int t = 0; t < VEC / 4; ++t)
                     dst[t] = make_float4(acc[r][4 * t], acc[r][4 * t + 1], acc[r][4 * t + 2], acc[r][4 * t + 3]);
@@ -515,7 +639,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 const float2 ml = lds_ml[w2 * R + r];
                 const float ww = __builtin_amdgcn_exp2f(ml.x - M);
                 L = fmaf(ml.y, ww, L);
-                const float *src = lds + (w2 * R + r) * D + lane * EPL;
+                const float *src = lds + w2 * PST + r * D + lane * EPL;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) o[e] = fmaf(src[e], ww, o[e]);
             }
@@ -1258,10 +1382,10 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
 // ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
-int keys_per_iteration(int head_dim, int rows_tile_, int dtype) {
+int keys_per_iteration(int head_dim, int rows_tile_, int dtype, int layout) {
     const int vec = dtype == KVRT_INT8 ? 16 : 8;
     const int kpw = 64 / (head_dim / vec);
-    return kpw * keys_unroll(rows_tile_);
+    return kpw * decode_unroll(rows_tile_, dtype, layout);
 }
 
 int rows_tile(int rows) {

@@ -563,7 +563,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int R = rows_tile(rows);
     const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D);
     const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys,
-                                      mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype));
+                                      mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
     if (rc != KVRT_OK) return rc;
@@ -1418,7 +1418,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     const bool mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D);
     a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv,
                               window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
-                              mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16));
+                              mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
     a.n_parts = (mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = i;

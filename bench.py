@@ -66,9 +66,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
-    p.add_argument("--mode", choices=("step", "prefill"), default="step",
+    p.add_argument("--mode", choices=("step", "prefill", "kernels"), default="step",
                    help="step: the north-star decode step (default); prefill: the MFMA chunked-prefill "
-                        "attention at thinker/talker shapes (one JSON line of per-case TFLOP/s)")
+                        "attention at thinker/talker shapes (one JSON line of per-case TFLOP/s); kernels: each "
+                        "hot-path kernel alone at a BASELINE config shape against the HBM roofline")
     return p.parse_args()
 
 
@@ -339,6 +340,134 @@ def run_prefill(args) -> int:
     return 0
 
 
+def _event_median(fn, warmup: int, reps: int) -> float:
+    """Median seconds of fn's GPU work: HIP events around each call on the
+    current stream, after a GPU sleep so the host enqueues the whole call
+    before the GPU reaches it."""
+    times = []
+    for _ in range(warmup + reps):
+        torch.cuda._sleep(1_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3)
+    t = sorted(times[warmup:])
+    return t[len(t) // 2]
+
+
+def run_kernels(args) -> int:
+    """Each hot-path kernel at a BASELINE configuration shape, timed alone
+    (median of HIP-event-timed launches) against the HBM roofline.
+
+    Algorithmic bytes: K/V rows read or written once, sources read once,
+    q/out once, masks once (no padding or repeat traffic)."""
+    from kvrt import KVRuntime, LayerSpec
+
+    torch.manual_seed(0)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    res = []
+
+    def bf(shape, scale=1.0):
+        return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16)
+
+    def add(name, kernel, t, nbytes, shape):
+        res.append({"case": name, "kernel": kernel, "shape": shape, "us": round(t * 1e6, 2),
+                    "bytes": int(nbytes), "gbps": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / HBM_PEAK, 4)})
+
+    w, r = args.warmup, args.steps
+    # import (append_kernel, host position): one talker layer, 4 streams x [8, 8192, 128]
+    rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)], 4, 8192 + 64, max_q=1, device="cuda")
+    kv = [bf((1, 8, 8192, 128)) for _ in range(2)]
+    add("import_talker_8192", "append_kernel<128,bf16,contig> (import)",
+        _event_median(lambda: rt.import_(0, 0, kv[0], kv[1]), w, r), 4 * 8 * 8192 * 128 * 2, "[1,8,8192,128] x K,V")
+    # per-frame append (device cursor): 4 streams x 1 row x 8 heads
+    for s in range(4):
+        rt.import_(s, 0, kv[0][:, :, :4096], kv[1][:, :, :4096])
+    k1, v1 = bf((4, 8, 1, 128)), bf((4, 8, 1, 128))
+
+    add("append_frame_talker", "append_kernel<128,bf16,contig> (device cursor)",
+        _event_median(lambda: rt.append(0, k1, v1, [0, 1, 2, 3]), w, min(r, 50)), 4 * 8 * 128 * 2 * 4,
+        "4 streams x [8,1,128] x K,V (latency-bound)")
+    rt.close()
+
+    # listener micro-batch gather (config 3): N = 4, L ~ U[64, 1024], 8 heads, D 128
+    g2 = torch.Generator().manual_seed(2)
+    lens = [int(x) for x in torch.randint(64, 1025, (4,), generator=g2)]
+    rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)], 4, 1100, max_q=2, device="cuda")
+    for s, n in enumerate(lens):
+        rt.import_(s, 0, bf((1, 8, n, 128)), bf((1, 8, n, 128)))
+    lmax = max(lens)
+    ok = torch.empty((4, 8, lmax, 128), dtype=torch.bfloat16, device="cuda")
+    ov = torch.empty_like(ok)
+    add("gather_listener_n4", "gather_kernel<128,bf16,contig>",
+        _event_median(lambda: rt.gather(0, [0, 1, 2, 3], out=(ok, ov)), w, r),
+        sum(lens) * 8 * 128 * 2 * 2 + 4 * lmax * 8 * 128 * 2 * 2 + 4 * lmax, f"N=4, L={lens} -> [4,8,{lmax},128] + mask")
+    rt.close()
+
+    # decode attention (fused append + attend where the layout allows)
+    def decode_case(name, kernel, hq, hkv, d, n, L, qn=1, window=0, layout="contig", fused=True, dtype="bf16",
+                    lens=None, **kw):
+        rr = window + qn - 1 if layout == "ring" else 0
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window, ring_rows=rr, dtype=dtype)
+        lens = lens or [L] * n
+        cap = max(lens) + w + r + 64
+        rt = KVRuntime([spec], n, cap, max_q=qn, device="cuda", decode_wgs=args.talker_wgs, **kw)
+        for s, ln in enumerate(lens):
+            first = max(0, ln - window + 1) if layout == "paged" and window else 0
+            kk = torch.zeros((1, hkv, ln, d), dtype=torch.bfloat16, device="cuda")
+            kk[:, :, first:] = bf((1, hkv, ln - first, d))
+            rt.import_(s, 0, kk, kk, first_pos=first)
+        q = bf((n, hq, qn, d), 0.5)
+        kn, vn = bf((n, hkv, qn, d), 0.5), bf((n, hkv, qn, d), 0.5)
+        o = torch.empty_like(q)
+        slots = list(range(n))
+        sc = 1.0 / math.sqrt(d)
+        if fused:
+            fn = lambda: rt.append_attend(0, q, kn, vn, slots, sc, out=o)  # noqa: E731
+        else:
+            fn = lambda: rt.attend(0, q, slots, sc, out=o)  # noqa: E731
+        t = _event_median(fn, w, r)
+        if rt.health() != 0:
+            raise RuntimeError(f"kvrt health check failed in kernel case {name}")
+        row = hkv * d * (1 if dtype == "int8" else 2) + (hkv * 4 if dtype == "int8" else 0)  # K or V bytes per position
+        after = [ln + (qn if fused else 0) for ln in lens]  # length the queries see
+        vis = sum(min(la, window + qn - 1) if window else la for la in after)
+        nbytes = 2 * row * vis + 2 * n * hq * qn * d * 2 + (2 * n * hkv * qn * d * 2 * 2 if fused else 0)
+        add(name, kernel, t, nbytes, f"{n} streams, Hq {hq} / Hkv {hkv}, D {d}, Q {qn}, " +
+            (f"window {window}, " if window else "") + f"{layout} {dtype}, L {'~' if len(set(lens)) > 1 else ''}"
+            f"{sum(lens) // len(lens)}")
+        rt.close()
+
+    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring) + merge", 16, 8, 128, 4, 4096)
+    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig> + merge", 8, 1, 256, 4, 4096)
+    decode_case("decode_thinker_sliding", "decode_kernel<256,8,bf16,ring> + merge", 8, 1, 256, 4, 4096,
+                window=512, layout="ring")
+    decode_case("decode_listener_q2_d512", "decode_mfma_kernel<512,16,contig> + merge", 8, 1, 512, 4, 8192, qn=2)
+    g4 = torch.Generator().manual_seed(4)
+    lens5 = [int(x) for x in torch.randint(256, 8193, (16,), generator=g4)]
+    decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> + merge (attend only)", 16, 8, 128, 16, 0,
+                window=4096, layout="paged", fused=False, dtype="int8", lens=lens5, block_size=16,
+                pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
+
+    # slot lifecycle: clone a 4096-position talker session (28 layers, one launch)
+    rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)] * 28, 2, 4096 + 64, max_q=1, device="cuda")
+    for layer in range(28):
+        rt.import_(0, layer, kv[0][:, :, :4096], kv[1][:, :, :4096])
+    add("copy_prefix_talker", "slot_copy_kernel (28 layers)",
+        _event_median(lambda: rt.copy_prefix(0, 1, 4096), w, min(r, 20)), 2 * 28 * 8 * 4096 * 128 * 2 * 2,
+        "28 layers x [8,4096,128] x K,V")
+    rt.close()
+
+    best = max(res, key=lambda x: x["frac"])
+    print(json.dumps({
+        "metric": "hot-path kernels vs the HBM roofline (GB/s), 1 MI355X", "value": best["gbps"], "unit": "GB/s",
+        "n_gpus": 1, "steps": r, "warmup": w, "higher_is_better": True, "dtype": "bf16/int8", "data": "synthetic",
+        "roofline": {"bound": "hbm", "peak": HBM_PEAK / 1e9, "unit": "GB/s"}, "cases": res}))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -351,6 +480,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.mode == "prefill":
         return run_prefill(args)
+    if args.mode == "kernels":
+        return run_kernels(args)
     gen = torch.Generator(device="cuda").manual_seed(1)
     margin = args.warmup + args.steps + args.kernel_reps + 8
     capacity = args.ctx + margin

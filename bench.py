@@ -408,12 +408,12 @@ def run_kernels(args) -> int:
 
     # decode attention (fused append + attend where the layout allows)
     def decode_case(name, kernel, hq, hkv, d, n, L, qn=1, window=0, layout="contig", fused=True, dtype="bf16",
-                    lens=None, **kw):
+                    lens=None, wgs=0, **kw):
         rr = window + qn - 1 if layout == "ring" else 0
         spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window, ring_rows=rr, dtype=dtype)
         lens = lens or [L] * n
         cap = max(lens) + w + r + 64
-        rt = KVRuntime([spec], n, cap, max_q=qn, device="cuda", decode_wgs=args.talker_wgs, **kw)
+        rt = KVRuntime([spec], n, cap, max_q=qn, device="cuda", decode_wgs=wgs, **kw)
         for s, ln in enumerate(lens):
             first = max(0, ln - window + 1) if layout == "paged" and window else 0
             kk = torch.zeros((1, hkv, ln, d), dtype=torch.bfloat16, device="cuda")
@@ -440,10 +440,14 @@ def run_kernels(args) -> int:
             f"{sum(lens) // len(lens)}")
         rt.close()
 
-    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring) + merge", 16, 8, 128, 4, 4096)
-    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig> + merge", 8, 1, 256, 4, 4096)
+    # the north-star step's talker and thinker launches at the step's workgroup targets; the
+    # other shapes at the runtime default (kvrt_config.decode_wgs = 0)
+    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring) + merge", 16, 8, 128, 4, 4096,
+                wgs=args.talker_wgs)
+    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig> + merge", 8, 1, 256, 4, 4096,
+                wgs=args.thinker_wgs)
     decode_case("decode_thinker_sliding", "decode_kernel<256,8,bf16,ring> + merge", 8, 1, 256, 4, 4096,
-                window=512, layout="ring")
+                window=512, layout="ring", wgs=args.thinker_wgs)
     decode_case("decode_listener_q2_d512", "decode_mfma_kernel<512,16,contig> + merge", 8, 1, 512, 4, 8192, qn=2)
     g4 = torch.Generator().manual_seed(4)
     lens5 = [int(x) for x in torch.randint(256, 8193, (16,), generator=g4)]

@@ -40,12 +40,20 @@ constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
 #endif
 constexpr int kDmaUnroll = KVRT_DMA_UNROLL;
 constexpr int kDmaStages = KVRT_DMA_STAGES;
-constexpr bool decode_dma(int R, int dtype, int layout) {
-    return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= 4;
+// Bytes of one wave's ring: q rows (ceil(R * D/8 / 64) KiB) + stages x groups x (K, V).
+constexpr int dma_wave_bytes(int R, int head_dim) {
+    return (kDmaStages * kDmaUnroll * 2 + (R * (head_dim / 8) + 63) / 64) * 1024;
+}
+// The rings of a workgroup stay inside the first 64 KiB of LDS (the range an
+// M0-addressed LDS DMA is known to reach), with 1 KiB left for the merge's
+// (m, l) table.
+constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
+    return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= 4 &&
+           kWaves * dma_wave_bytes(R, head_dim) <= 64 * 1024 - 1024;
 }
 // Key groups per main-loop pass of decode_kernel.
-constexpr int decode_unroll(int R, int dtype, int layout) {
-    return decode_dma(R, dtype, layout) ? kDmaUnroll : keys_unroll(R);
+constexpr int decode_unroll(int R, int dtype, int layout, int head_dim) {
+    return decode_dma(R, dtype, layout, head_dim) ? kDmaUnroll : keys_unroll(R);
 }
 
 // Where the rows of one layer live. Row (slot, head, pos) starts at element

@@ -280,13 +280,14 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     constexpr int VEC = (KDT == KVRT_INT8) ? 16 : 8;
     constexpr int LPR = D / VEC;
     constexpr int KPW = 64 / LPR;
-    constexpr bool DMA = decode_dma(R, KDT, LAYOUT);
-    constexpr int U = decode_unroll(R, KDT, LAYOUT);
+    constexpr bool DMA = decode_dma(R, KDT, LAYOUT, D);
+    constexpr int U = decode_unroll(R, KDT, LAYOUT, D);
     constexpr int QW = VEC / 2;  // packed bf16 pairs of q per lane and row
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad head_dim");
     constexpr int STG = kDmaStages;
     constexpr int QI = (R * LPR + 63) / 64;                  // q DMA instructions per wave
-    constexpr int WAVE_BYTES = DMA ? (STG * U * 2 + QI) * 1024 : 16;
+    constexpr int WAVE_BYTES = DMA ? dma_wave_bytes(R, D) : 16;
+    static_assert(!DMA || WAVE_BYTES == (STG * U * 2 + QI) * 1024, "ring layout");
     static_assert(!DMA || (STG >= 1 && 2 * U * STG < 64), "DMA ring: outstanding loads fit vmcnt");
     static_assert(!DMA || R * D * 4 <= WAVE_BYTES, "DMA ring holds the wave's partial");
 
@@ -1385,7 +1386,7 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
 int keys_per_iteration(int head_dim, int rows_tile_, int dtype, int layout) {
     const int vec = dtype == KVRT_INT8 ? 16 : 8;
     const int kpw = 64 / (head_dim / vec);
-    return kpw * decode_unroll(rows_tile_, dtype, layout);
+    return kpw * decode_unroll(rows_tile_, dtype, layout, head_dim);
 }
 
 int rows_tile(int rows) {

@@ -119,6 +119,12 @@ _DECODE_SHAPES = [
     (8, 1, 512, 1, 0, "contig"),
     (16, 8, 128, 1, 0, "paged"),
     (4, 2, 64, 3, 0, "contig"),     # odd Q: rows tile padding
+    # LDS-DMA ring decodes (bf16 CONTIG / RING, <= 4 rows per kv head) at each head_dim
+    (2, 1, 256, 1, 64, "ring"),
+    (4, 1, 64, 1, 32, "ring"),
+    (1, 1, 128, 1, 0, "contig"),
+    (2, 1, 512, 1, 0, "contig"),    # q staged over 2 KiB of the ring
+    (4, 1, 512, 1, 0, "contig"),    # ring over the LDS budget: register loads
 ]
 # g * Q of 8 or 16 rows per kv head has two kernels (decode_kernel="auto"
 # picks one by shape): run those shapes on each, forced.

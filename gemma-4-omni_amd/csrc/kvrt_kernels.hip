@@ -677,6 +677,26 @@ __device__ __forceinline__ f32x4_t mfma16k16(uint2 a, uint2 b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
                                                      c, 0, 0, 0);
 }
+// Online-softmax update of an MFMA accumulator column with a lazy reference
+// max: m (log2 units, uniform per column) moves only when the tile's max
+// exceeds it by more than kRescaleSlack, so p = 2^(s - m) stays <= 2^8 and
+// the l / o rescale (o lives in AGPRs: a read, multiply and write per
+// element) runs a few times per wave instead of on most tiles. Exact: l and
+// o always refer to the same m, and the merges weight partials by their own m.
+constexpr float kRescaleSlack = 8.0f;
+template <int NB>
+__device__ __forceinline__ void lazy_rescale(float tmax, float &m, float &l, f32x4_t (&o)[NB]) {
+    if (tmax > m + kRescaleSlack) {
+        if (m != kNegBig) {  // otherwise nothing has been accumulated yet
+            const float corr = __builtin_amdgcn_exp2f(m - tmax);
+            l *= corr;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) o[b] *= corr;
+        }
+        m = tmax;
+    }
+}
+
 // gfx950 LDS transpose read: in each group of 16 lanes, lane s gives the
 // address of 4 consecutive bf16; lane t = 4a + e receives element e of the
 // chunks of lanes a, a + 4, a + 8, a + 12.
@@ -754,11 +774,15 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const bool rvalid = col < rows;
     uint4 qop[D / 32];
     {
+        // every lane loads (rows past the tile's real rows read row 0), then
+        // those lanes zero their operand: no branch around the loads
         const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
         const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D + 8 * grp;
 #pragma unroll
+        for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + 32 * c);
+#pragma unroll
         for (int c = 0; c < D / 32; ++c)
-            qop[c] = rvalid ? *reinterpret_cast<const uint4 *>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
+            if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
     }
     const int hi = rvalid ? p0 + col % Qn : -1;
     const int lo = a.window > 0 ? p0 + col % Qn - a.window + 1 : 0;
@@ -820,14 +844,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             tmax = fmaxf(tmax, sc[v]);
         }
         tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
-        const float mn = fmaxf(m, tmax);
-        const float corr = __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        l *= corr;
-        if (__any(corr != 1.0f)) {
-#pragma unroll
-            for (int b = 0; b < D / 16; ++b) o[b] *= corr;
-        }
+        lazy_rescale<D / 16>(tmax, m, l, o);
         float p[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -1132,14 +1149,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             tmax = fmaxf(tmax, sc[j]);
         }
         tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
-        const float mn = fmaxf(m, tmax);
-        const float corr = __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        l *= corr;
-        if (__any(corr != 1.0f)) {
-#pragma unroll
-            for (int b = 0; b < D / 16; ++b) o[b] *= corr;
-        }
+        lazy_rescale<D / 16>(tmax, m, l, o);
         // P = P_hi + P_lo, both bf16 (P_lo = the rounding error of P_hi): the
         // two products keep P to ~2^-17 relative, where one bf16 P (2^-9)
         // would be visible in bf16 outputs of few-key rows.

@@ -51,9 +51,15 @@ constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
     return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= 4 &&
            kWaves * dma_wave_bytes(R, head_dim) <= 64 * 1024 - 1024;
 }
+// int8 decodes are VALU-bound (a dequantise and R FMAs per value): 2 key
+// groups per pass keep them at 118 VGPRs, 4 waves per SIMD.
+#ifndef KVRT_INT8_UNROLL
+#define KVRT_INT8_UNROLL 2
+#endif
 // Key groups per main-loop pass of decode_kernel.
 constexpr int decode_unroll(int R, int dtype, int layout, int head_dim) {
-    return decode_dma(R, dtype, layout, head_dim) ? kDmaUnroll : keys_unroll(R);
+    return decode_dma(R, dtype, layout, head_dim) ? kDmaUnroll
+           : dtype == KVRT_INT8 ? KVRT_INT8_UNROLL : keys_unroll(R);
 }
 
 // Where the rows of one layer live. Row (slot, head, pos) starts at element

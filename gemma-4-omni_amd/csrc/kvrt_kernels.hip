@@ -39,6 +39,22 @@ __device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int hea
     }
 }
 
+// PAGED row offset with the page taken from a wave's window of page-table
+// entries (lane i holds the entry of logical page win0 + i; pages past the
+// window are looked up directly). Every lane of the wave must call it.
+__device__ __forceinline__ int64_t paged_offset(const KVView &v, int slot, int head, int pos, int D, int win,
+                                                int win0) {
+    const int lp = pos >> v.block_shift;
+    const int idx = lp - win0;
+    int page = __shfl(win, idx & 63);
+    if (idx < 0 || idx >= 64) {
+        if (pos < 0 || lp >= v.pt_stride) return -1;
+        page = v.page_table[(int64_t)slot * v.pt_stride + lp];
+    }
+    if (page < 0 || page >= v.pool_pages) return -1;
+    return (((int64_t)page * v.kv_heads + head) * v.rows + (pos & (v.rows - 1))) * (int64_t)D;
+}
+
 // ---------------------------------------------------------------------------
 // append / import
 // ---------------------------------------------------------------------------
@@ -408,6 +424,15 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int64_t new_base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * VEC;
     bool bad = false;  // a visible key on an unmapped page (PAGED)
     const int npass = we > ws ? (we - ws + KPW * U - 1) / (KPW * U) : 0;
+    // PAGED: the page-table entries of the wave's first 64 pages, one per
+    // lane, so that a pass finds its pages with a lane shuffle instead of a
+    // dependent global load
+    int pwin = -1, pwin0 = 0;
+    if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+        pwin0 = ws >> a.kv.block_shift;
+        const int lp = pwin0 + lane;
+        if (lp < a.kv.pt_stride) pwin = a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp];
+    }
     __shared__ __align__(16) u32x4_t dma_lds[DMA ? kWaves * WAVE_BYTES / 16 : 1];
     // this wave's LDS: q rows (QI KiB), then STG stages of U x (K, V) KiB
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -488,7 +513,9 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         for (int u = 0; u < U; ++u) {
             const int kk = base + u * KPW + sub;
             const int kc = kk < we ? kk : ws;  // clamped: always a readable row
-            int64_t o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+            int64_t o;
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) o = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
+            else o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
             bool ok = kk < we;
             if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
                 bad |= ok && o < 0;

@@ -214,9 +214,14 @@ bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim) {
     return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512;
 }
 
-int target_wgs(const kvrt_config &cfg) {
+// Split-K workgroups a decode launch aims at: the context's decode_wgs, else
+// KVRT_TARGET_WGS (512), doubled for int8 layers — their VALU-bound waves
+// (2 groups of 8 keys per pass, 118 VGPRs) need 4 waves per SIMD to hide the
+// dequantise and FMA latencies.
+int target_wgs(const kvrt_config &cfg, int dtype = KVRT_BF16) {
     static const int v = env_int("KVRT_TARGET_WGS", 512);
-    return cfg.decode_wgs > 0 ? cfg.decode_wgs : v;
+    if (cfg.decode_wgs > 0) return cfg.decode_wgs;
+    return dtype == KVRT_INT8 ? 2 * v : v;
 }
 // Keys a wave must own at least: one main-loop iteration of the kernel
 // variant (8..32 keys), unless KVRT_MIN_KEYS_PER_WAVE asks for more.
@@ -252,7 +257,7 @@ size_t workspace_bound(const kvrt_ctx *c) {
     size_t best = 0;
     for (const Layer &L : c->layers) {
         const int hkv = L.spec.kv_heads;
-        const int total_wgs = std::min(target_wgs(c->cfg) + n * hkv, n * hkv * kMaxWgPerHead);
+        const int total_wgs = std::min(target_wgs(c->cfg, L.spec.dtype) + n * hkv, n * hkv * kMaxWgPerHead);
         const size_t parts = (size_t)total_wgs * kWaves * 16;
         best = std::max(best, ((parts * L.spec.head_dim + 63) / 64) * 64 * 4 + parts * 8 + 256);
     }
@@ -562,7 +567,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     }
     const int R = rows_tile(rows);
     const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D);
-    const int n_split = choose_splits(target_wgs(c->cfg), n, hkv, max_keys,
+    const int n_split = choose_splits(target_wgs(c->cfg, s.dtype), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));

@@ -27,7 +27,7 @@ constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
 
 // bf16 CONTIG / RING decodes of <= 4 rows per kv head stream K/V straight
 // into LDS (global_load_lds_dwordx4) through a ring of kDmaStages stages of
-// kDmaUnroll key groups per wave, so the next stages stay in flight while a
+// dma_unroll(R) key groups per wave, so the next stages stay in flight while a
 // wave computes on the current one without holding registers for them.
 #ifndef KVRT_DMA_UNROLL
 #define KVRT_DMA_UNROLL 3
@@ -38,18 +38,26 @@ constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
 #ifndef KVRT_DECODE_DMA
 #define KVRT_DECODE_DMA 1
 #endif
-constexpr int kDmaUnroll = KVRT_DMA_UNROLL;
+#ifndef KVRT_DMA_MAX_ROWS
+#define KVRT_DMA_MAX_ROWS 4
+#endif
+#ifndef KVRT_DMA_UNROLL8
+#define KVRT_DMA_UNROLL8 2
+#endif
 constexpr int kDmaStages = KVRT_DMA_STAGES;
+// Key groups per ring stage (8-row tiles hold more q rows and accumulators).
+constexpr int dma_unroll(int R) { return R <= 4 ? KVRT_DMA_UNROLL : KVRT_DMA_UNROLL8; }
 // Bytes of one wave's ring: q rows (ceil(R * D/8 / 64) KiB) + stages x groups x (K, V).
 constexpr int dma_wave_bytes(int R, int head_dim) {
-    return (kDmaStages * kDmaUnroll * 2 + (R * (head_dim / 8) + 63) / 64) * 1024;
+    return (kDmaStages * dma_unroll(R) * 2 + (R * (head_dim / 8) + 63) / 64) * 1024;
 }
 // The rings of a workgroup stay inside the first 64 KiB of LDS (the range an
 // M0-addressed LDS DMA is known to reach), with 1 KiB left for the merge's
-// (m, l) table.
+// (m, l) table; a wave's fp32 partial (R x D) must fit its own ring.
 constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
-    return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= 4 &&
-           kWaves * dma_wave_bytes(R, head_dim) <= 64 * 1024 - 1024;
+    return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= KVRT_DMA_MAX_ROWS &&
+           kWaves * dma_wave_bytes(R, head_dim) <= 64 * 1024 - 1024 &&
+           R * head_dim * 4 <= dma_wave_bytes(R, head_dim);  // the wave's partial fits its drained ring
 }
 // int8 decodes are VALU-bound (a dequantise and R FMAs per value): 2 key
 // groups per pass keep them at 118 VGPRs, 4 waves per SIMD.
@@ -58,7 +66,7 @@ constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
 #endif
 // Key groups per main-loop pass of decode_kernel.
 constexpr int decode_unroll(int R, int dtype, int layout, int head_dim) {
-    return decode_dma(R, dtype, layout, head_dim) ? kDmaUnroll
+    return decode_dma(R, dtype, layout, head_dim) ? dma_unroll(R)
            : dtype == KVRT_INT8 ? KVRT_INT8_UNROLL : keys_unroll(R);
 }
 

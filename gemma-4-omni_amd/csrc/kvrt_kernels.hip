@@ -821,45 +821,73 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const uint16_t *sv_lane = sv + (4 * grp + (col >> 2)) * KP + 4 * (col & 3);
     bool bad = false;
     const int64_t new_base = ((int64_t)item * hkv + kvh) * Qn * D;
-    for (int t0 = ws; t0 < we; t0 += T) {
-        // K as the A operand (lane (col, grp): key t0 + col, dims 32c + 8grp)
-        // and the V tile (unit u = lane + 64i: key row u / (D/8), 16 B
-        // segment u % (D/8)); keys past we read row ws and are masked; the
-        // rows of a fused append come from k_new / v_new.
-        uint4 ka[D / 32], vt[D / 32];
-#pragma unroll
-        for (int i = -1; i < D / 32; ++i) {
-            const int kr = i < 0 ? col : (lane + 64 * i) / (D / 8);
-            const int kk = t0 + kr;
-            const int kc = kk < we ? kk : ws;
-            int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
-            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
-                bad |= kk < we && off < 0;
-                off = off < 0 ? 0 : off;
-            }
-            const uint16_t *kp = static_cast<const uint16_t *>(a.kv.k) + off;
-            const uint16_t *vp = static_cast<const uint16_t *>(a.kv.v) + off;
-            if (fused) {
-                const bool nw = kc >= len;
-                const int64_t on = new_base + (int64_t)(kc - len) * D;
-                kp = nw ? a.k_new + on : kp;
-                vp = nw ? a.v_new + on : vp;
-            }
-            if (i < 0) {
-#pragma unroll
-                for (int c = 0; c < D / 32; ++c) ka[c] = load_stream16(kp + 32 * c + 8 * grp);
-            } else {
-                vt[i] = load_stream16(vp + 8 * ((lane + 64 * i) % (D / 8)));
-            }
+    // Row address of key kk of the wave's range (keys past we read row ws and
+    // are masked; the rows of a fused append come from k_new / v_new).
+    auto key_rows = [&](int kk, const uint16_t *&kp, const uint16_t *&vp) __attribute__((always_inline)) {
+        const int kc = kk < we ? kk : ws;
+        int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+        if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+            bad |= kk < we && off < 0;
+            off = off < 0 ? 0 : off;
         }
+        kp = static_cast<const uint16_t *>(a.kv.k) + off;
+        vp = static_cast<const uint16_t *>(a.kv.v) + off;
+        if (fused) {
+            const bool nw = kc >= len;
+            const int64_t on = new_base + (int64_t)(kc - len) * D;
+            kp = nw ? a.k_new + on : kp;
+            vp = nw ? a.v_new + on : vp;
+        }
+    };
+    // K of the tile at t0 as the A operand (lane (col, grp): key t0 + col,
+    // dims 32c + 8grp); V of the tile as units u = lane + 64i (key row
+    // u / (D/8), 16 B segment u % (D/8)).
+    auto load_k = [&](int t0, uint4 (&ka)[D / 32]) __attribute__((always_inline)) {
+        const uint16_t *kp, *vp;
+        key_rows(t0 + col, kp, vp);
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) ka[c] = load_stream16(kp + 32 * c + 8 * grp);
+    };
+    auto load_v = [&](int t0, uint4 (&vt)[D / 32]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            const uint16_t *kp, *vp;
+            key_rows(t0 + (lane + 64 * i) / (D / 8), kp, vp);
+            vt[i] = load_stream16(vp + 8 * ((lane + 64 * i) % (D / 8)));
+        }
+    };
+    // Software pipeline over the wave's tiles: tile t + 1's K is loaded into
+    // the A-operand registers as soon as tile t's S MFMAs have read them, and
+    // its V as soon as tile t's V is in LDS, so both are in flight during tile
+    // t's softmax and P.V.
+    // (PAGED at D 512 keeps one tile in flight: the page lookups of a second
+    // tile do not fit the registers.)
+    constexpr bool PIPE = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
+    uint4 ka[D / 32], vt[D / 32];
+    if (PIPE && ws < we) {
+        load_k(ws, ka);
+        load_v(ws, vt);
+    }
+    // The loop runs the tiles that have a successor with unconditional loads
+    // of the next tile (a conditional load would make the compiler's wait
+    // counts assume it may be missing, and wait on the next tile's first load
+    // before storing this tile's V); the last tile is peeled.
+    auto tile = [&](int t0, auto more_c) __attribute__((always_inline)) {
+        constexpr bool more = PIPE && decltype(more_c)::value;
+        if constexpr (!PIPE) {
+            load_k(t0, ka);
+            load_v(t0, vt);
+        }
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) s = mfma16(ka[c], qop[c], s);
+        if constexpr (more) load_k(t0 + T, ka);
 #pragma unroll
         for (int i = 0; i < D / 32; ++i) {
             const int u = lane + 64 * i;
             *reinterpret_cast<uint4 *>(sv + (u / (D / 8)) * KP + 8 * (u % (D / 8))) = vt[i];
         }
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < D / 32; ++c) s = mfma16(ka[c], qop[c], s);
+        if constexpr (more) load_v(t0 + T, vt);
         // this lane: keys t0 + 4grp + v of row col
         float sc[4];
         float tmax = -INFINITY;
@@ -888,7 +916,10 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             const uint2 va = lds_read_tr16(sv_lane + 16 * b);
             o[b] = mfma16k16(va, pl, mfma16k16(va, ph, o[b]));
         }
-    }
+    };
+    int t0 = ws;
+    for (; t0 + T < we; t0 += T) tile(t0, std::true_type{});
+    if (t0 < we) tile(t0, std::false_type{});
     if (bad) a.err[0] = 1;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));
     // Workgroup merge: every wave puts its partial in LDS (over the tiles);

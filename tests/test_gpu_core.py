@@ -228,6 +228,37 @@ def test_paged_int8_quantise_dequantise_attend_and_evict():
     assert c["pages_in_use"] <= 2 * (96 // 16 + 2) + 2
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+def test_paged_decode_past_the_preloaded_page_window(dtype):
+    """A wave preloads the page-table entries of its first 64 pages and looks
+    further pages up directly: with one workgroup per (session, kv head)
+    (decode_wgs 1) a 5000-key session gives each wave ~78 pages of 16 keys,
+    so both lookups are exercised; pages come from a shuffled pool."""
+    from kvrt import LayerSpec
+
+    gen = torch.Generator().manual_seed(17)
+    spec = LayerSpec(kv_heads=8, head_dim=128, layout="paged", dtype=dtype)
+    rt = _rt([spec], n_slots=2, capacity=5200, max_q=1, block_size=16, pool_pages=700, pool_seed=9,
+             decode_wgs=1)
+    orc = O.OracleCache(_oracle_layers([spec]), 2)
+    for s, n in ((0, 5000), (1, 777)):
+        k = randn_bf16(gen, (1, 8, n, 128))
+        v = randn_bf16(gen, (1, 8, n, 128))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    for step in range(2):
+        q = randn_bf16(gen, (2, 16, 1, 128), 0.5)
+        out = rt.attend(0, q.cuda(), [0, 1], 1 / math.sqrt(128))
+        for i in range(2):
+            ref = orc.attend(i, 0, to_np(q[i]), 1 / math.sqrt(128))
+            assert np.abs(to_np(out[i]) - ref).max() <= ATOL
+        k = randn_bf16(gen, (2, 8, 1, 128), 0.5)
+        rt.append(0, k.cuda(), k.cuda(), [0, 1])
+        for i in range(2):
+            orc.append(i, 0, to_np(k[i]), to_np(k[i]))
+    assert rt.health() == 0
+
+
 def test_gather_then_attend_tensors_matches_oracle():
     """Listener micro-batch path: ragged gather -> padded batch -> attend."""
     from kvrt import LayerSpec, attend_tensors

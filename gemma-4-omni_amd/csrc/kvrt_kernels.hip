@@ -231,14 +231,14 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 // decode attention (split-K)
 // ---------------------------------------------------------------------------
 // LDS DMA: global_load_lds_dwordx4 moves lane l's 16 bytes at g to LDS byte
-// lds + 16 * l without passing through registers. It is issued from inline
-// assembly that sets M0 in the same statement, so the compiler neither tracks
-// these loads nor inserts its own (all-or-nothing) waits for them: the decode
-// waits with explicit vmcnt waits — vector loads complete in issue order, so
-// vmcnt(N) means every DMA but the N most recent has landed — and reads the
-// LDS back only after such a wait. The kernels using it set M0 nowhere else.
+// M0 + 16 * l without passing through registers. It is issued from inline
+// assembly (the LDS address is an M0 operand the compiler sets up), so the
+// compiler neither tracks these loads nor inserts its own (all-or-nothing)
+// waits for them: the decode waits with explicit vmcnt waits — vector loads
+// complete in issue order, so vmcnt(N) means every DMA but the N most recent
+// has landed — and reads the LDS back only after such a wait.
 __device__ __forceinline__ void dma_load16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds) : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmem() {

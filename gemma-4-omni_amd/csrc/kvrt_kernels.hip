@@ -1094,12 +1094,23 @@ __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kv
     vx = *reinterpret_cast<const u32x4_t *>(vg + off + 8 * ks);
 }
 
+// LDS layout of a staged K or V tile: row r (key) at r * pf_pitch<D>() bf16,
+// its 16-B chunk k at chunk position k ^ pf_swz<D>(r). With D >= 128 the
+// rows carry 32 B of padding and chunks are XOR-swizzled by bits 3 and 4 of
+// the row, so that the 16 rows x 16 B of one S^T A-operand read and the 8 rows
+// x 32 B of one V^T transposed read of a half-wave fall on distinct banks
+// (64 banks of 4 B); D = 64 keeps 16 B of padding and no swizzle.
+template <int D>
+constexpr int pf_pitch() { return D >= 128 ? D + 16 : D + 8; }
+template <int D>
+__device__ __forceinline__ int pf_swz(int r) { return D >= 128 ? (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1) : 0; }
+
 template <int D>
 __device__ __forceinline__ void pf_stage_unit(uint16_t *sk, uint16_t *sv, int c, const u32x4_t &kx, const u32x4_t &vx) {
     constexpr int UNITS = kPfKeys * (D / 8);
-    constexpr int KP = D + 8;
+    constexpr int KP = pf_pitch<D>();
     if (c < UNITS) {
-        const int kr = c / (D / 8), ks = c % (D / 8);
+        const int kr = c / (D / 8), ks = (c % (D / 8)) ^ pf_swz<D>(c / (D / 8));
         *reinterpret_cast<u32x4_t *>(&sk[kr * KP + 8 * ks]) = kx;
         *reinterpret_cast<u32x4_t *>(&sv[kr * KP + 8 * ks]) = vx;
     }
@@ -1126,7 +1137,7 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
 
 template <int D, int LAYOUT, int NW, bool PF>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
-    constexpr int KP = D + 8;        // K tile row pitch (bf16): 16 B of padding per row
+    constexpr int KP = pf_pitch<D>();  // K / V tile row pitch (bf16)
     constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
     constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
     constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
@@ -1170,7 +1181,14 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     // 16 lanes, lane s points at key row 8*grp + s/4 (+4 for the second
     // read), dims 4*(s%4) .. +3 of the 16-dim block; lane t = 4a + e then
     // receives dim 4a + e of key rows 8*grp + j, j = 0..3, i.e. A[d][k].
-    const uint16_t *sv_lane = &sv[(8 * grp + (col >> 2)) * KP + 4 * (col & 3)];
+    // (swizzle: row 8grp + ... has bit 3 = grp & 1 and bit 4 = grp >> 1, so
+    // chunk (col&3)/2 + 2*b sits at ((col&3)/2 ^ (grp >> 1)) + 2*(b ^ 4*(grp & 1)):
+    // blocks b with bit 2 clear read 64 elements further when grp is odd, the
+    // others 64 nearer)
+    const int vd = D >= 128 ? (grp & 1) * 64 : 0;
+    const uint16_t *sv_base =
+        &sv[(8 * grp + (col >> 2)) * KP + 8 * (((col & 3) >> 1) ^ (D >= 128 ? grp >> 1 : 0)) + 4 * (col & 1)];
+    const uint16_t *sv_lo = sv_base + vd, *sv_hi = sv_base - vd;
     auto read_vt = [&](const uint16_t *p) __attribute__((always_inline)) {
         typedef short v4s_t __attribute__((ext_vector_type(4)));
         const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1191,9 +1209,15 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             s[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            const uint16_t *kp = &sk[pf_key(b, col) * KP + 8 * grp];
+            // chunk grp + 4c of key row kr sits at (grp ^ s0) + 4 * (c ^ 2 s3)
+            // (s0, s3: bits 4 and 3 of kr): slices c with bit 1 clear read 64
+            // elements further when s3 is set, the others 64 nearer
+            const int kr = pf_key(b, col);
+            const int kd = D >= 128 ? ((kr >> 3) & 1) * 64 : 0;
+            const uint16_t *kp = &sk[kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
 #pragma unroll
-            for (int c = 0; c < D / 32; ++c) s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c), qop[c], s[b]);
+            for (int c = 0; c < D / 32; ++c)
+                s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd)), qop[c], s[b]);
         }
         // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile
         float sc[8];
@@ -1225,7 +1249,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // O^T += V^T P^T: A row i = d (16b + col), k = keys 8grp .. +7
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) {
-            const uint4 va = read_vt(sv_lane + 16 * b);
+            const uint4 va = read_vt(((b >> 2) & 1 ? sv_hi : sv_lo) + 16 * b);
             o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
         }
     };

@@ -22,8 +22,12 @@ constexpr int kMaxInt8Rows = 8;      // query rows per kv head of an INT8 decode
 // Key-row groups a decode wave keeps in flight per main-loop pass, by row
 // tile R: all of them are loaded before the first is used, so a wave has
 // U * 2 KiB (bf16: K and V, 16 B per lane) outstanding; fewer for larger R,
-// whose query rows and accumulators take the registers.
-constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? 4 : 2); }
+// whose query rows and accumulators take the registers (8 rows: 3 groups,
+// 182 VGPRs — lighter on a concurrently running stream than 4).
+#ifndef KVRT_UNROLL8
+#define KVRT_UNROLL8 3
+#endif
+constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? KVRT_UNROLL8 : 2); }
 
 // bf16 CONTIG / RING decodes of <= 4 rows per kv head stream K/V straight
 // into LDS (global_load_lds_dwordx4) through a ring of kDmaStages stages of

@@ -233,11 +233,17 @@ int min_keys_per_wave(int keys_per_iter) {
 // Number of wave splits per (item, kv head): enough workgroups to fill the
 // chip, but at least min_keys keys per wave. n_items * kv_heads * (splits /
 // kWaves) <= target + n_items * kv_heads, which bounds the workspace.
+// The key count is taken at its power-of-two bucket (>= 256), so that the
+// split count, and with it the order of the fp32 reductions, stays the same
+// over the many decode steps of a bucket: a HIP graph captured at one length
+// and replayed at the next ones then matches eager calls bit for bit.
 int choose_splits(int target, int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
     const int per_head = n_items * kv_heads;
     const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave(keys_per_iter);
     int wg = (target + per_head - 1) / per_head;
-    const int64_t cap = std::max<int64_t>(1, (max_keys + per_wg - 1) / per_wg);
+    int64_t bucket = 256;
+    while (bucket < max_keys) bucket *= 2;
+    const int64_t cap = std::max<int64_t>(1, (bucket + per_wg - 1) / per_wg);
     if (wg > cap) wg = (int)cap;
     if (wg > kMaxWgPerHead) wg = kMaxWgPerHead;  // fix-up merges <= 256 wave partials
     if (wg < 1) wg = 1;

@@ -361,24 +361,29 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         }
     }
 
-    // q rows of this kv head, packed bf16 pairs.
+    // q rows of this kv head, packed bf16 pairs. Row r = j*Q + i of the tile
+    // is query i of q head kvh*g + j; rows past the real ones (r >= rows) load
+    // row 0 and are never used (no key is visible to them), so the loads issue
+    // back to back with no branch (a branch around a load makes the compiler
+    // wait for it at the join, before the K/V loads are issued).
     uint32_t qw[R][QW];
     const int hq = hkv * a.group;
+    if constexpr (!DMA) {  // DMA: staged through LDS below
+        const uint16_t *q0 = a.q + ((int64_t)item * hq + kvh * a.group) * Qn * D + seg * VEC;
+        int j = 0, i = 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if constexpr (DMA) break;  // staged through LDS below
-        if (r < rows) {
-            const int j = r / Qn, i = r % Qn;
-            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + seg * VEC;
+        for (int r = 0; r < R; ++r) {
+            const uint16_t *qp = q0 + (r < rows ? (int64_t)(j * Qn + i) * D : 0);
 #pragma unroll
             for (int t = 0; t < VEC / 8; ++t) {
                 const uint4 x = *reinterpret_cast<const uint4 *>(qp + t * 8);
                 qw[r][4 * t + 0] = x.x; qw[r][4 * t + 1] = x.y;
                 qw[r][4 * t + 2] = x.z; qw[r][4 * t + 3] = x.w;
             }
-        } else {
-#pragma unroll
-            for (int t = 0; t < QW; ++t) qw[r][t] = 0u;
+            if (++i == Qn) {
+                i = 0;
+                ++j;
+            }
         }
     }
     // Per-row visibility: key in [lo_r, hi_r]; talker rows add the audio
@@ -542,6 +547,10 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 vsc[u] = a.kv.vs[o / D];
             }
         }
+        // keep all 2U loads of the pass ahead of the arithmetic (the scheduler
+        // would otherwise sink the last ones under register pressure and
+        // expose a second memory round trip per pass)
+        __builtin_amdgcn_sched_barrier(0);
         }
         // scores (log2 domain)
         float s[U][R];

@@ -233,16 +233,19 @@ int min_keys_per_wave(int keys_per_iter) {
 // Number of wave splits per (item, kv head): enough workgroups to fill the
 // chip, but at least min_keys keys per wave. n_items * kv_heads * (splits /
 // kWaves) <= target + n_items * kv_heads, which bounds the workspace.
-// The key count is taken at its power-of-two bucket (>= 256), so that the
+// The key count is rounded up to a multiple of kSplitKeyBucket, so that the
 // split count, and with it the order of the fp32 reductions, stays the same
-// over the many decode steps of a bucket: a HIP graph captured at one length
-// and replayed at the next ones then matches eager calls bit for bit.
+// over the decode steps of a bucket: a HIP graph captured at one length and
+// replayed at the next ones then matches eager calls bit for bit.
+#ifndef KVRT_SPLIT_KEY_BUCKET
+#define KVRT_SPLIT_KEY_BUCKET 128
+#endif
+constexpr int64_t kSplitKeyBucket = KVRT_SPLIT_KEY_BUCKET;
 int choose_splits(int target, int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
     const int per_head = n_items * kv_heads;
     const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave(keys_per_iter);
     int wg = (target + per_head - 1) / per_head;
-    int64_t bucket = 256;
-    while (bucket < max_keys) bucket *= 2;
+    const int64_t bucket = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
     const int64_t cap = std::max<int64_t>(1, (bucket + per_wg - 1) / per_wg);
     if (wg > cap) wg = (int)cap;
     if (wg > kMaxWgPerHead) wg = kMaxWgPerHead;  // fix-up merges <= 256 wave partials

@@ -55,12 +55,13 @@ constexpr int dma_unroll(int R) { return R <= 4 ? KVRT_DMA_UNROLL : KVRT_DMA_UNR
 constexpr int dma_wave_bytes(int R, int head_dim) {
     return (kDmaStages * dma_unroll(R) * 2 + (R * (head_dim / 8) + 63) / 64) * 1024;
 }
-// The rings of a workgroup stay inside the first 64 KiB of LDS (the range an
-// M0-addressed LDS DMA is known to reach), with 1 KiB left for the merge's
-// (m, l) table; a wave's fp32 partial (R x D) must fit its own ring.
+// The rings of a workgroup fit gfx950's 160 KiB of LDS with 1 KiB left for
+// the merge's (m, l) table (an M0-addressed LDS DMA reaches the whole range:
+// probed at byte 96 KiB of a 128 KiB allocation); a wave's fp32 partial
+// (R x D) must fit its own ring.
 constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
     return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= KVRT_DMA_MAX_ROWS &&
-           kWaves * dma_wave_bytes(R, head_dim) <= 64 * 1024 - 1024 &&
+           kWaves * dma_wave_bytes(R, head_dim) <= 160 * 1024 - 1024 &&
            R * head_dim * 4 <= dma_wave_bytes(R, head_dim);  // the wave's partial fits its drained ring
 }
 // int8 decodes are VALU-bound (a dequantise and R FMAs per value): 2 key

@@ -124,7 +124,7 @@ _DECODE_SHAPES = [
     (4, 1, 64, 1, 32, "ring"),
     (1, 1, 128, 1, 0, "contig"),
     (2, 1, 512, 1, 0, "contig"),    # q staged over 2 KiB of the ring
-    (4, 1, 512, 1, 0, "contig"),    # ring over the LDS budget: register loads
+    (4, 1, 512, 1, 0, "contig"),    # q staged over 4 KiB of the ring (64 KiB of LDS)
 ]
 # g * Q of 8 or 16 rows per kv head has two kernels (decode_kernel="auto"
 # picks one by shape): run those shapes on each, forced.

@@ -1150,8 +1150,11 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
     constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
     constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
-    __shared__ __align__(16) uint16_t sk[kPfKeys * KP];
-    __shared__ __align__(16) uint16_t sv[kPfKeys * KP];
+    // PF: two K/V tile buffers, so tile t + 1 is staged while tile t is computed
+    constexpr int NBUF = PF ? 2 : 1;
+    constexpr int TILE = kPfKeys * KP;  // bf16 elements of one K (or V) tile buffer
+    __shared__ __align__(16) uint16_t sk[NBUF * TILE];
+    __shared__ __align__(16) uint16_t sv[NBUF * TILE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
@@ -1207,7 +1210,8 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         return make_uint4(l2.x, l2.y, h2.x, h2.y);
     };
-    auto compute_tile = [&](int t0) __attribute__((always_inline)) {
+    auto compute_tile = [&](int t0, auto buf_c) __attribute__((always_inline)) {
+        constexpr int BO = decltype(buf_c)::value * TILE;  // the tile's buffer
         // every key of the tile visible to all 16 queries of the block (the
         // block's first query sees up to its own position, the last one's
         // window starts at or before t0): no per-key mask
@@ -1223,7 +1227,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             // elements further when s3 is set, the others 64 nearer
             const int kr = pf_key(b, col);
             const int kd = D >= 128 ? ((kr >> 3) & 1) * 64 : 0;
-            const uint16_t *kp = &sk[kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
+            const uint16_t *kp = &sk[BO + kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
 #pragma unroll
             for (int c = 0; c < D / 32; ++c)
                 s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd)), qop[c], s[b]);
@@ -1258,7 +1262,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // O^T += V^T P^T: A row i = d (16b + col), k = keys 8grp .. +7
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) {
-            const uint4 va = read_vt(((b >> 2) & 1 ? sv_hi : sv_lo) + 16 * b);
+            const uint4 va = read_vt(((b >> 2) & 1 ? sv_hi : sv_lo) + BO + 16 * b);
             o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
         }
     };
@@ -1267,24 +1271,33 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     // prefetches behind it (vmcnt counts in order).
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     if constexpr (PF) {
-        // PD tiles in flight in registers: the loop runs PD tiles per pass,
-        // phase p staging ring entry p and refilling it with the tile PD
-        // ahead (keys past kend read row kstart: in bounds, never visible).
+        // PD tiles in flight in registers (ring slot s holds tiles s, s + PD,
+        // ...; keys past kend read row kstart: in bounds, never visible) and
+        // two tile buffers in LDS (tile i in buffer i % 2; PD is even). Per
+        // tile one barrier: after it, tile i is staged and every wave is done
+        // with tile i - 1, whose buffer then takes tile i + 1 while tile i is
+        // computed.
+        static_assert(PD % 2 == 0, "tile parity follows the ring slot");
         u32x4_t kreg[PD][KU], vreg[PD][KU];
         StaticFor<0, PD>::run([&](auto pc) {
             constexpr int p = decltype(pc)::value;
             pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, kstart + p * kPfKeys, kstart, kend, kreg[p], vreg[p], bad);
         });
+        pf_stage<D, KU>(sk, sv, kreg[0], vreg[0]);
+        pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, kstart + PD * kPfKeys, kstart, kend, kreg[0], vreg[0], bad);
         for (int t0 = kstart; t0 < kend; t0 += PD * kPfKeys) {
             StaticFor<0, PD>::run([&](auto pc) {
                 constexpr int p = decltype(pc)::value;
+                constexpr int pn = (p + 1) % PD;  // ring slot of the next tile
                 const int tt = t0 + p * kPfKeys;
                 if (tt < kend) {
-                    __syncthreads();  // the previous tile has been consumed
-                    pf_stage<D, KU>(sk, sv, kreg[p], vreg[p]);
                     __syncthreads();
-                    pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, tt + PD * kPfKeys, kstart, kend, kreg[p], vreg[p], bad);
-                    if (computes) compute_tile(tt);
+                    if (tt + kPfKeys < kend) {
+                        pf_stage<D, KU>(sk + (pn % 2) * TILE, sv + (pn % 2) * TILE, kreg[pn], vreg[pn]);
+                        pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, tt + kPfKeys + PD * kPfKeys, kstart, kend, kreg[pn],
+                                                vreg[pn], bad);
+                    }
+                    if (computes) compute_tile(tt, std::integral_constant<int, p % 2>{});
                 }
             });
         }
@@ -1297,7 +1310,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                 pf_stage_unit<D>(sk, sv, c, kx, vx);
             }
             __syncthreads();
-            if (computes) compute_tile(t0);
+            if (computes) compute_tile(t0, std::integral_constant<int, 0>{});
         }
     }
     if (bad) a.err[0] = 1;

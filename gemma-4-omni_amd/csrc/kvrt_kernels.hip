@@ -240,6 +240,10 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 __device__ __forceinline__ void dma_load16(const void *g, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
 }
+// The same without the streaming hint, for tiles other workgroups read again.
+__device__ __forceinline__ void dma_load16_cached(const void *g, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
@@ -1073,6 +1077,30 @@ struct StaticFor {
 // Tile units: unit c = (row c / (D/8), 16 B segment c % (D/8)) of both the
 // K and the V tile, both staged row-major. Keys at or past kend read row
 // kstart (masked in the softmax).
+// Element offset of row kr of the tile at t0 (key t0 + kr; keys at or past
+// kend read row kstart, masked in the softmax).
+template <int D, int LAYOUT>
+__device__ __forceinline__ int64_t pf_row_offset(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend,
+                                                 int kr, bool &bad) {
+    const int key = t0 + kr;
+    if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
+        // one multiply-add per row from the (slot, head) base
+        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
+        return base + (int64_t)(key < kend ? key : kstart) * D;
+    } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
+        // t0 % rows once per tile: rows of the tile wrap at most once
+        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
+        const int r0 = t0 % kv.rows, rs = kstart % kv.rows;
+        int rk = r0 + kr;
+        rk = rk >= kv.rows ? rk - kv.rows : rk;
+        return base + (int64_t)(key < kend ? rk : rs) * D;
+    } else {
+        const int64_t off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kstart, D);
+        bad |= off < 0;
+        return off < 0 ? 0 : off;
+    }
+}
+
 template <int D, int LAYOUT>
 __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend, int c,
                                               u32x4_t &kx, u32x4_t &vx, bool &bad) {
@@ -1081,24 +1109,7 @@ __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kv
     const uint16_t *vg = static_cast<const uint16_t *>(kv.v);
     const int cc = c < UNITS ? c : 0;
     const int kr = cc / (D / 8), ks = cc % (D / 8);
-    const int key = t0 + kr;
-    int64_t off;
-    if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
-        // one multiply-add per row from the (slot, head) base
-        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
-        off = base + (int64_t)(key < kend ? key : kstart) * D;
-    } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
-        // t0 % rows once per tile: rows of the tile wrap at most once
-        const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
-        const int r0 = t0 % kv.rows, rs = kstart % kv.rows;
-        int rk = r0 + kr;
-        rk = rk >= kv.rows ? rk - kv.rows : rk;
-        off = base + (int64_t)(key < kend ? rk : rs) * D;
-    } else {
-        off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kstart, D);
-        bad |= off < 0;
-        off = off < 0 ? 0 : off;
-    }
+    const int64_t off = pf_row_offset<D, LAYOUT>(kv, slot, kvh, t0, kstart, kend, kr, bad);
     kx = *reinterpret_cast<const u32x4_t *>(kg + off + 8 * ks);
     vx = *reinterpret_cast<const u32x4_t *>(vg + off + 8 * ks);
 }
@@ -1150,8 +1161,8 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
     constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
     constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
-    // PF: two K/V tile buffers, so tile t + 1 is staged while tile t is computed
-    constexpr int NBUF = PF ? 2 : 1;
+    // two K/V tile buffers, so tile t + 1 is staged while tile t is computed
+    constexpr int NBUF = 2;
     constexpr int TILE = kPfKeys * KP;  // bf16 elements of one K (or V) tile buffer
     __shared__ __align__(16) uint16_t sk[NBUF * TILE];
     __shared__ __align__(16) uint16_t sv[NBUF * TILE];
@@ -1302,15 +1313,37 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             });
         }
     } else {
-        for (int t0 = kstart; t0 < kend; t0 += kPfKeys) {
-            __syncthreads();  // the previous tile has been consumed
-            for (int c = threadIdx.x; c < UNITS; c += blockDim.x) {  // one unit in registers at a time
-                u32x4_t kx, vx;
-                pf_fetch_unit<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, c, kx, vx, bad);
-                pf_stage_unit<D>(sk, sv, c, kx, vx);
+        // D = 512 (no registers to spare for a prefetch ring): each key row of
+        // a tile is one LDS DMA of 64 x 16 B straight into the tile buffer
+        // (row pitch and chunk swizzle as pf_stage_unit: lane l fetches the
+        // logical chunk that lands on physical chunk l), issued by the waves in
+        // turn, one tile ahead, into the other buffer. Per tile: each wave
+        // waits for its own DMAs, then one barrier.
+        static_assert(D / 8 == 64, "one DMA instruction per key row");
+        const uint16_t *kg = static_cast<const uint16_t *>(a.kv.k);
+        const uint16_t *vg = static_cast<const uint16_t *>(a.kv.v);
+        const uint32_t sk_a = lds_addr(sk), sv_a = lds_addr(sv);
+        auto dma_tile = [&](int t0, int buf) __attribute__((always_inline)) {
+            for (int rr = wave; rr < 2 * kPfKeys; rr += NW) {  // rr < 32: K row rr, else V row rr - 32
+                const int kr = rr % kPfKeys;
+                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, kr, bad);
+                const uint16_t *g = (rr < kPfKeys ? kg : vg) + off + 8 * (lane ^ pf_swz<D>(kr));
+                const uint32_t dst = (rr < kPfKeys ? sk_a : sv_a) + (uint32_t)(buf * TILE + kr * KP) * 2;
+                dma_load16_cached(g, __builtin_amdgcn_readfirstlane(dst));
             }
-            __syncthreads();
-            if (computes) compute_tile(t0, std::integral_constant<int, 0>{});
+        };
+        if (kstart < kend) dma_tile(kstart, 0);
+        for (int t0 = kstart; t0 < kend; t0 += 2 * kPfKeys) {
+            StaticFor<0, 2>::run([&](auto pc) {
+                constexpr int p = decltype(pc)::value;
+                const int tt = t0 + p * kPfKeys;
+                if (tt < kend) {
+                    wait_vmem<0>();  // this wave's rows of tile tt have landed
+                    __syncthreads();  // every wave's have; tile tt - 32's buffer is free
+                    if (tt + kPfKeys < kend) dma_tile(tt + kPfKeys, 1 - p);
+                    if (computes) compute_tile(tt, std::integral_constant<int, p>{});
+                }
+            });
         }
     }
     if (bad) a.err[0] = 1;

@@ -63,6 +63,8 @@ def parse() -> argparse.Namespace:
                    help="split-K decode workgroups per thinker launch (kvrt_config.decode_wgs)")
     p.add_argument("--decode-kernel", choices=("auto", "valu", "mfma"), default="auto",
                    help="kernel for bf16 decodes of 8 or 16 query rows per kv head (kvrt_config.decode_kernel)")
+    p.add_argument("--decode-merge", choices=("auto", "separate", "last_wg"), default="auto",
+                   help="how split-K decodes merge their partials (kvrt_config.decode_merge)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
@@ -91,8 +93,11 @@ def build_runtimes(args, capacity: int, n_slots: int):
     th_wgs = getattr(args, "thinker_wgs", 0) if args is not None else 0
     tk_wgs = getattr(args, "talker_wgs", 0) if args is not None else 0
     kern = getattr(args, "decode_kernel", "auto") if args is not None else "auto"
-    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, decode_wgs=th_wgs, decode_kernel=kern, device="cuda")
-    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, decode_wgs=tk_wgs, decode_kernel=kern, device="cuda")
+    merge = getattr(args, "decode_merge", "auto") if args is not None else "auto"
+    thinker = KVRuntime(th_specs, n_slots, capacity, max_q=1, decode_wgs=th_wgs, decode_kernel=kern,
+                        decode_merge=merge, device="cuda")
+    talker = KVRuntime(tk_specs, n_slots, capacity, max_q=1, decode_wgs=tk_wgs, decode_kernel=kern,
+                       decode_merge=merge, device="cuda")
     return thinker, talker
 
 
@@ -179,9 +184,11 @@ def step_bytes(streams: int, ctx_after: int) -> dict:
             "total": streams * (th + tk)}
 
 
-def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int]:
-    """Average duration of one talker-layer attention launch pair (decode +
-    merge kernels) over one session group, HIP events on the stream they run on.
+def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int, int]:
+    """Average duration of one talker-layer fused append + attention call over
+    one session group (the decode kernel, plus the merge kernel when the
+    decode does not merge its own partials), HIP events on the stream they run
+    on; also the algorithmic bytes and the kernel launches per call.
 
     A GPU sleep ahead of each (event, launch, event) triple lets the host
     enqueue all three before the GPU reaches them, so the events bracket the
@@ -191,6 +198,7 @@ def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int]:
     stream = torch.cuda.current_stream()
     times = []
     bytes_total = 0
+    launches0 = model.rt.counters()["launches"]
     for _ in range(reps):
         L_before = model.rt.seq_length(0, 0)
         torch.cuda._sleep(2_000_000)
@@ -206,7 +214,7 @@ def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int]:
     # mean of the central 80 % (drop warm-up and preemption outliers)
     lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
     mean_t = sum(times[lo:hi]) / (hi - lo)
-    return mean_t, bytes_total // reps
+    return mean_t, bytes_total // reps, (model.rt.counters()["launches"] - launches0) // reps
 
 
 def pmc_traffic() -> tuple[int | None, str | None]:
@@ -412,7 +420,7 @@ def run_kernels(args) -> int:
         rr = window + qn - 1 if layout == "ring" else 0
         spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window, ring_rows=rr, dtype=dtype)
         lens = lens or [L] * n
-        cap = max(lens) + w + r + 64
+        cap = max(lens) + (w + r) * qn + 64
         rt = KVRuntime([spec], n, cap, max_q=qn, device="cuda", decode_wgs=wgs, **kw)
         for s, ln in enumerate(lens):
             first = max(0, ln - window + 1) if layout == "paged" and window else 0
@@ -541,7 +549,7 @@ def main() -> int:
     total_bytes = sum(step_bytes(args.streams, L)["total"] for L in range(len0 + 1, len1 + 1))
     ms = 1e3 * elapsed / args.steps
     tokens_per_step = 2 * args.streams
-    k_time, k_bytes = time_dominant_kernel(talker0, args.kernel_reps)
+    k_time, k_bytes, k_launches = time_dominant_kernel(talker0, args.kernel_reps)
     if talker0.rt.health() != 0:
         raise RuntimeError("kvrt health check failed after the kernel timing")
     achieved = k_bytes / k_time
@@ -578,14 +586,17 @@ def main() -> int:
             "tokens_per_step": tokens_per_step,
             "decode_wgs": {"talker": args.talker_wgs, "thinker": args.thinker_wgs},
             "decode_kernel": args.decode_kernel,
+            "decode_merge": args.decode_merge,
         },
         "step_hbm_gbps": round(total_bytes / elapsed / 1e9, 1),
         "step_hbm_frac": round(total_bytes / elapsed / HBM_PEAK, 4),
         "step_algorithmic_bytes": total_bytes // args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"talker layer attention, {n} streams, fused append: kvrt::decode_kernel<128,2,bf16,contig> "
-                      "+ kvrt::merge_kernel<128,2> (one kvrt_append_attend_async launch pair)",
+            "kernel": f"talker layer attention, {n} streams, fused append: kvrt::decode_kernel<128,2,bf16,contig>"
+                      + (" + kvrt::merge_kernel<128,2,1>" if k_launches > 1 else " (merges its own partials)")
+                      + " (one kvrt_append_attend_async call)",
+            "launches_per_call": k_launches,
             "achieved": round(achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",

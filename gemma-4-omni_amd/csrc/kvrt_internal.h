@@ -166,9 +166,16 @@ struct DecodeArgs {
     int32_t n_split;        // wave splits per (item, kv head) = gridDim.x * kWaves
     int32_t advance;        // the merge kernel adds qn to each item's length
     int32_t n_parts;        // partials per (item, kv head) the merge kernel combines
+    uint32_t *cnt;          // non-null: the decode merges its own partials (see kCntItems)
     float scale_log2;       // softmax scale * log2(e)
     int32_t slots[kMaxItems];
 };
+
+// Arrival counters of the single-launch decode, per context: one per (item,
+// kv head) at item * kv_heads + kvh, then one per item at kCntItemBase + item.
+// Every launch leaves them at zero.
+constexpr int kCntItemBase = kMaxItems * 64;
+constexpr int kCntWords = kCntItemBase + kMaxItems;
 
 // The split-K decode merges its 4 waves' partials in LDS (one partial per
 // workgroup) when R * D floats per wave fit.

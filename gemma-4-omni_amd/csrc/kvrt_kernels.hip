@@ -271,6 +271,102 @@ __device__ __forceinline__ uint32_t lds_addr(const T *p) {
 
 // LDS floats a decode workgroup needs for its cross-wave merge: the partials
 // of waves 1..3, when R * D is small enough to stage them.
+// Online merge of the partials sp = j, j + G, ... < n of one output element
+// into (M, L, O), 16 at a time; ld(sp, ml, acc) reads partial sp. The merge
+// kernel and the single-launch decode tail both use it, so the two paths
+// round identically.
+template <int G, class Ld>
+__device__ __forceinline__ void merge_partials(int j, int n, Ld ld, float &M, float &L, float &O) {
+    constexpr int B = 16;
+    for (int s0 = j; s0 < n; s0 += B * G) {
+        float2 m[B];
+        float v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int sp = s0 + u * G;
+            m[u] = make_float2(kNegBig, 0.f);
+            v[u] = 0.f;
+            if (sp < n) ld(sp, m[u], v[u]);
+        }
+        float bm = M;
+#pragma unroll
+        for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
+        const float c = __builtin_amdgcn_exp2f(M - bm);
+        L *= c;
+        O *= c;
+        M = bm;
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const float w = __builtin_amdgcn_exp2f(m[u].x - M);
+            L = fmaf(m[u].y, w, L);
+            O = fmaf(v[u], w, O);
+        }
+    }
+}
+
+// Agent-scope (cross-XCD) coherent accesses. On gfx950 a relaxed agent-scope
+// store is written through the XCD's L2 and a relaxed agent-scope load reads
+// past it, so data exchanged only through them needs no L2 write-back or
+// invalidate between workgroups, only the completion wait of the stores.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(float2 *p, float2 v) {
+    const uint64_t b = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent(const float2 *p) {
+    const uint64_t b = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float2 *>(p)), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
+}
+
+// Single-launch decode: after every workgroup has stored its partials (with
+// store_agent), the last workgroup of each (item, kv head) to arrive merges
+// them in the merge kernel's order and writes the output; the last of an
+// item's kv heads then advances the item's length. Every workgroup of the
+// grid reaches this point exactly once, which returns the counters to zero.
+template <int D, int R>
+__device__ __forceinline__ void decode_merge_tail(const DecodeArgs &a, int item, int kvh, int hkv, int rows) {
+    __shared__ uint32_t arrived;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
+    __syncthreads();
+    uint32_t *hc = a.cnt + item * hkv + kvh;
+    if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(hc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != gridDim.x - 1) return;
+    const int n_parts = gridDim.x;
+    const int Qn = a.qn;
+    const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
+    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
+        const int r = idx / D, d = idx % D;
+        const float2 *ml = a.part_ml + pbase + r;
+        const float *acc = a.part_acc + (pbase + r) * D + d;
+        float M = kNegBig, L = 0.f, O = 0.f;
+        merge_partials<1>(0, n_parts, [&](int sp, float2 &m, float &v) {
+            m = load_agent(ml + (int64_t)sp * R);
+            v = load_agent(acc + (int64_t)sp * R * D);
+        }, M, L, O);
+        const int jh = r / Qn, i = r % Qn;
+        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
+            f32_to_bf16(L > 0.f ? O / L : 0.f);
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(hc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.advance) {
+            // every workgroup of the item has read its length by now
+            uint32_t *ic = a.cnt + kCntItemBase + item;
+            if (__hip_atomic_fetch_add(ic, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)hkv - 1) {
+                __hip_atomic_store(ic, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                a.len.lens[(int64_t)a.slots[item] * a.len.stride + a.len.offset] += Qn;
+            }
+        }
+    }
+}
+
 template <int D, int R>
 struct DecodeLds {
     static constexpr bool kWgMerge = decode_wg_merge(D, R);
@@ -685,10 +781,17 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 for (int e = 0; e < EPL; ++e) o[e] = fmaf(src[e], ww, o[e]);
             }
             float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
+            if (a.cnt) {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) dst[e] = o[e];
-            if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+                for (int e = 0; e < EPL; ++e) store_agent(dst + e, o[e]);
+                if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) dst[e] = o[e];
+                if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+            }
         }
+        if (a.cnt) decode_merge_tail<D, R>(a, item, kvh, hkv, rows);
     } else if (sub == 0) {
         // one partial per wave
         const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + split) * R;
@@ -985,7 +1088,6 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
 // every decode workgroup has read the lengths by then.
 template <int D, int R, int G>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-    constexpr int B = 16;
     const int item = blockIdx.y, kvh = blockIdx.x, hkv = gridDim.x;
     const int n_parts = a.n_parts;
     const int Qn = a.qn;
@@ -998,30 +1100,10 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     const float2 *ml = a.part_ml + pbase + r;
     const float *acc = a.part_acc + (pbase + r) * D + d;
     float M = kNegBig, L = 0.f, O = 0.f;
-    for (int s0 = j; s0 < n_parts; s0 += B * G) {
-        float2 m[B];
-        float v[B];
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int sp = s0 + u * G;
-            const bool ok = live && sp < n_parts;
-            m[u] = ok ? ml[(int64_t)sp * R] : make_float2(kNegBig, 0.f);
-            v[u] = ok ? acc[(int64_t)sp * R * D] : 0.f;
-        }
-        float bm = M;
-#pragma unroll
-        for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
-        const float c = __builtin_amdgcn_exp2f(M - bm);
-        L *= c;
-        O *= c;
-        M = bm;
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const float w = __builtin_amdgcn_exp2f(m[u].x - M);
-            L = fmaf(m[u].y, w, L);
-            O = fmaf(v[u], w, O);
-        }
-    }
+    merge_partials<G>(j, live ? n_parts : 0, [&](int sp, float2 &m, float &v) {
+        m = ml[(int64_t)sp * R];
+        v = acc[(int64_t)sp * R * D];
+    }, M, L, O);
     if constexpr (G > 1) {
         const float Mg = group_max<G>(M);
         const float w = __builtin_amdgcn_exp2f(M - Mg);
@@ -1611,6 +1693,7 @@ static hipError_t launch_merge(const DecodeArgs &a, hipStream_t s) {
 
 template <int HD, int RT>
 static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s) {
+    if (a.cnt && !decode_wg_merge(HD, RT)) return hipErrorInvalidValue;  // no workgroup partials to merge
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     if (dtype == KVRT_INT8) {
         // int8 rows carry 16 values per lane: 16 query rows would not fit in registers
@@ -1624,12 +1707,13 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
             hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, LY>), grid, block, 0, s, a));
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.cnt) return e;
     return launch_merge<HD, RT>(a, s);
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s) {
-    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves) return hipErrorInvalidValue;
+    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves || a.cnt)
+        return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     const int rt = rows_tile(rows_per_head);
     auto go = [&](auto rc) -> hipError_t {
@@ -1664,10 +1748,11 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_
 
 template <int HD, int RT>
 static hipError_t launch_talker_rt(const TalkerArgs &a, hipStream_t s) {
+    if (a.cnt && !decode_wg_merge(HD, RT)) return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     hipLaunchKernelGGL((decode_kernel<HD, RT, KVRT_BF16, KVRT_LAYOUT_CONTIG, TalkerArgs>), grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.cnt) return e;
     return launch_merge<HD, RT>(a, s);
 }
 

@@ -66,6 +66,7 @@ struct kvrt_ctx {
     std::vector<int32_t> len;       // host shadow [slot * n_layers + layer]
     int32_t *d_len = nullptr;
     int32_t *d_err = nullptr;
+    uint32_t *d_cnt = nullptr;      // arrival counters of single-launch decodes [kCntWords], zero between launches
     bool paged = false;
     int pt_stride = 0;
     std::vector<int32_t> pt;        // host page table mirror, -1 unmapped
@@ -241,6 +242,18 @@ int min_keys_per_wave(int keys_per_iter) {
 #define KVRT_SPLIT_KEY_BUCKET 128
 #endif
 constexpr int64_t kSplitKeyBucket = KVRT_SPLIT_KEY_BUCKET;
+// Whether a VALU decode merges its workgroup partials in its last workgroup
+// (kvrt_config.decode_merge) instead of a second kernel. AUTO: when the
+// partials of one (item, kv head) total at most KVRT_SINGLE_LAUNCH_BYTES
+// (32 KiB): the merging workgroup reads them all, three dependent memory
+// round trips after the last partial lands, which costs about what the merge
+// kernel's launch does; beyond that one workgroup's read takes longer.
+bool single_launch_decode(int mode, int head_dim, int R, int rows, int n_parts) {
+    static const int limit = env_int("KVRT_SINGLE_LAUNCH_BYTES", 32768);
+    if (mode == KVRT_MERGE_SEPARATE || !decode_wg_merge(head_dim, R)) return false;
+    return mode == KVRT_MERGE_LAST_WG || (int64_t)n_parts * rows * head_dim * 4 <= limit;
+}
+
 int choose_splits(int target, int n_items, int kv_heads, int64_t max_keys, int keys_per_iter) {
     const int per_head = n_items * kv_heads;
     const int64_t per_wg = (int64_t)kWaves * min_keys_per_wave(keys_per_iter);
@@ -387,7 +400,8 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     if (cfg->struct_size != sizeof(kvrt_config)) return KVRT_EINVAL;
     if (cfg->n_layers <= 0 || cfg->n_layers > 4096 || cfg->n_slots <= 0 || cfg->n_slots > (1 << 20) ||
         cfg->capacity <= 0 || cfg->max_q <= 0 || cfg->max_q > 65536 || cfg->decode_wgs < 0 ||
-        cfg->decode_wgs > 65536 || cfg->decode_kernel < KVRT_DECODE_AUTO || cfg->decode_kernel > KVRT_DECODE_MFMA)
+        cfg->decode_wgs > 65536 || cfg->decode_kernel < KVRT_DECODE_AUTO || cfg->decode_kernel > KVRT_DECODE_MFMA ||
+        cfg->decode_merge < KVRT_MERGE_AUTO || cfg->decode_merge > KVRT_MERGE_LAST_WG)
         return KVRT_EINVAL;
     bool any_paged = false;
     for (int i = 0; i < cfg->n_layers; ++i) {
@@ -466,6 +480,8 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     if (launch_zero(c->d_len, len_bytes, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
     if (hipMalloc((void **)&c->d_err, 16) != hipSuccess) return fail(KVRT_EDEVICE);
     if (launch_zero(c->d_err, 16, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (hipMalloc((void **)&c->d_cnt, kCntWords * 4) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (launch_zero(c->d_cnt, kCntWords * 4, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
     if (any_paged) {
         c->pt_stride = (cfg->capacity + cfg->block_size - 1) / cfg->block_size;
         c->pt.assign((size_t)cfg->n_slots * c->pt_stride, -1);
@@ -605,9 +621,10 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.n_split = n_split;
     a.advance = fused ? 1 : 0;
     a.n_parts = (mfma || decode_wg_merge(D, R)) ? n_split / kWaves : n_split;
+    a.cnt = !mfma && single_launch_decode(c->cfg.decode_merge, D, R, rows, a.n_parts) ? c->d_cnt : nullptr;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
-    c->counters.launches += 2;
+    c->counters.launches += a.cnt ? 1 : 2;
     if (talker) {
         TalkerArgs t{};
         static_cast<DecodeArgs &>(t) = a;
@@ -795,6 +812,7 @@ int kvrt_destroy(kvrt_ctx *c) {
     if (c->d_desc) (void)hipFree(c->d_desc);
     if (c->d_len) (void)hipFree(c->d_len);
     if (c->d_err) (void)hipFree(c->d_err);
+    if (c->d_cnt) (void)hipFree(c->d_cnt);
     if (c->d_pt) (void)hipFree(c->d_pt);
     if (c->ws) (void)hipFree(c->ws);
     for (float *w : c->retired_ws) (void)hipFree(w);

@@ -70,6 +70,9 @@ class KvrtLayerSpec(ctypes.Structure):
 # kvrt_config.decode_kernel (kvrt.h KVRT_DECODE_*)
 KVRT_DECODE_AUTO, KVRT_DECODE_VALU, KVRT_DECODE_MFMA = 0, 1, 2
 DECODE_KERNELS = {"auto": KVRT_DECODE_AUTO, "valu": KVRT_DECODE_VALU, "mfma": KVRT_DECODE_MFMA}
+# kvrt_config.decode_merge (kvrt.h KVRT_MERGE_*)
+KVRT_MERGE_AUTO, KVRT_MERGE_SEPARATE, KVRT_MERGE_LAST_WG = 0, 1, 2
+DECODE_MERGES = {"auto": KVRT_MERGE_AUTO, "separate": KVRT_MERGE_SEPARATE, "last_wg": KVRT_MERGE_LAST_WG}
 
 
 class KvrtConfig(ctypes.Structure):
@@ -84,6 +87,7 @@ class KvrtConfig(ctypes.Structure):
         ("pool_seed", c_int32),
         ("decode_wgs", c_int32),
         ("decode_kernel", c_int32),
+        ("decode_merge", c_int32),
     ]
 
 

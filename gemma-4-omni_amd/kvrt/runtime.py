@@ -161,6 +161,7 @@ class KVRuntime:
         pool_seed: int = 0,
         decode_wgs: int = 0,
         decode_kernel: str = "auto",
+        decode_merge: str = "auto",
         device: torch.device | str | None = None,
     ) -> None:
         self.lib = L.load()
@@ -189,6 +190,9 @@ class KVRuntime:
         if decode_kernel not in L.DECODE_KERNELS:
             raise ValueError(f"decode_kernel must be one of {sorted(L.DECODE_KERNELS)}, got {decode_kernel!r}")
         cfg.decode_kernel = L.DECODE_KERNELS[decode_kernel]
+        if decode_merge not in L.DECODE_MERGES:
+            raise ValueError(f"decode_merge must be one of {sorted(L.DECODE_MERGES)}, got {decode_merge!r}")
+        cfg.decode_merge = L.DECODE_MERGES[decode_merge]
         self._cfg = cfg
         specs = (L.KvrtLayerSpec * len(self.layers))(*[s.to_c() for s in self.layers])
         self._specs = specs

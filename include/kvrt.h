@@ -122,6 +122,8 @@ typedef struct kvrt_config {
                              stream do better with fewer (e.g. 192)          */
     int32_t decode_kernel; /* KVRT_DECODE_*: which kernel runs bf16 decodes of
                              8 or 16 query rows per kv head                   */
+    int32_t decode_merge;  /* KVRT_MERGE_*: how a split-K decode combines its
+                             partial results                                  */
 } kvrt_config;
 
 /* kvrt_config.decode_kernel. AUTO: MFMA for 16 rows per kv head and for 8 rows
@@ -131,6 +133,20 @@ typedef struct kvrt_config {
 #define KVRT_DECODE_AUTO 0
 #define KVRT_DECODE_VALU 1
 #define KVRT_DECODE_MFMA 2
+
+/* kvrt_config.decode_merge. A split-K decode leaves one partial (running max,
+ * sum, output) per workgroup and kv head, combined by a merge step:
+ * SEPARATE: a second kernel launch merges them;
+ * LAST_WG: the last workgroup of each (slot, kv head) to finish merges them
+ *   inside the decode launch (one launch per layer); VALU decodes only —
+ *   MFMA decodes and 16-row tiles at head_dim 512 always use SEPARATE;
+ * AUTO: LAST_WG when a (slot, kv head) has at most 32 KiB of partials (one
+ *   workgroup reads them all), SEPARATE otherwise.
+ * Every mode gives the same results, bit for bit, when a (slot, kv head) has
+ * at most 16 partial workgroups; beyond that the merge order differs. */
+#define KVRT_MERGE_AUTO 0
+#define KVRT_MERGE_SEPARATE 1
+#define KVRT_MERGE_LAST_WG 2
 
 /* Optional caller-owned storage for one layer (kvrt_create_with_storage).
  * Sizes must equal kvrt_layer_storage_bytes for that layer. */

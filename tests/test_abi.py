@@ -70,7 +70,7 @@ int main(void) {
   F(kvrt_layer_spec, reserved);
   F(kvrt_config, struct_size); F(kvrt_config, n_layers); F(kvrt_config, n_slots); F(kvrt_config, capacity);
   F(kvrt_config, block_size); F(kvrt_config, pool_pages); F(kvrt_config, max_q); F(kvrt_config, pool_seed);
-  F(kvrt_config, decode_wgs); F(kvrt_config, decode_kernel);
+  F(kvrt_config, decode_wgs); F(kvrt_config, decode_kernel); F(kvrt_config, decode_merge);
   F(kvrt_storage, k); F(kvrt_storage, v); F(kvrt_storage, k_scale); F(kvrt_storage, v_scale);
   F(kvrt_counters, launches); F(kvrt_counters, appended_rows); F(kvrt_counters, appended_bytes);
   F(kvrt_counters, attended_keys); F(kvrt_counters, attended_bytes); F(kvrt_counters, gathered_bytes);
@@ -81,6 +81,8 @@ int main(void) {
   F(kvrt_talker_mask, visible_prefix_count); F(kvrt_talker_mask, prefix_log_gate);
   printf("\"const.KVRT_DECODE_AUTO\": [%d, 0], \"const.KVRT_DECODE_VALU\": [%d, 0], \"const.KVRT_DECODE_MFMA\": [%d, 0],\n",
          KVRT_DECODE_AUTO, KVRT_DECODE_VALU, KVRT_DECODE_MFMA);
+  printf("\"const.KVRT_MERGE_AUTO\": [%d, 0], \"const.KVRT_MERGE_SEPARATE\": [%d, 0], \"const.KVRT_MERGE_LAST_WG\": [%d, 0],\n",
+         KVRT_MERGE_AUTO, KVRT_MERGE_SEPARATE, KVRT_MERGE_LAST_WG);
   printf("\"sizeof.kvrt_tensor\": [%zu, 0], \"sizeof.kvrt_layer_spec\": [%zu, 0], \"sizeof.kvrt_config\": [%zu, 0],"
          " \"sizeof.kvrt_storage\": [%zu, 0], \"sizeof.kvrt_counters\": [%zu, 0],"
          " \"sizeof.kvrt_talker_mask\": [%zu, 0]\n}\n",
@@ -153,6 +155,8 @@ def test_layer_storage_bytes_per_layout():
     dict(cfg=dict(decode_wgs=-1)),
     dict(cfg=dict(decode_kernel=3)),
     dict(cfg=dict(decode_kernel=-1)),
+    dict(cfg=dict(decode_merge=3)),
+    dict(cfg=dict(decode_merge=-1)),
     dict(spec=dict(head_dim=96)),
     dict(spec=dict(kv_heads=0)),
     dict(spec=dict(dtype=1)),                                   # int8 needs PAGED

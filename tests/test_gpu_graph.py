@@ -11,11 +11,11 @@ from tests.helpers import bits, randn_bf16
 pytestmark = pytest.mark.gpu
 
 
-def _pair(specs, n_slots, capacity, gen, prefill):
+def _pair(specs, n_slots, capacity, gen, prefill, merge="auto"):
     from kvrt import KVRuntime
 
-    a = KVRuntime(specs, n_slots, capacity, max_q=1, device="cuda")
-    b = KVRuntime(specs, n_slots, capacity, max_q=1, device="cuda")
+    a = KVRuntime(specs, n_slots, capacity, max_q=1, decode_merge=merge, device="cuda")
+    b = KVRuntime(specs, n_slots, capacity, max_q=1, decode_merge=merge, device="cuda")
     for layer, spec in enumerate(specs):
         for s in range(n_slots):
             k = randn_bf16(gen, (1, spec.kv_heads, prefill, spec.head_dim)).cuda()
@@ -26,7 +26,8 @@ def _pair(specs, n_slots, capacity, gen, prefill):
     return a, b
 
 
-def test_graph_replays_match_eager_bitwise():
+@pytest.mark.parametrize("merge", ["auto", "separate", "last_wg"])
+def test_graph_replays_match_eager_bitwise(merge):
     from kvrt import LayerSpec
 
     gen = torch.Generator().manual_seed(21)
@@ -38,7 +39,7 @@ def test_graph_replays_match_eager_bitwise():
     hq = [16, 8, 8]
     n = 3
     steps = 6
-    a, b = _pair(specs, n, 1500, gen, prefill=1100)
+    a, b = _pair(specs, n, 1500, gen, prefill=1100, merge=merge)
     inputs = [[(randn_bf16(gen, (n, hq[l], 1, s.head_dim), 0.5).cuda(),
                 randn_bf16(gen, (n, s.kv_heads, 1, s.head_dim), 0.5).cuda(),
                 randn_bf16(gen, (n, s.kv_heads, 1, s.head_dim), 0.5).cuda()) for l, s in enumerate(specs)]

@@ -436,7 +436,10 @@ def run_kernels(args) -> int:
             fn = lambda: rt.append_attend(0, q, kn, vn, slots, sc, out=o)  # noqa: E731
         else:
             fn = lambda: rt.attend(0, q, slots, sc, out=o)  # noqa: E731
+        l0 = rt.counters()["launches"]
         t = _event_median(fn, w, r)
+        if rt.counters()["launches"] - l0 > w + r:  # the decode did not merge its own partials
+            kernel += " + merge_kernel"
         if rt.health() != 0:
             raise RuntimeError(f"kvrt health check failed in kernel case {name}")
         row = hkv * d * (1 if dtype == "int8" else 2) + (hkv * 4 if dtype == "int8" else 0)  # K or V bytes per position
@@ -450,16 +453,16 @@ def run_kernels(args) -> int:
 
     # the north-star step's talker and thinker launches at the step's workgroup targets; the
     # other shapes at the runtime default (kvrt_config.decode_wgs = 0)
-    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring) + merge", 16, 8, 128, 4, 4096,
+    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring)", 16, 8, 128, 4, 4096,
                 wgs=args.talker_wgs)
-    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig> + merge", 8, 1, 256, 4, 4096,
+    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig>", 8, 1, 256, 4, 4096,
                 wgs=args.thinker_wgs)
-    decode_case("decode_thinker_sliding", "decode_kernel<256,8,bf16,ring> + merge", 8, 1, 256, 4, 4096,
+    decode_case("decode_thinker_sliding", "decode_kernel<256,8,bf16,ring>", 8, 1, 256, 4, 4096,
                 window=512, layout="ring", wgs=args.thinker_wgs)
-    decode_case("decode_listener_q2_d512", "decode_mfma_kernel<512,16,contig> + merge", 8, 1, 512, 4, 8192, qn=2)
+    decode_case("decode_listener_q2_d512", "decode_mfma_kernel<512,16,contig>", 8, 1, 512, 4, 8192, qn=2)
     g4 = torch.Generator().manual_seed(4)
     lens5 = [int(x) for x in torch.randint(256, 8193, (16,), generator=g4)]
-    decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> + merge (attend only)", 16, 8, 128, 16, 0,
+    decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> (attend only)", 16, 8, 128, 16, 0,
                 window=4096, layout="paged", fused=False, dtype="int8", lens=lens5, block_size=16,
                 pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
 

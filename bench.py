@@ -56,7 +56,7 @@ def parse() -> argparse.Namespace:
                    help="session groups per model: each (model, group) gets its own kvrt context and HIP stream")
     p.add_argument("--one-stream", action="store_true",
                    help="run every launch on the caller's stream (default: one stream per model and group)")
-    p.add_argument("--kernel-reps", type=int, default=50, help="event-timed launches of the dominant kernel")
+    p.add_argument("--kernel-reps", type=int, default=50, help="event-timed repetitions of the dominant kernel (a layer sequence, and one launch alone)")
     p.add_argument("--talker-wgs", type=int, default=192,
                    help="split-K decode workgroups per talker launch (kvrt_config.decode_wgs)")
     p.add_argument("--thinker-wgs", type=int, default=192,
@@ -184,23 +184,46 @@ def step_bytes(streams: int, ctx_after: int) -> dict:
             "total": streams * (th + tk)}
 
 
-def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int, int]:
-    """Average duration of one talker-layer fused append + attention call over
-    one session group (the decode kernel, plus the merge kernel when the
-    decode does not merge its own partials), HIP events on the stream they run
-    on; also the algorithmic bytes and the kernel launches per call.
+def time_dominant_kernel(model: Model, reps: int) -> dict:
+    """Average duration of the talker-layer fused append + attention launch
+    (the decode kernel, plus the merge kernel when the decode does not merge
+    its own partials), HIP events on the stream the launches run on.
 
-    A GPU sleep ahead of each (event, launch, event) triple lets the host
-    enqueue all three before the GPU reaches them, so the events bracket the
-    kernels and not the host launch latency.
+    Each repetition runs the model's layers back to back, as the step does
+    (one launch per layer, each layer its own cache), between two events, and
+    divides by the number of layers: the per-launch average of a sequence of
+    launches, the duration rocprof reports per kernel. The time of one launch
+    alone (events around a single launch after a GPU sleep, which adds the
+    dispatch latency of an idle queue) is reported beside it. A GPU sleep ahead
+    of each repetition lets the host enqueue it before the GPU reaches it, so
+    the events bracket the kernels and not the host.
     """
-    q, k, v, o = model.bufs[0]
     stream = torch.cuda.current_stream()
-    times = []
+
+    def central_mean(times):
+        times = sorted(times)
+        # mean of the central 80 % (drop warm-up and preemption outliers)
+        lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
+        return sum(times[lo:hi]) / (hi - lo)
+
+    n_layers = len(model.bufs)
+    seq, single = [], []
     bytes_total = 0
     launches0 = model.rt.counters()["launches"]
     for _ in range(reps):
         L_before = model.rt.seq_length(0, 0)
+        torch.cuda._sleep(20_000_000)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        model.run()
+        e1.record(stream)
+        e1.synchronize()
+        seq.append(e0.elapsed_time(e1) * 1e-3 / n_layers)
+        bytes_total += step_bytes(len(model.slots), L_before + 1)["talker_layer"]
+    launches = (model.rt.counters()["launches"] - launches0) // (reps * n_layers)
+    q, k, v, o = model.bufs[0]
+    for _ in range(reps):
         torch.cuda._sleep(2_000_000)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -208,17 +231,13 @@ def time_dominant_kernel(model: Model, reps: int) -> tuple[float, int, int]:
         model.rt.append_attend(0, q, k, v, model.slots, model.scale, out=o)
         e1.record(stream)
         e1.synchronize()
-        times.append(e0.elapsed_time(e1) * 1e-3)
-        bytes_total += step_bytes(len(model.slots), L_before + 1)["talker_layer"]
-    times.sort()
-    # mean of the central 80 % (drop warm-up and preemption outliers)
-    lo, hi = int(0.1 * len(times)), max(int(0.9 * len(times)), int(0.1 * len(times)) + 1)
-    mean_t = sum(times[lo:hi]) / (hi - lo)
-    return mean_t, bytes_total // reps, (model.rt.counters()["launches"] - launches0) // reps
+        single.append(e0.elapsed_time(e1) * 1e-3)
+    return {"time": central_mean(seq), "bytes": bytes_total // reps, "launches": launches,
+            "single": central_mean(single)}
 
 
 def pmc_traffic() -> tuple[int | None, str | None]:
-    """HBM bytes per launch of the dominant launch pair, from the committed
+    """HBM bytes per launch of the dominant launch, from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a 256 MiB
     copy); None when that summary is absent."""
     path = ROOT / "profiles" / "pmc_traffic.json"
@@ -498,7 +517,7 @@ def main() -> int:
     if args.mode == "kernels":
         return run_kernels(args)
     gen = torch.Generator(device="cuda").manual_seed(1)
-    margin = args.warmup + args.steps + args.kernel_reps + 8
+    margin = args.warmup + args.steps + 2 * args.kernel_reps + 8
     capacity = args.ctx + margin
     if args.streams % args.groups:
         raise SystemExit("--streams must be a multiple of --groups")
@@ -552,7 +571,8 @@ def main() -> int:
     total_bytes = sum(step_bytes(args.streams, L)["total"] for L in range(len0 + 1, len1 + 1))
     ms = 1e3 * elapsed / args.steps
     tokens_per_step = 2 * args.streams
-    k_time, k_bytes, k_launches = time_dominant_kernel(talker0, args.kernel_reps)
+    dom = time_dominant_kernel(talker0, args.kernel_reps)
+    k_time, k_bytes, k_launches = dom["time"], dom["bytes"], dom["launches"]
     if talker0.rt.health() != 0:
         raise RuntimeError("kvrt health check failed after the kernel timing")
     achieved = k_bytes / k_time
@@ -607,6 +627,8 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": traffic_src,
             "avg_launch_us": round(k_time * 1e6, 3),
+            "timing": f"HIP events around the talker's {TALKER['layers']} layer launches back to back, per launch",
+            "single_launch_us": round(dom["single"] * 1e6, 3),
             "algorithmic_bytes_per_launch": k_bytes,
         },
         "cpu_baseline": cpu,

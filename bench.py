@@ -474,7 +474,7 @@ def run_kernels(args) -> int:
     # other shapes at the runtime default (kvrt_config.decode_wgs = 0)
     decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring)", 16, 8, 128, 4, 4096,
                 wgs=args.talker_wgs)
-    decode_case("decode_thinker_global", "decode_kernel<256,8,bf16,contig>", 8, 1, 256, 4, 4096,
+    decode_case("decode_thinker_global", "decode_mfma_kernel<256,8,contig>", 8, 1, 256, 4, 4096,
                 wgs=args.thinker_wgs)
     decode_case("decode_thinker_sliding", "decode_kernel<256,8,bf16,ring>", 8, 1, 256, 4, 4096,
                 window=512, layout="ring", wgs=args.thinker_wgs)

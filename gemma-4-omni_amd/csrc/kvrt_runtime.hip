@@ -206,13 +206,18 @@ bool is_contiguous(const kvrt_tensor *t) {
 constexpr int kMaxWgPerHead = 64;
 
 // Which bf16 decodes run on the MFMA kernel (kvrt_config.decode_kernel).
-// AUTO: 16 query rows per kv head (GQA group 8 with Q = 2), and 8 rows at
-// head_dim 512 — the shapes where the VALU kernel's dot products and P.V
-// products make it compute-bound. 8 rows at head_dim <= 256 stay on the VALU
-// kernel, which is as fast there and lighter on a concurrent stream.
-bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim) {
+// AUTO: 16 query rows per kv head (GQA group 8 with Q = 2), 8 rows at
+// head_dim 512, and 8 rows at head_dim <= 256 over at least
+// kMfmaDecodeMinKeys8 visible keys — the shapes where the VALU kernel's dot
+// products and P.V products make it compute-bound. Short 8-row decodes (a
+// 512-key sliding window) stay on the VALU kernel: latency-bound either way,
+// and lighter on a concurrent stream. `keys` is the launch's key count
+// rounded up to the split bucket, so the choice, like the split count, stays
+// fixed within a bucket.
+constexpr int64_t kMfmaDecodeMinKeys8 = 2048;
+bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t keys) {
     if (mode == KVRT_DECODE_VALU || dtype != KVRT_BF16 || rows_tile_ < kMfmaDecodeMinRows) return false;
-    return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512;
+    return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512 || keys >= kMfmaDecodeMinKeys8;
 }
 
 // Split-K workgroups a decode launch aims at: the context's decode_wgs, else
@@ -591,7 +596,8 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
     }
     const int R = rows_tile(rows);
-    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D);
+    const int64_t bucket_keys = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
+    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys);
     const int n_split = choose_splits(target_wgs(c->cfg, s.dtype), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
     const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
@@ -1447,9 +1453,10 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.qn = (int)qn;
     a.window = window;
     const int R = rows_tile(rows);
-    const bool mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D);
-    a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv,
-                              window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax,
+    const int64_t keys = window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax;
+    const bool mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D,
+                                      (keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket);
+    a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv, keys,
                               mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
     a.n_parts = (mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
     a.scale_log2 = scale * 1.4426950408889634f;

@@ -1070,10 +1070,17 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             for (int e = 0; e < EPL; ++e) acc[e] = fmaf(src[e], ww, acc[e]);
         }
         float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
+        if (a.cnt) {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) dst[e] = acc[e];
-        if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+            for (int e = 0; e < EPL; ++e) store_agent(dst + e, acc[e]);
+            if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[e] = acc[e];
+            if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+        }
     }
+    if (a.cnt) decode_merge_tail<D, R>(a, item, kvh, hkv, rows);
 }
 
 // grid (kv_heads, n_items, chunks), 256 threads: G consecutive threads merge
@@ -1712,8 +1719,7 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s) {
-    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves || a.cnt)
-        return hipErrorInvalidValue;
+    if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves) return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     const int rt = rows_tile(rows_per_head);
     auto go = [&](auto rc) -> hipError_t {
@@ -1722,7 +1728,7 @@ hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_he
             KVRT_DISPATCH_LAYOUT(a.kv.layout,
                 hipLaunchKernelGGL((decode_mfma_kernel<HD, RT, LY>), grid, block, 0, s, a));
             hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
+            if (e != hipSuccess || a.cnt) return e;
             return launch_merge<HD, RT>(a, s);
         });
         return hipErrorInvalidValue;

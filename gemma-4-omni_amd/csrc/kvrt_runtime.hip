@@ -247,15 +247,15 @@ int min_keys_per_wave(int keys_per_iter) {
 #define KVRT_SPLIT_KEY_BUCKET 128
 #endif
 constexpr int64_t kSplitKeyBucket = KVRT_SPLIT_KEY_BUCKET;
-// Whether a VALU decode merges its workgroup partials in its last workgroup
+// Whether a decode merges its workgroup partials in its last workgroup
 // (kvrt_config.decode_merge) instead of a second kernel. AUTO: when the
 // partials of one (item, kv head) total at most KVRT_SINGLE_LAUNCH_BYTES
 // (32 KiB): the merging workgroup reads them all, three dependent memory
 // round trips after the last partial lands, which costs about what the merge
 // kernel's launch does; beyond that one workgroup's read takes longer.
-bool single_launch_decode(int mode, int head_dim, int R, int rows, int n_parts) {
+bool single_launch_decode(int mode, bool mfma, int head_dim, int R, int rows, int n_parts) {
     static const int limit = env_int("KVRT_SINGLE_LAUNCH_BYTES", 32768);
-    if (mode == KVRT_MERGE_SEPARATE || !decode_wg_merge(head_dim, R)) return false;
+    if (mode == KVRT_MERGE_SEPARATE || !(mfma || decode_wg_merge(head_dim, R))) return false;
     return mode == KVRT_MERGE_LAST_WG || (int64_t)n_parts * rows * head_dim * 4 <= limit;
 }
 
@@ -627,7 +627,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.n_split = n_split;
     a.advance = fused ? 1 : 0;
     a.n_parts = (mfma || decode_wg_merge(D, R)) ? n_split / kWaves : n_split;
-    a.cnt = !mfma && single_launch_decode(c->cfg.decode_merge, D, R, rows, a.n_parts) ? c->d_cnt : nullptr;
+    a.cnt = single_launch_decode(c->cfg.decode_merge, mfma, D, R, rows, a.n_parts) ? c->d_cnt : nullptr;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches += a.cnt ? 1 : 2;

@@ -139,8 +139,8 @@ typedef struct kvrt_config {
  * sum, output) per workgroup and kv head, combined by a merge step:
  * SEPARATE: a second kernel launch merges them;
  * LAST_WG: the last workgroup of each (slot, kv head) to finish merges them
- *   inside the decode launch (one launch per layer); VALU decodes only —
- *   MFMA decodes and 16-row tiles at head_dim 512 always use SEPARATE;
+ *   inside the decode launch (one launch per layer); the VALU kernel's
+ *   16-row tiles at head_dim 512 (no workgroup partials) always use SEPARATE;
  * AUTO: LAST_WG when a (slot, kv head) has at most 32 KiB of partials (one
  *   workgroup reads them all), SEPARATE otherwise.
  * Every mode gives the same results, bit for bit, when a (slot, kv head) has

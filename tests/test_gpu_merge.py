@@ -26,6 +26,8 @@ _CASES = [
     (8, 1, 256, 1, "ring", 64, "bf16", 24),      # thinker sliding, 8 rows per kv head (VALU)
     (8, 1, 256, 1, "contig", 0, "bf16", 48),     # thinker global
     (2, 1, 512, 1, "contig", 0, "bf16", 48),     # D 512, DMA ring
+    (8, 1, 256, 2, "contig", 0, "bf16", 48),     # 16 rows per kv head: MFMA kernel
+    (8, 1, 512, 1, "contig", 0, "bf16", 48),     # 8 rows at D 512: MFMA kernel
     (16, 8, 128, 1, "paged", 0, "int8", 96),     # paged int8
     (16, 8, 128, 1, "paged", 0, "bf16", 96),
 ]

@@ -275,7 +275,7 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int dtype, int rows_
                          hipStream_t s);
 // The same decode with S and P.V on MFMA (bf16, row tiles 8 and 16), one
 // partial per workgroup; then the merge kernel.
-hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s);
+hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s);
 // The same split-K decode under the talker visibility (bf16 CONTIG layers).
 hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_head, hipStream_t s);
 // Chunked-prefill attention on MFMA (bf16 CONTIG / RING / PAGED layers).

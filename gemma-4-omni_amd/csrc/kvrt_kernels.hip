@@ -858,11 +858,20 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
 // transposed (ds_read_b64_tr_b16), and P as two bf16 terms. Lane layouts:
 // 16x16x32 A[i l%16][k 8(l/16)+j], 16x16x16 A[i l%16][k 4(l/16)+j],
 // B[k ..][n l%16], D[i 4(l/16)+v][n l%16]; column n is query row r.
-template <int D, int R, int LAYOUT>
+// Four int8 values (one dword) as four bf16 (two packed dwords); exact, as
+// every int8 value has at most 7 significant bits.
+__device__ __forceinline__ uint2 i8x4_to_bf16(uint32_t w) {
+    return make_uint2(pack_bf16x2((float)(int8_t)w, (float)(int8_t)(w >> 8)),
+                      pack_bf16x2((float)(int8_t)(w >> 16), (float)(int8_t)(w >> 24)));
+}
+
+template <int D, int R, int LAYOUT, int KDT = KVRT_BF16>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int T = kMfmaDecodeKeys;
     constexpr int KP = D + 8;  // V tile row pitch (bf16)
+    constexpr bool I8 = KDT == KVRT_INT8;
     static_assert(R == 8 || R == 16, "MFMA decode row tiles");
+    static_assert(!I8 || LAYOUT == KVRT_LAYOUT_PAGED, "int8 rows are PAGED");
     // the waves' V tiles while streaming, their partials for the merge after
     constexpr int kTileBytes = kWaves * T * KP * 2, kPartBytes = kWaves * R * D * 4;
     __shared__ __align__(16) uint8_t lds_raw[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
@@ -876,7 +885,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     const int Qn = a.qn;
     const int rows = a.group * Qn;
-    const bool fused = a.k_new != nullptr;
+    const bool fused = !I8 && a.k_new != nullptr;  // int8 rows are quantised by the append kernel
     int kend = fused ? len + Qn : len;
     if (LAYOUT == KVRT_LAYOUT_CONTIG && kend > a.kv.rows) {
         if (threadIdx.x == 0 && blockIdx.x == 0) a.err[0] = 1;
@@ -892,7 +901,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
 
     // Fused append: workgroup 0 of every (item, kv head) stores the new rows;
     // no workgroup of this launch reads them from the cache.
-    if (fused && blockIdx.x == 0) {
+    if (!I8 && fused && blockIdx.x == 0) {
         for (int c = threadIdx.x; c < Qn * (D / 8); c += blockDim.x) {
             const int r = c / (D / 8), sg = c % (D / 8);
             const int pos = len + r;
@@ -912,7 +921,11 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     }
 
     // Q^T as the B operand: column col is row r = col (q head kvh*g + r/Qn,
-    // query r % Qn); lane (col, grp) holds dims 32c + 8grp .. +7.
+    // query r % Qn); lane (col, grp) holds dims kdim(c) .. +7 of reduction
+    // step c, K's A operand the same dims of its key: 32c + 8grp (bf16), or
+    // 64(c/2) + 16grp + 8(c%2) for int8, so that a lane's two steps c, c + 1
+    // are one 16-byte int8 load.
+    auto kdim = [&](int c) { return I8 ? 64 * (c >> 1) + 16 * grp + 8 * (c & 1) : 32 * c + 8 * grp; };
     const int hq = hkv * a.group;
     const bool rvalid = col < rows;
     uint4 qop[D / 32];
@@ -920,9 +933,9 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         // every lane loads (rows past the tile's real rows read row 0), then
         // those lanes zero their operand: no branch around the loads
         const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
-        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D + 8 * grp;
+        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D;
 #pragma unroll
-        for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + 32 * c);
+        for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + kdim(c));
 #pragma unroll
         for (int c = 0; c < D / 32; ++c)
             if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
@@ -937,39 +950,76 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const uint16_t *sv_lane = sv + (4 * grp + (col >> 2)) * KP + 4 * (col & 3);
     bool bad = false;
     const int64_t new_base = ((int64_t)item * hkv + kvh) * Qn * D;
-    // Row address of key kk of the wave's range (keys past we read row ws and
-    // are masked; the rows of a fused append come from k_new / v_new).
-    auto key_rows = [&](int kk, const uint16_t *&kp, const uint16_t *&vp) __attribute__((always_inline)) {
+    // PAGED below D 512: the page-table entries of the wave's first 64 pages,
+    // one per lane, so that a tile finds its pages with a lane shuffle instead
+    // of a dependent global load ahead of its K/V loads (at D 512 the window
+    // does not fit the registers)
+    constexpr bool PWIN = LAYOUT == KVRT_LAYOUT_PAGED && D < 512;
+    int pwin = -1, pwin0 = 0;
+    if constexpr (PWIN) {
+        pwin0 = ws >> a.kv.block_shift;
+        const int lp = pwin0 + lane;
+        if (lp < a.kv.pt_stride) pwin = a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp];
+    }
+    // Row offset of key kk of the wave's range (keys past we read row ws and
+    // are masked; the rows of a fused append come from k_new / v_new: nw).
+    auto key_off = [&](int kk, int64_t &off, bool &nw) __attribute__((always_inline)) {
         const int kc = kk < we ? kk : ws;
-        int64_t off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+        if constexpr (PWIN) off = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
+        else off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
         if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
             bad |= kk < we && off < 0;
             off = off < 0 ? 0 : off;
         }
-        kp = static_cast<const uint16_t *>(a.kv.k) + off;
-        vp = static_cast<const uint16_t *>(a.kv.v) + off;
-        if (fused) {
-            const bool nw = kc >= len;
-            const int64_t on = new_base + (int64_t)(kc - len) * D;
-            kp = nw ? a.k_new + on : kp;
-            vp = nw ? a.v_new + on : vp;
+        nw = fused && kc >= len;
+        if (nw) off = new_base + (int64_t)(kc - len) * D;
+    };
+    auto key_rows = [&](int kk, const uint16_t *&kp, const uint16_t *&vp) __attribute__((always_inline)) {
+        int64_t off;
+        bool nw;
+        key_off(kk, off, nw);
+        kp = (nw ? a.k_new : static_cast<const uint16_t *>(a.kv.k)) + off;
+        vp = (nw ? a.v_new : static_cast<const uint16_t *>(a.kv.v)) + off;
+    };
+    // The K and V loads of a tile, as loaded (KR / VR 16-byte units per
+    // lane). bf16: K of the tile at t0 is the A operand (lane (col, grp): key
+    // t0 + col, dims kdim(c)), V units u = lane + 64i (key row u / (D/8), 16 B
+    // segment u % (D/8)). int8: K units of 16 dims (steps c, c + 1), V units
+    // u of 16 values (key row u / (D/16)), plus the K and V scales of key
+    // t0 + col; the tile converts them to bf16.
+    constexpr int KR = I8 ? D / 64 : D / 32, VR = I8 ? D / 64 : D / 32;
+    constexpr int VU = I8 ? D / 16 : D / 8;  // 16-byte units per V row
+    auto load_k = [&](int t0, uint4 (&ka)[KR], float &ks, float &vs) __attribute__((always_inline)) {
+        if constexpr (I8) {
+            int64_t off;
+            bool nw;
+            key_off(t0 + col, off, nw);
+            const int8_t *kp = static_cast<const int8_t *>(a.kv.k) + off;
+#pragma unroll
+            for (int c2 = 0; c2 < KR; ++c2) ka[c2] = load_stream16(kp + kdim(2 * c2));
+            ks = a.kv.ks[off / D];
+            vs = a.kv.vs[off / D];
+        } else {
+            const uint16_t *kp, *vp;
+            key_rows(t0 + col, kp, vp);
+#pragma unroll
+            for (int c = 0; c < KR; ++c) ka[c] = load_stream16(kp + kdim(c));
         }
     };
-    // K of the tile at t0 as the A operand (lane (col, grp): key t0 + col,
-    // dims 32c + 8grp); V of the tile as units u = lane + 64i (key row
-    // u / (D/8), 16 B segment u % (D/8)).
-    auto load_k = [&](int t0, uint4 (&ka)[D / 32]) __attribute__((always_inline)) {
-        const uint16_t *kp, *vp;
-        key_rows(t0 + col, kp, vp);
+    auto load_v = [&](int t0, uint4 (&vt)[VR]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < D / 32; ++c) ka[c] = load_stream16(kp + 32 * c + 8 * grp);
-    };
-    auto load_v = [&](int t0, uint4 (&vt)[D / 32]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i) {
-            const uint16_t *kp, *vp;
-            key_rows(t0 + (lane + 64 * i) / (D / 8), kp, vp);
-            vt[i] = load_stream16(vp + 8 * ((lane + 64 * i) % (D / 8)));
+        for (int i = 0; i < VR; ++i) {
+            const int u = lane + 64 * i;
+            if constexpr (I8) {
+                int64_t off;
+                bool nw;
+                key_off(t0 + u / VU, off, nw);
+                vt[i] = load_stream16(static_cast<const int8_t *>(a.kv.v) + off + 16 * (u % VU));
+            } else {
+                const uint16_t *kp, *vp;
+                key_rows(t0 + u / VU, kp, vp);
+                vt[i] = load_stream16(vp + 8 * (u % VU));
+            }
         }
     };
     // Software pipeline over the wave's tiles: tile t + 1's K is loaded into
@@ -979,9 +1029,10 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     // (PAGED at D 512 keeps one tile in flight: the page lookups of a second
     // tile do not fit the registers.)
     constexpr bool PIPE = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
-    uint4 ka[D / 32], vt[D / 32];
+    uint4 ka[KR], vt[VR];
+    float ksl = 0.f, vsl = 0.f;  // int8: scales of key t0 + col
     if (PIPE && ws < we) {
-        load_k(ws, ka);
+        load_k(ws, ka, ksl, vsl);
         load_v(ws, vt);
     }
     // The loop runs the tiles that have a successor with unconditional loads
@@ -991,17 +1042,41 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     auto tile = [&](int t0, auto more_c) __attribute__((always_inline)) {
         constexpr bool more = PIPE && decltype(more_c)::value;
         if constexpr (!PIPE) {
-            load_k(t0, ka);
+            load_k(t0, ka, ksl, vsl);
             load_v(t0, vt);
         }
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        float ksv[4], vsv[4];  // int8: K and V scales of this lane's keys t0 + 4grp + v
+        if constexpr (I8) {
 #pragma unroll
-        for (int c = 0; c < D / 32; ++c) s = mfma16(ka[c], qop[c], s);
-        if constexpr (more) load_k(t0 + T, ka);
+            for (int v = 0; v < 4; ++v) {
+                ksv[v] = __shfl(ksl, 4 * grp + v);
+                vsv[v] = __shfl(vsl, 4 * grp + v);
+            }
 #pragma unroll
-        for (int i = 0; i < D / 32; ++i) {
+            for (int c2 = 0; c2 < KR; ++c2) {
+                const uint2 a0 = i8x4_to_bf16(ka[c2].x), a1 = i8x4_to_bf16(ka[c2].y);
+                const uint2 a2 = i8x4_to_bf16(ka[c2].z), a3 = i8x4_to_bf16(ka[c2].w);
+                s = mfma16(make_uint4(a0.x, a0.y, a1.x, a1.y), qop[2 * c2], s);
+                s = mfma16(make_uint4(a2.x, a2.y, a3.x, a3.y), qop[2 * c2 + 1], s);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < KR; ++c) s = mfma16(ka[c], qop[c], s);
+        }
+        if constexpr (more) load_k(t0 + T, ka, ksl, vsl);
+#pragma unroll
+        for (int i = 0; i < VR; ++i) {
             const int u = lane + 64 * i;
-            *reinterpret_cast<uint4 *>(sv + (u / (D / 8)) * KP + 8 * (u % (D / 8))) = vt[i];
+            if constexpr (I8) {
+                const uint2 b0 = i8x4_to_bf16(vt[i].x), b1 = i8x4_to_bf16(vt[i].y);
+                const uint2 b2 = i8x4_to_bf16(vt[i].z), b3 = i8x4_to_bf16(vt[i].w);
+                uint4 *dst = reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 16 * (u % VU));
+                dst[0] = make_uint4(b0.x, b0.y, b1.x, b1.y);
+                dst[1] = make_uint4(b2.x, b2.y, b3.x, b3.y);
+            } else {
+                *reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 8 * (u % VU)) = vt[i];
+            }
         }
         if constexpr (more) load_v(t0 + T, vt);
         // this lane: keys t0 + 4grp + v of row col
@@ -1011,7 +1086,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         for (int v = 0; v < 4; ++v) {
             const int key = t0 + 4 * grp + v;
             const bool vis = key < we && key <= hi && key >= lo;
-            sc[v] = vis ? s[v] * a.scale_log2 : -INFINITY;
+            sc[v] = vis ? (I8 ? s[v] * ksv[v] : s[v]) * a.scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, sc[v]);
         }
         tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
@@ -1021,6 +1096,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         for (int v = 0; v < 4; ++v) {
             p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
             l += p[v];
+            if constexpr (I8) p[v] *= vsv[v];  // dequantise V through P
         }
         // P = P_hi + P_lo in bf16 (as in the prefill kernel)
         const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
@@ -1718,22 +1794,32 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
     return launch_merge<HD, RT>(a, s);
 }
 
-hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int rows_per_head, hipStream_t s) {
+// MFMA decode: 16-row tiles, and 8-row tiles for up to 8 rows per kv head;
+// int8 rows (PAGED, up to kMaxInt8Rows rows) are converted to bf16 operands.
+hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s) {
     if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves) return hipErrorInvalidValue;
+    if (dtype == KVRT_INT8 && (a.kv.layout != KVRT_LAYOUT_PAGED || rows_tile(rows_per_head) > kMaxInt8Rows))
+        return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     const int rt = rows_tile(rows_per_head);
     auto go = [&](auto rc) -> hipError_t {
         constexpr int RT = decltype(rc)::value;
         KVRT_DISPATCH_D(head_dim, {
-            KVRT_DISPATCH_LAYOUT(a.kv.layout,
-                hipLaunchKernelGGL((decode_mfma_kernel<HD, RT, LY>), grid, block, 0, s, a));
+            if (dtype == KVRT_INT8) {
+                if constexpr (RT <= kMaxInt8Rows)
+                    hipLaunchKernelGGL((decode_mfma_kernel<HD, RT, KVRT_LAYOUT_PAGED, KVRT_INT8>), grid, block, 0, s,
+                                       a);
+            } else {
+                KVRT_DISPATCH_LAYOUT(a.kv.layout,
+                    hipLaunchKernelGGL((decode_mfma_kernel<HD, RT, LY>), grid, block, 0, s, a));
+            }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || a.cnt) return e;
             return launch_merge<HD, RT>(a, s);
         });
         return hipErrorInvalidValue;
     };
-    if (rt == 8) return go(std::integral_constant<int, 8>{});
+    if (rt >= 1 && rt <= 8) return go(std::integral_constant<int, 8>{});
     if (rt == 16) return go(std::integral_constant<int, 16>{});
     return hipErrorInvalidValue;
 }

@@ -206,7 +206,7 @@ bool is_contiguous(const kvrt_tensor *t) {
 constexpr int kMaxWgPerHead = 64;
 
 // Which bf16 decodes run on the MFMA kernel (kvrt_config.decode_kernel).
-// AUTO: 16 query rows per kv head (GQA group 8 with Q = 2), 8 rows at
+// AUTO (bf16): 16 query rows per kv head (GQA group 8 with Q = 2), 8 rows at
 // head_dim 512, and 8 rows at head_dim <= 256 over at least
 // kMfmaDecodeMinKeys8 visible keys — the shapes where the VALU kernel's dot
 // products and P.V products make it compute-bound. Short 8-row decodes (a
@@ -216,7 +216,12 @@ constexpr int kMaxWgPerHead = 64;
 // fixed within a bucket.
 constexpr int64_t kMfmaDecodeMinKeys8 = 2048;
 bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t keys) {
-    if (mode == KVRT_DECODE_VALU || dtype != KVRT_BF16 || rows_tile_ < kMfmaDecodeMinRows) return false;
+    if (mode == KVRT_DECODE_VALU) return false;
+    // int8 (PAGED): AUTO keeps the VALU kernel; its page-window lookups and
+    // 16 keys per pass in 4 waves per SIMD beat the MFMA kernel's one 16-key
+    // tile in flight per wave at this row size (config 5: 32.6 vs 44.5 us)
+    if (dtype == KVRT_INT8) return mode == KVRT_DECODE_MFMA;
+    if (rows_tile_ < kMfmaDecodeMinRows) return false;
     return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512 || keys >= kMfmaDecodeMinKeys8;
 }
 
@@ -598,10 +603,11 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int R = rows_tile(rows);
     const int64_t bucket_keys = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
     const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys);
-    const int n_split = choose_splits(target_wgs(c->cfg, s.dtype), n, hkv, max_keys,
+    const int n_split = choose_splits(target_wgs(c->cfg, mfma ? KVRT_BF16 : s.dtype), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
-    const size_t acc_elems = (size_t)n * hkv * n_split * R * D;
-    int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, R, D));
+    const int Rw = mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial (MFMA tiles are 8 or 16)
+    const size_t acc_elems = (size_t)n * hkv * n_split * Rw * D;
+    int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, Rw, D));
     if (rc != KVRT_OK) return rc;
     std::vector<int32_t> pidx, pval;
     if (fused && s.layout == KVRT_LAYOUT_PAGED) {
@@ -643,7 +649,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         }
         return KVRT_OK;
     }
-    if ((mfma ? launch_decode_mfma(a, D, rows, c->stream) : launch_decode(a, D, s.dtype, rows, c->stream)) !=
+    if ((mfma ? launch_decode_mfma(a, D, s.dtype, rows, c->stream) : launch_decode(a, D, s.dtype, rows, c->stream)) !=
         hipSuccess)
         return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
@@ -1484,7 +1490,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.err = reinterpret_cast<int32_t *>(g_tensor_ws.ptr);
     a.part_acc = g_tensor_ws.ptr + kTensorWsHead;
     a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + kTensorWsHead + ((acc_elems + 63) / 64) * 64);
-    if ((mfma ? launch_decode_mfma(a, (int)D, rows, static_cast<hipStream_t>(stream))
+    if ((mfma ? launch_decode_mfma(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream))
               : launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream))) != hipSuccess)
         return KVRT_EDEVICE;
     return KVRT_OK;

@@ -126,11 +126,12 @@ typedef struct kvrt_config {
                              partial results                                  */
 } kvrt_config;
 
-/* kvrt_config.decode_kernel. AUTO: MFMA for 16 rows per kv head, and for 8
- * rows at head_dim 512 or over >= 2048 visible keys; the VALU kernel
- * otherwise. VALU / MFMA force one kernel for every eligible decode (MFMA:
- * bf16, 8 or 16 rows per kv head, not the talker masks; other decodes always
- * run on the VALU kernel). */
+/* kvrt_config.decode_kernel. AUTO: MFMA for bf16 decodes of 16 rows per kv
+ * head, and of 8 rows at head_dim 512 or over >= 2048 visible keys; the VALU
+ * kernel otherwise (int8 included). VALU / MFMA force one kernel for every
+ * eligible decode (MFMA: bf16 with 8 or 16 rows per kv head, or int8 PAGED
+ * with up to 8; not the talker masks; other decodes always run on the VALU
+ * kernel). */
 #define KVRT_DECODE_AUTO 0
 #define KVRT_DECODE_VALU 1
 #define KVRT_DECODE_MFMA 2

@@ -194,12 +194,13 @@ def test_fused_equals_append_then_attend_bitwise():
     np.testing.assert_array_equal(bits(rt_a.storage(0)[0]), bits(rt_b.storage(0)[0]))
 
 
-def test_paged_int8_quantise_dequantise_attend_and_evict():
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_paged_int8_quantise_dequantise_attend_and_evict(kernel):
     from kvrt import LayerSpec
 
     gen = torch.Generator().manual_seed(4)
     spec = LayerSpec(kv_heads=8, head_dim=128, layout="paged", dtype="int8", window=96)
-    rt = _rt([spec], n_slots=3, capacity=1024, max_q=1, block_size=16, pool_pages=128)
+    rt = _rt([spec], n_slots=3, capacity=1024, max_q=1, block_size=16, pool_pages=128, decode_kernel=kernel)
     orc = O.OracleCache(_oracle_layers([spec]), 3)
     lens = {0: 300, 2: 130}
     for s, n in lens.items():
@@ -228,8 +229,8 @@ def test_paged_int8_quantise_dequantise_attend_and_evict():
     assert c["pages_in_use"] <= 2 * (96 // 16 + 2) + 2
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "int8"])
-def test_paged_decode_past_the_preloaded_page_window(dtype):
+@pytest.mark.parametrize("dtype,kernel", [("bf16", "auto"), ("int8", "valu"), ("int8", "mfma")])
+def test_paged_decode_past_the_preloaded_page_window(dtype, kernel):
     """A wave preloads the page-table entries of its first 64 pages and looks
     further pages up directly: with one workgroup per (session, kv head)
     (decode_wgs 1) a 5000-key session gives each wave ~78 pages of 16 keys,
@@ -239,7 +240,7 @@ def test_paged_decode_past_the_preloaded_page_window(dtype):
     gen = torch.Generator().manual_seed(17)
     spec = LayerSpec(kv_heads=8, head_dim=128, layout="paged", dtype=dtype)
     rt = _rt([spec], n_slots=2, capacity=5200, max_q=1, block_size=16, pool_pages=700, pool_seed=9,
-             decode_wgs=1)
+             decode_wgs=1, decode_kernel=kernel)
     orc = O.OracleCache(_oracle_layers([spec]), 2)
     for s, n in ((0, 5000), (1, 777)):
         k = randn_bf16(gen, (1, 8, n, 128))
@@ -256,6 +257,41 @@ def test_paged_decode_past_the_preloaded_page_window(dtype):
         rt.append(0, k.cuda(), k.cuda(), [0, 1])
         for i in range(2):
             orc.append(i, 0, to_np(k[i]), to_np(k[i]))
+    assert rt.health() == 0
+
+
+@pytest.mark.parametrize("d,hq,hkv,qn", [(128, 16, 8, 1), (64, 4, 1, 2), (256, 8, 2, 2), (512, 8, 1, 1),
+                                         (128, 8, 8, 1), (128, 4, 1, 1)])
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_int8_paged_decode_matches_oracle(d, hq, hkv, qn, kernel):
+    """INT8 PAGED decode on both kernels (the MFMA kernel converts the int8
+    rows to bf16 operands and applies the K scale to the scores and the V
+    scale to the probabilities), head dims 64..512, 1..8 rows per kv head,
+    ragged lengths over a shuffled pool."""
+    from kvrt import LayerSpec
+
+    gen = torch.Generator().manual_seed(d + hq + qn)
+    spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="paged", dtype="int8")
+    rt = _rt([spec], n_slots=3, capacity=1100, max_q=2, block_size=16, pool_pages=3 * 72, pool_seed=3,
+             decode_kernel=kernel)
+    orc = O.OracleCache(_oracle_layers([spec]), 3)
+    slots = [2, 0, 1]
+    for s, n in zip(slots, (1000, 37, 431)):
+        k = randn_bf16(gen, (1, hkv, n, d))
+        v = randn_bf16(gen, (1, hkv, n, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    scale = 1 / math.sqrt(d)
+    for step in range(2):
+        q = randn_bf16(gen, (3, hq, qn, d), 0.5)
+        k = randn_bf16(gen, (3, hkv, qn, d), 0.5)
+        v = randn_bf16(gen, (3, hkv, qn, d), 0.5)
+        rt.append(0, k.cuda(), v.cuda(), slots)
+        out = rt.attend(0, q.cuda(), slots, scale)
+        for i, s in enumerate(slots):
+            orc.append(s, 0, to_np(k[i]), to_np(v[i]))
+            err = np.abs(to_np(out[i]) - orc.attend(s, 0, to_np(q[i]), scale)).max()
+            assert err <= ATOL, (step, s, err)
     assert rt.health() == 0
 
 

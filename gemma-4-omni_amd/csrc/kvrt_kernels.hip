@@ -21,6 +21,12 @@
 namespace kvrt {
 
 constexpr float kNegBig = -1.0e30f;  // running-max start; exp2(kNegBig - m) == 0
+// Lazy online softmax: a running max m (log2 units) moves only when a block's
+// max exceeds it by more than kRescaleSlack, so p = 2^(s - m) stays <= 2^8
+// and the accumulator rescale runs a few times per wave instead of on most
+// blocks. Exact: l and the accumulator always refer to the same m, and every
+// merge weights a partial by its own m.
+constexpr float kRescaleSlack = 8.0f;
 
 // Element offset of the first element of row (slot, head, pos); -1 if the
 // page is unmapped or out of the pool.
@@ -687,18 +693,32 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 }
             }
         }
-        // online softmax, one rescale per block of U keys
+        // online softmax, one update per block of U keys; int8 decodes keep a
+        // lazy running max (they are VALU-bound: the skipped rescales are ~9 %
+        // of their instructions; config 5 32.8 -> 31.4 us), bf16 ones update
+        // it every block (the branch slowed the bandwidth-bound talker launch
+        // by 0.4 us and the sliding-window one by the same)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float mb = s[0][r];
 #pragma unroll
             for (int u = 1; u < U; ++u) mb = fmaxf(mb, s[u][r]);
-            const float mn = fmaxf(m_run[r], mb);
-            const float corr = __builtin_amdgcn_exp2f(m_run[r] - mn);
-            m_run[r] = mn;
-            l_run[r] *= corr;
+            if constexpr (KDT == KVRT_INT8) {
+                if (mb > m_run[r] + kRescaleSlack) {
+                    const float corr = __builtin_amdgcn_exp2f(m_run[r] - mb);
+                    m_run[r] = mb;
+                    l_run[r] *= corr;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) acc[r][e] *= corr;
+                    for (int e = 0; e < VEC; ++e) acc[r][e] *= corr;
+                }
+            } else {
+                const float mn = fmaxf(m_run[r], mb);
+                const float corr = __builtin_amdgcn_exp2f(m_run[r] - mn);
+                m_run[r] = mn;
+                l_run[r] *= corr;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc[r][e] *= corr;
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -821,12 +841,8 @@ __device__ __forceinline__ f32x4_t mfma16k16(uint2 a, uint2 b, f32x4_t c) {
                                                      c, 0, 0, 0);
 }
 // Online-softmax update of an MFMA accumulator column with a lazy reference
-// max: m (log2 units, uniform per column) moves only when the tile's max
-// exceeds it by more than kRescaleSlack, so p = 2^(s - m) stays <= 2^8 and
-// the l / o rescale (o lives in AGPRs: a read, multiply and write per
-// element) runs a few times per wave instead of on most tiles. Exact: l and
-// o always refer to the same m, and the merges weight partials by their own m.
-constexpr float kRescaleSlack = 8.0f;
+// max (kRescaleSlack): the l / o rescale (o lives in AGPRs: a read, multiply
+// and write per element) runs a few times per wave instead of on most tiles.
 template <int NB>
 __device__ __forceinline__ void lazy_rescale(float tmax, float &m, float &l, f32x4_t (&o)[NB]) {
     if (tmax > m + kRescaleSlack) {
@@ -962,24 +978,32 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         if (lp < a.kv.pt_stride) pwin = a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp];
     }
     // Row offset of key kk of the wave's range (keys past we read row ws and
-    // are masked; the rows of a fused append come from k_new / v_new: nw).
-    auto key_off = [&](int kk, int64_t &off, bool &nw) __attribute__((always_inline)) {
+    // are masked).
+    auto key_off = [&](int kk) __attribute__((always_inline)) {
         const int kc = kk < we ? kk : ws;
+        int64_t off;
         if constexpr (PWIN) off = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
         else off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
         if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
             bad |= kk < we && off < 0;
             off = off < 0 ? 0 : off;
         }
-        nw = fused && kc >= len;
-        if (nw) off = new_base + (int64_t)(kc - len) * D;
+        return off;
     };
+    // bf16 row addresses; the rows of a fused append come from k_new / v_new
+    // (address selects under a uniform branch: a divergent branch here splits
+    // the tile's loads and makes the compiler wait on the earlier ones)
     auto key_rows = [&](int kk, const uint16_t *&kp, const uint16_t *&vp) __attribute__((always_inline)) {
-        int64_t off;
-        bool nw;
-        key_off(kk, off, nw);
-        kp = (nw ? a.k_new : static_cast<const uint16_t *>(a.kv.k)) + off;
-        vp = (nw ? a.v_new : static_cast<const uint16_t *>(a.kv.v)) + off;
+        const int64_t off = key_off(kk);
+        kp = static_cast<const uint16_t *>(a.kv.k) + off;
+        vp = static_cast<const uint16_t *>(a.kv.v) + off;
+        if (fused) {
+            const int kc = kk < we ? kk : ws;
+            const bool nw = kc >= len;
+            const int64_t on = new_base + (int64_t)(kc - len) * D;
+            kp = nw ? a.k_new + on : kp;
+            vp = nw ? a.v_new + on : vp;
+        }
     };
     // The K and V loads of a tile, as loaded (KR / VR 16-byte units per
     // lane). bf16: K of the tile at t0 is the A operand (lane (col, grp): key
@@ -991,9 +1015,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int VU = I8 ? D / 16 : D / 8;  // 16-byte units per V row
     auto load_k = [&](int t0, uint4 (&ka)[KR], float &ks, float &vs) __attribute__((always_inline)) {
         if constexpr (I8) {
-            int64_t off;
-            bool nw;
-            key_off(t0 + col, off, nw);
+            const int64_t off = key_off(t0 + col);
             const int8_t *kp = static_cast<const int8_t *>(a.kv.k) + off;
 #pragma unroll
             for (int c2 = 0; c2 < KR; ++c2) ka[c2] = load_stream16(kp + kdim(2 * c2));
@@ -1011,9 +1033,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         for (int i = 0; i < VR; ++i) {
             const int u = lane + 64 * i;
             if constexpr (I8) {
-                int64_t off;
-                bool nw;
-                key_off(t0 + u / VU, off, nw);
+                const int64_t off = key_off(t0 + u / VU);
                 vt[i] = load_stream16(static_cast<const int8_t *>(a.kv.v) + off + 16 * (u % VU));
             } else {
                 const uint16_t *kp, *vp;

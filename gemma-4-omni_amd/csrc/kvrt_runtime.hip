@@ -1405,10 +1405,16 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     a.group = group;
     a.qn = (int)qn;
     a.window = s.window;
-    // q heads per workgroup: the largest divisor of the group a workgroup
-    // can hold (each further part of the group stages the K/V tiles again)
+    // q heads per workgroup: the largest divisor of the group up to 8 at
+    // D 512 and up to 4 below (each further part of the group stages the K/V
+    // tiles again, but at D <= 256 twice the workgroups of 4 heads fill more
+    // of the chip: thinker sliding Q 291 44.0 -> 40.2 us, Q 2048 112.8 ->
+    // 107.1 us; at D 512 four heads per workgroup take 1.9x as long);
+    // KVRT_PF_HEADS_PER_WG lowers the cap
+    static const int hw_env = env_int("KVRT_PF_HEADS_PER_WG", kPfMaxHeads);
+    const int hw_cap = std::min(hw_env, D <= 256 ? 4 : kPfMaxHeads);
     int hw = 1;
-    for (int d = 1; d <= std::min(group, kPfMaxHeads); ++d)
+    for (int d = 1; d <= std::min({group, kPfMaxHeads, hw_cap}); ++d)
         if (group % d == 0) hw = d;
     a.heads_per_wg = hw;
     a.scale_log2 = scale * 1.4426950408889634f;

@@ -33,8 +33,10 @@ constexpr int keys_unroll(int R) { return R <= 4 ? 8 : (R == 8 ? KVRT_UNROLL8 : 
 // into LDS (global_load_lds_dwordx4) through a ring of kDmaStages stages of
 // dma_unroll(R) key groups per wave, so the next stages stay in flight while a
 // wave computes on the current one without holding registers for them.
+// 4 groups x 2 stages (68 KB of LDS per workgroup) give the shortest
+// two-stream step with the single-launch decode (3, 5 and 6 groups measured).
 #ifndef KVRT_DMA_UNROLL
-#define KVRT_DMA_UNROLL 3
+#define KVRT_DMA_UNROLL 4
 #endif
 #ifndef KVRT_DMA_STAGES
 #define KVRT_DMA_STAGES 2

@@ -147,7 +147,16 @@ class TalkerMask:
 
 
 class KVRuntime:
-    """One kvrt context: the KV state of ``n_slots`` sessions over ``layers``."""
+    """One kvrt context: the KV state of ``n_slots`` sessions over ``layers``.
+
+    Launch tuning (``kvrt_config``): ``decode_wgs`` is the split-K workgroup
+    target of a decode launch (0: the library default); ``decode_kernel``
+    ("auto", "valu", "mfma") picks the kernel of 8- and 16-row bf16 decodes
+    (and, forced to "mfma", of int8 ones); ``decode_merge`` ("auto",
+    "separate", "last_wg") picks whether a decode's last workgroup per (slot,
+    kv head) merges the split-K partials inside the launch or a second kernel
+    does. One stream per context: overlapping calls race on its workspace.
+    """
 
     def __init__(
         self,

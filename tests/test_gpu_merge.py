@@ -138,3 +138,40 @@ def test_talker_masks_last_workgroup_merge_equals_the_merge_kernel():
         np.testing.assert_array_equal(bits(outs["separate"]), bits(outs["last_wg"]), err_msg=f"step {step}")
     for rt in rts.values():
         assert rt.health() == 0
+
+
+def test_last_workgroup_merge_many_layers_and_steps():
+    """The talker topology of the north-star step (28 layers, 4 streams,
+    16 / 8 heads, D 128, fused append) for 8 steps, fresh q/k/v per layer and
+    step: 224 single-launch decodes, each compared bit for bit with the merge
+    kernel's result, so that a partial read before it landed, or a counter
+    left non-zero by an earlier launch, shows up."""
+    from kvrt import LayerSpec
+
+    gen = torch.Generator().manual_seed(41)
+    specs = [LayerSpec(kv_heads=8, head_dim=128)] * 28
+    rts = {m: _runtime_layers(specs, 4, 700, m) for m in ("separate", "last_wg")}
+    for layer in range(28):
+        k = randn_bf16(gen, (1, 8, 600, 128)).cuda()
+        v = randn_bf16(gen, (1, 8, 600, 128)).cuda()
+        for rt in rts.values():
+            for s in range(4):
+                rt.import_(s, layer, k, v)
+    slots = [0, 1, 2, 3]
+    for step in range(8):
+        for layer in range(28):
+            q = randn_bf16(gen, (4, 16, 1, 128), 0.5).cuda()
+            k = randn_bf16(gen, (4, 8, 1, 128), 0.5).cuda()
+            v = randn_bf16(gen, (4, 8, 1, 128), 0.5).cuda()
+            outs = {m: rt.append_attend(layer, q, k, v, slots, 0.088) for m, rt in rts.items()}
+            np.testing.assert_array_equal(bits(outs["separate"]), bits(outs["last_wg"]),
+                                          err_msg=f"step {step} layer {layer}")
+    for rt in rts.values():
+        assert rt.health() == 0
+        assert rt.seq_length(3, 27) == 608
+
+
+def _runtime_layers(specs, n, capacity, merge):
+    from kvrt import KVRuntime
+
+    return KVRuntime(specs, n, capacity, max_q=1, decode_wgs=192, decode_merge=merge, device="cuda")

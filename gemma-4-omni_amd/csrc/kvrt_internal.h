@@ -218,6 +218,9 @@ struct PrefillArgs {
     int32_t qn;             // Q (query rows per item)
     int32_t window;
     int32_t heads_per_wg;   // q heads of the group served by one workgroup (divides group)
+    int32_t n_ksplit;       // key ranges per query block; > 1: partials to part_o / part_ml
+    float *part_o;          // [n, Hq, Q, n_ksplit, D] unnormalised outputs
+    float2 *part_ml;        // [n, Hq, Q, n_ksplit] (running max in log2 units, sum)
     float scale_log2;
     int32_t slots[kMaxItems];
 };

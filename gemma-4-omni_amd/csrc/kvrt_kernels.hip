@@ -1361,14 +1361,24 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     const int Qn = a.qn;
-    const int qrow0 = blockIdx.x * 16;
+    const int nks = a.n_ksplit, ks = blockIdx.x % nks;
+    const int qrow0 = (blockIdx.x / nks) * 16;
     const int base_pos = L - Qn;               // position of query row 0
     const int qr = qrow0 + col;                // this lane's query row (S^T / O^T column)
     const bool qvalid = computes && qr < Qn;
     const int pq = base_pos + qr;
     const int lo_q = a.window > 0 ? pq - a.window + 1 : 0;
-    const int kend = base_pos + min(Qn, qrow0 + 16);  // keys < kend: up to the block's last query
-    const int kstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
+    // the block's keys: up to its last query, from its first query's window;
+    // with a key split, part ks of them in whole tiles
+    int kend = base_pos + min(Qn, qrow0 + 16);
+    int kstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
+    if (nks > 1) {
+        const int span = (kend - kstart + nks - 1) / nks;
+        const int part = (span + kPfKeys - 1) / kPfKeys * kPfKeys;
+        const int k0 = kstart + ks * part;
+        kend = min(kend, k0 + part);
+        kstart = min(k0, kend);
+    }
 
     // Q^T as the B operand: lane (col, grp) holds d = 32c + 8grp .. +7 of query qr.
     uint4 qop[D / 32];
@@ -1535,6 +1545,15 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     if (!computes) return;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));
     if (!qvalid) return;
+    if (nks > 1) {  // this key range's partial: o unnormalised, (m, l)
+        const int64_t pi = (((int64_t)item * hq + head) * Qn + qr) * nks + ks;
+        float *po = a.part_o + pi * D + 4 * grp;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b)
+            *reinterpret_cast<float4 *>(po + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+        if (grp == 0) a.part_ml[pi] = make_float2(m, l);
+        return;
+    }
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     uint16_t *op = a.out + (((int64_t)item * hq + head) * Qn + qr) * D + 4 * grp;
 #pragma unroll
@@ -1543,6 +1562,24 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         const uint32_t w1 = (uint32_t)f32_to_bf16(o[b][2] * inv) | ((uint32_t)f32_to_bf16(o[b][3] * inv) << 16);
         *reinterpret_cast<uint2 *>(op + 16 * b) = make_uint2(w0, w1);
     }
+}
+
+// Merge of a key-split prefill: one thread per (item, q head, query, dim),
+// the n_ksplit partials in key order (merge_partials), bf16 out.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int D, int64_t outs) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= outs) return;
+    const int64_t row = t / D;  // (item, q head, query)
+    const int d = (int)(t % D);
+    const int nks = a.n_ksplit;
+    const float2 *ml = a.part_ml + row * nks;
+    const float *po = a.part_o + row * nks * D + d;
+    float M = kNegBig, L = 0.f, O = 0.f;
+    merge_partials<1>(0, nks, [&](int sp, float2 &m, float &v) {
+        m = ml[sp];
+        v = po[(int64_t)sp * D];
+    }, M, L, O);
+    a.out[t] = f32_to_bf16(L > 0.f ? O / L : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1885,7 +1922,8 @@ hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int hw = a.heads_per_wg;
     if (hw <= 0 || a.group % hw != 0 || hw > kPfMaxHeads) return hipErrorInvalidValue;
-    dim3 grid((a.qn + 15) / 16, a.kv.kv_heads * (a.group / hw), a.n_items);
+    if (a.n_ksplit < 1 || (a.n_ksplit > 1 && (!a.part_o || !a.part_ml))) return hipErrorInvalidValue;
+    dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
     // 4 or 8 waves; D = 512 keeps no tile in flight across the MFMAs (registers)
     if (hw > 4) {
         KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
@@ -1894,6 +1932,10 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
         KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
             hipLaunchKernelGGL((prefill_kernel<HD, LY, 4, (HD < 512)>), grid, dim3(256), 0, s, a)));
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.n_ksplit == 1) return e;
+    const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim, outs);
     return hipGetLastError();
 }
 

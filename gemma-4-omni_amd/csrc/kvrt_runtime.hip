@@ -1382,6 +1382,7 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     const int group = (int)(hq / hkv);
     if (!std::isfinite(scale)) return KVRT_EINVAL;
     uint64_t tile_keys = 0;
+    int64_t block_keys = 0;  // most keys any 16-query block sees
     for (int i = 0; i < n; ++i) {
         const int L = c->len_at(slots[i], layer);
         if (L < qn) return KVRT_ESTATE;
@@ -1393,6 +1394,7 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
             const int64_t kend = L - qn + std::min<int64_t>(qn, q0 + 16);
             const int64_t kstart = s.window > 0 ? std::max<int64_t>(0, L - qn + q0 - s.window + 1) : 0;
             tile_keys += (uint64_t)(kend - kstart);
+            block_keys = std::max<int64_t>(block_keys, kend - kstart);
         }
     }
     PrefillArgs a{};
@@ -1417,9 +1419,35 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     for (int d = 1; d <= std::min({group, kPfMaxHeads, hw_cap}); ++d)
         if (group % d == 0) hw = d;
     a.heads_per_wg = hw;
+    // Key split: when the query blocks give fewer than 128 workgroups (a short
+    // chunk over a long context: thinker full layers, Q 291 over 2048 keys,
+    // 76 workgroups on 256 CUs), each block's keys are cut into n_ksplit
+    // ranges of >= 256 keys, as many as keep the grid within 256 workgroups
+    // (one round: a D 512 workgroup holds 135 KB of LDS, one per CU); a merge
+    // kernel then combines the ranges' partials. Q 291 at D 512: 253.6 us
+    // unsplit, 168.9 / 133.9 / 171.7 / 148.6 us with 2 / 3 / 4 / 6 ranges.
+    // Not inside a capture that would need a larger workspace.
+    // KVRT_PF_KSPLIT=1 turns it off, n >= 2 forces n ranges.
+    static const int ksplit_env = env_int("KVRT_PF_KSPLIT", 0);
+    a.n_ksplit = 1;
+    const int64_t wgs1 = (int64_t)((qn + 15) / 16) * hkv * (group / hw) * n;
+    if (ksplit_env != 1 && (ksplit_env > 1 || wgs1 < 128) && block_keys >= 512) {
+        const int64_t want = ksplit_env > 1 ? ksplit_env : std::min<int64_t>(256 / wgs1, block_keys / 256);
+        const int nks = (int)std::max<int64_t>(1, std::min<int64_t>(want, 16));
+        const size_t po = ((size_t)n * hq * qn * nks * D + 63) / 64 * 64;
+        const size_t bytes = po * 4 + (size_t)n * hq * qn * nks * 8 + 256;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        const bool capturing = hipStreamIsCapturing(c->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+        if (nks > 1 && (bytes <= c->ws_bytes || (!capturing && ensure_workspace(c, bytes) == KVRT_OK))) {
+            a.n_ksplit = nks;
+            a.part_o = c->ws;
+            a.part_ml = reinterpret_cast<float2 *>(c->ws + po);
+        }
+        if (c->poisoned) return KVRT_EDEVICE;
+    }
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
-    c->counters.launches++;
+    c->counters.launches += a.n_ksplit > 1 ? 2 : 1;
     if (launch_prefill(a, D, c->stream) != hipSuccess) return poison(c);
     c->counters.attended_keys += tile_keys * hkv;
     c->counters.attended_bytes += tile_keys * hkv * (uint64_t)D * 2 * 2;

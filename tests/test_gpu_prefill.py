@@ -72,6 +72,10 @@ def _check(rt, orc, q, scale, prefill=True):
         (8, 1, 256, 0, "contig", [300], 3),          # Q3 text append
         (4, 4, 64, 0, "paged", [45, 300], 37),       # paged pool
         (4, 2, 128, 24, "paged", [200], 50),         # paged + window
+        # few query blocks over many keys: the keys of a block are split over
+        # workgroups and the partials merged (8 and 2 key ranges)
+        (8, 1, 512, 0, "contig", [2000, 900], 64),
+        (4, 2, 128, 600, "paged", [1500], 40),
     ],
 )
 def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):

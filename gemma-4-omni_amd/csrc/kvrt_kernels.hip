@@ -1354,15 +1354,27 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
-    const int item = blockIdx.z, kvh = blockIdx.y / nhb, hkv = gridDim.y / nhb;
+    // Dispatch order: workgroups start in linear id order, so the id maps to
+    // (query block, key range, head part, item) with the query block most
+    // significant and the last blocks first. Without a window the last blocks
+    // see the most keys: the longest workgroups start first and the grid's
+    // tail is short ones.
+    const int nks = a.n_ksplit;
+    const int nqb = gridDim.x / nks;
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int per_qb = nks * gridDim.y * gridDim.z;
+    const int qb = nqb - 1 - lin / per_qb;
+    const int ks = lin % nks;
+    const int by = (lin / nks) % gridDim.y;
+    const int item = (lin / (nks * gridDim.y)) % gridDim.z;
+    const int kvh = by / nhb, hkv = gridDim.y / nhb;
     const int g = a.group, hq = hkv * g;
     const bool computes = wave < hw;
-    const int head = kvh * g + (blockIdx.y % nhb) * hw + (computes ? wave : 0);
+    const int head = kvh * g + (by % nhb) * hw + (computes ? wave : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     const int Qn = a.qn;
-    const int nks = a.n_ksplit, ks = blockIdx.x % nks;
-    const int qrow0 = (blockIdx.x / nks) * 16;
+    const int qrow0 = qb * 16;
     const int base_pos = L - Qn;               // position of query row 0
     const int qr = qrow0 + col;                // this lane's query row (S^T / O^T column)
     const bool qvalid = computes && qr < Qn;

@@ -169,6 +169,7 @@ struct DecodeArgs {
     int32_t advance;        // the merge kernel adds qn to each item's length
     int32_t n_parts;        // partials per (item, kv head) the merge kernel combines
     uint32_t *cnt;          // non-null: the decode merges its own partials (see kCntItems)
+    uint8_t order[kMaxItems];  // PAGED: item of grid z-index i, the most visible keys first
     float scale_log2;       // softmax scale * log2(e)
     int32_t slots[kMaxItems];
 };

@@ -417,7 +417,12 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int wave = threadIdx.x >> 6;
     const int sub = lane / LPR;
     const int seg = lane % LPR;
-    const int item = blockIdx.z;
+    // workgroups start in linear id order, z slowest: PAGED items (pools of
+    // ragged sessions) come sorted by visible keys, longest first, so the
+    // grid ends on short ones; other layouts keep z (the indirection is a
+    // dependent argument load ahead of every workgroup's first load: +1 % on
+    // the north-star step, whose items are equally long)
+    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? a.order[blockIdx.z] : (int)blockIdx.z;
     const int kvh = blockIdx.y;
     const int hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
@@ -895,7 +900,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     uint16_t *sv_all = reinterpret_cast<uint16_t *>(lds_raw);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int item = blockIdx.z, kvh = blockIdx.y, hkv = gridDim.y;
+    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? a.order[blockIdx.z] : (int)blockIdx.z;
+    const int kvh = blockIdx.y, hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];

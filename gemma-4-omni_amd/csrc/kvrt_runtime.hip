@@ -589,6 +589,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     // host-side state checks
     int64_t max_keys = 0;
     std::vector<int> from(n);
+    std::vector<int64_t> item_keys(n);
     for (int i = 0; i < n; ++i) {
         const int L = c->len_at(slots[i], layer);
         const int Lnew = fused ? L + (int)qn : L;
@@ -598,7 +599,8 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         if (s.layout == KVRT_LAYOUT_PAGED && Lnew - (int)qn - s.window + 1 < c->first_live[slots[i]] * c->cfg.block_size &&
             (s.window == 0 || c->first_live[slots[i]] > 0))
             return KVRT_ESTATE;  // the window would read evicted pages
-        max_keys = std::max<int64_t>(max_keys, talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn));
+        item_keys[i] = talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn);
+        max_keys = std::max<int64_t>(max_keys, item_keys[i]);
     }
     const int R = rows_tile(rows);
     const int64_t bucket_keys = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
@@ -636,6 +638,12 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.cnt = single_launch_decode(c->cfg.decode_merge, mfma, D, R, rows, a.n_parts) ? c->d_cnt : nullptr;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
+    // grid z order: most visible keys first (stable), so that a ragged batch's
+    // longest workgroups start first
+    std::vector<int> ord(n);
+    for (int i = 0; i < n; ++i) ord[i] = i;
+    std::stable_sort(ord.begin(), ord.end(), [&](int x, int y) { return item_keys[x] > item_keys[y]; });
+    for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)ord[i];
     c->counters.launches += a.cnt ? 1 : 2;
     if (talker) {
         TalkerArgs t{};
@@ -1500,6 +1508,7 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
                               mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
     a.n_parts = (mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
     a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)i;
     for (int i = 0; i < n; ++i) a.slots[i] = i;
     const size_t acc_elems = (size_t)n * hkv * a.n_split * R * D;
     const size_t bytes = (kTensorWsHead + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * R * 8;

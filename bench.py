@@ -107,7 +107,7 @@ def prefill(rt, hkv: int, d: int, n_layers: int, streams: int, ctx: int, gen: to
             k = torch.randn((1, hkv, ctx, d), generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16)
             v = torch.randn((1, hkv, ctx, d), generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16)
             rt.import_(s, layer, k, v)
-    torch.cuda.synchronize()
+    rt.synchronize()  # the steps run on another stream: nothing of rt's may be in flight here
 
 
 class Model:

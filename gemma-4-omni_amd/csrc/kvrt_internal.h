@@ -105,6 +105,30 @@ struct Lengths {
     int32_t offset;
 };
 
+// Prefix-attention mask of one slot (device, 128 B): key position k < len is
+// visible only if bit k of bits is set; bits at or past len are set. A
+// decode wave keeps word (lane & 15) in a register and finds the word of a
+// key with a lane shuffle.
+constexpr int kPrefixWords = KVRT_MAX_PREFIX_MASK / 32;
+struct PrefixMask {
+    int32_t len;
+    int32_t pad[15];
+    uint32_t bits[kPrefixWords];
+};
+static_assert(sizeof(PrefixMask) == 128, "prefix mask record");
+
+// Packs n masks (int64 / int32 / bool elements, [n, P] with element strides)
+// into PrefixMask records dst[index[i]].
+struct PrefixPackArgs {
+    const uint8_t *src;
+    int64_t item_stride;   // elements
+    int32_t elem_bytes;    // 8, 4 or 1
+    int32_t n_items;
+    int32_t plen;          // P
+    PrefixMask *dst;
+    int32_t index[kMaxItems];
+};
+
 struct AppendArgs {
     KVView kv;
     Lengths len;
@@ -169,6 +193,7 @@ struct DecodeArgs {
     int32_t advance;        // the merge kernel adds qn to each item's length
     int32_t n_parts;        // partials per (item, kv head) the merge kernel combines
     uint32_t *cnt;          // non-null: the decode merges its own partials (see kCntItems)
+    const PrefixMask *pmask;  // non-null: prefix-attention masks, indexed by slot
     uint8_t order[kMaxItems];  // PAGED: item of grid z-index i, the most visible keys first
     float scale_log2;       // softmax scale * log2(e)
     int32_t slots[kMaxItems];
@@ -222,6 +247,7 @@ struct PrefillArgs {
     int32_t n_ksplit;       // key ranges per query block; > 1: partials to part_o / part_ml
     float *part_o;          // [n, Hq, Q, n_ksplit, D] unnormalised outputs
     float2 *part_ml;        // [n, Hq, Q, n_ksplit] (running max in log2 units, sum)
+    const PrefixMask *pmask;  // non-null: prefix-attention masks, indexed by slot
     float scale_log2;
     int32_t slots[kMaxItems];
 };
@@ -299,6 +325,7 @@ hipError_t launch_slot_copy(const SlotMoveArgs &a, int64_t max_units, hipStream_
 // rotated by rope_delta positions where the layer has a RoPE table (bf16).
 hipError_t launch_slot_rebase(const SlotMoveArgs &a, int max_heads, hipStream_t s);
 hipError_t launch_zero(void *p, uint64_t bytes, hipStream_t s);
+hipError_t launch_prefix_pack(const PrefixPackArgs &a, hipStream_t s);
 
 // Smallest instantiated row tile >= rows (1, 2, 4, 8, 16); 0 if too large.
 int rows_tile(int rows);

@@ -45,6 +45,26 @@ __device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int hea
     }
 }
 
+// Prefix-attention mask of a slot as a wave holds it: its length plen (0: no
+// mask) and, in every lane, mask word (lane & 15). The record is read only
+// when the launch carries masks, so launches without them load nothing.
+__device__ __forceinline__ void load_prefix(const PrefixMask *pm, int slot, int lane, int &plen, uint32_t &pw) {
+    plen = 0;
+    pw = 0xffffffffu;
+    if (pm != nullptr) {
+        plen = pm[slot].len;
+        pw = pm[slot].bits[lane & (kPrefixWords - 1)];
+    }
+}
+// Mask bit of key position key (0 <= key < KVRT_MAX_PREFIX_MASK): the word
+// comes from the lane that holds it (ds_bpermute), so every lane of the wave
+// must call this together.
+__device__ __forceinline__ bool prefix_bit(uint32_t pw, int key) {
+    const uint32_t w = (uint32_t)__shfl((int)pw, (key >> 5) & (kPrefixWords - 1));
+    return ((w >> (key & 31)) & 1u) != 0;
+}
+
+
 // PAGED row offset with the page taken from a wave's window of page-table
 // entries (lane i holds the entry of logical page win0 + i; pages past the
 // window are looked up directly). Every lane of the wave must call it.
@@ -446,6 +466,9 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     chunk = (chunk + KPW - 1) / KPW * KPW;
     const int ws = kstart + split * chunk;
     const int we = min(kend, ws + chunk);
+    int plen = 0;          // prefix-attention mask (listener slots); the talker has its own masks
+    uint32_t pw = ~0u;
+    if constexpr (!TALK) load_prefix(a.pmask, slot, lane, plen, pw);
 
     if constexpr (KDT == KVRT_BF16) {
         // Fused append: workgroup 0 of every (item, kv head) stores the new
@@ -662,6 +685,15 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         // would otherwise sink the last ones under register pressure and
         // expose a second memory round trip per pass)
         __builtin_amdgcn_sched_barrier(0);
+        }
+        if (base < plen) {
+            // keys of this pass below the end of the prefix mask: a masked
+            // key becomes invisible to every row (wave-uniform branch)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool hidden = key[u] < plen && !prefix_bit(pw, key[u]);
+                key[u] = hidden ? 0x7fffffff : key[u];
+            }
         }
         // scores (log2 domain)
         float s[U][R];
@@ -920,6 +952,13 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     chunk = (chunk + T - 1) / T * T;
     const int ws = kstart + split * chunk;
     const int we = min(kend, ws + chunk);
+    // Prefix-attention mask of the slot. PAGED rows at D 512 use every
+    // register: launches with masks run that shape on decode_kernel instead
+    // (launch_decode_mfma refuses them), so this variant has no mask code.
+    constexpr bool PMASK = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
+    int plen = 0;
+    uint32_t pw = ~0u;
+    if constexpr (PMASK) load_prefix(a.pmask, slot, lane, plen, pw);
 
     // Fused append: workgroup 0 of every (item, kv head) stores the new rows;
     // no workgroup of this launch reads them from the cache.
@@ -1107,14 +1146,22 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         if constexpr (more) load_v(t0 + T, vt);
         // this lane: keys t0 + 4grp + v of row col
         float sc[4];
-        float tmax = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int key = t0 + 4 * grp + v;
             const bool vis = key < we && key <= hi && key >= lo;
             sc[v] = vis ? (I8 ? s[v] * ksv[v] : s[v]) * a.scale_log2 : -INFINITY;
-            tmax = fmaxf(tmax, sc[v]);
         }
+        if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int key = t0 + 4 * grp + v;
+                sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
         tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
         lazy_rescale<D / 16>(tmax, m, l, o);
         float p[4];
@@ -1379,6 +1426,9 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int head = kvh * g + (by % nhb) * hw + (computes ? wave : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    int plen;  // prefix-attention mask of the slot
+    uint32_t pw;
+    load_prefix(a.pmask, slot, lane, plen, pw);
     const int Qn = a.qn;
     const int qrow0 = qb * 16;
     const int base_pos = L - Qn;               // position of query row 0
@@ -1440,7 +1490,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // block's first query sees up to its own position, the last one's
         // window starts at or before t0): no per-key mask
         const bool all_visible = qrow0 + 16 <= Qn && t0 + kPfKeys - 1 <= base_pos + qrow0 &&
-                                 (a.window == 0 || t0 >= base_pos + qrow0 + 15 - a.window + 1);
+                                 (a.window == 0 || t0 >= base_pos + qrow0 + 15 - a.window + 1) && t0 >= plen;
         // S^T blocks: rows = keys pf_key(b, i), cols = queries
         f32x4_t s[2];
 #pragma unroll
@@ -1457,13 +1507,21 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                 s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd)), qop[c], s[b]);
         }
         // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile
+        uint32_t pvis = 0xffu;  // bit j: key 8grp + j passes the prefix mask
+        if (t0 < plen) {        // the tile reaches into the prefix mask (wave-uniform)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = t0 + 8 * grp + j;
+                if (key < plen && !prefix_bit(pw, key)) pvis &= ~(1u << j);
+            }
+        }
         float sc[8];
         float tmax = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int key = t0 + 8 * grp + j;
             const float raw = j < 4 ? s[0][j] : s[1][j - 4];
-            const bool vis = all_visible || (qvalid && key < kend && key <= pq && key >= lo_q);
+            const bool vis = all_visible || (qvalid && key < kend && key <= pq && key >= lo_q && ((pvis >> j) & 1u));
             sc[j] = vis ? raw * a.scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, sc[j]);
         }
@@ -1761,6 +1819,28 @@ __global__ __launch_bounds__(1024) void slot_rebase_kernel(SlotMoveArgs a) {
     }
 }
 
+// grid n_items, 512 threads (8 waves): thread t reads element t of its
+// item's mask (t < P; later positions count as visible), and each wave's
+// ballot gives mask words 2w and 2w + 1 of the record.
+__global__ __launch_bounds__(512) void prefix_pack_kernel(PrefixPackArgs a) {
+    const int item = blockIdx.x, t = threadIdx.x;
+    bool vis = true;
+    if (t < a.plen) {
+        const uint8_t *p = a.src + ((int64_t)item * a.item_stride + t) * a.elem_bytes;
+        if (a.elem_bytes == 8) vis = *reinterpret_cast<const int64_t *>(p) != 0;
+        else if (a.elem_bytes == 4) vis = *reinterpret_cast<const int32_t *>(p) != 0;
+        else vis = *p != 0;
+    }
+    const uint64_t b = __ballot(vis);
+    PrefixMask *m = a.dst + a.index[item];
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) {
+        m->bits[2 * wave] = (uint32_t)b;
+        m->bits[2 * wave + 1] = (uint32_t)(b >> 32);
+    }
+    if (t == 0) m->len = a.plen;
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, uint64_t n16) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
          i += (uint64_t)gridDim.x * blockDim.x)
@@ -1873,6 +1953,7 @@ static hipError_t launch_decode_rt(const DecodeArgs &a, int dtype, hipStream_t s
 // int8 rows (PAGED, up to kMaxInt8Rows rows) are converted to bf16 operands.
 hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int dtype, int rows_per_head, hipStream_t s) {
     if (a.n_split % kWaves != 0 || a.n_split <= 0 || a.n_parts != a.n_split / kWaves) return hipErrorInvalidValue;
+    if (a.pmask && a.kv.layout == KVRT_LAYOUT_PAGED && head_dim >= 512) return hipErrorInvalidValue;  // no mask code
     if (dtype == KVRT_INT8 && (a.kv.layout != KVRT_LAYOUT_PAGED || rows_tile(rows_per_head) > kMaxInt8Rows))
         return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
@@ -2001,6 +2082,14 @@ hipError_t launch_slot_rebase(const SlotMoveArgs &a, int max_heads, hipStream_t 
     if (a.n_entries <= 0) return hipSuccess;
     if (a.n_entries > kMaxMoveLayers || max_heads <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(slot_rebase_kernel, dim3(a.n_entries, max_heads), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefix_pack(const PrefixPackArgs &a, hipStream_t s) {
+    static_assert(kPrefixWords * 32 == 512, "one 512-thread workgroup per mask");
+    if (a.n_items <= 0) return hipSuccess;
+    if (a.n_items > kMaxItems || a.plen < 0 || a.plen > KVRT_MAX_PREFIX_MASK) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prefix_pack_kernel, dim3(a.n_items), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

@@ -11,9 +11,11 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <new>
 #include <random>
+#include <utility>
 #include <vector>
 
 #include "kvrt_internal.h"
@@ -43,9 +45,17 @@ int elem_size(int dtype) {
         case KVRT_FP32: return 4;
         case KVRT_BOOL: return 1;
         case KVRT_INT32: return 4;
+        case KVRT_INT64: return 8;
         default: return 0;
     }
 }
+
+// Host record of one slot: its generation (renewed when its contents are
+// replaced) and the length of its prefix-attention mask.
+struct SlotState {
+    uint64_t generation = 0;
+    int32_t prefix_len = 0;
+};
 
 int env_int(const char *name, int dflt) {
     const char *s = std::getenv(name);
@@ -60,9 +70,13 @@ struct kvrt_ctx {
     kvrt_config cfg{};
     std::vector<Layer> layers;
     hipStream_t stream = nullptr;
+    bool dirty = false;             // work enqueued since the bound stream was last synchronised
     int device = 0;
     bool poisoned = false;
     bool inject = false;
+    std::vector<SlotState> slot;    // per slot
+    uint64_t next_generation = 1;
+    PrefixMask *d_prefix = nullptr; // device [n_slots] prefix-attention masks
     std::vector<int32_t> len;       // host shadow [slot * n_layers + layer]
     int32_t *d_len = nullptr;
     int32_t *d_err = nullptr;
@@ -95,7 +109,8 @@ int device_ok(kvrt_ctx *c, hipError_t e) {
     return KVRT_OK;
 }
 
-// Preamble of every mutating call.
+// Preamble of every mutating call. The context counts as having work in
+// flight on its bound stream from here until a synchronising call.
 int begin(kvrt_ctx *c) {
     if (!c) return KVRT_EINVAL;
     if (c->poisoned) return KVRT_EPOISONED;
@@ -103,6 +118,7 @@ int begin(kvrt_ctx *c) {
         c->inject = false;
         return poison(c);
     }
+    c->dirty = true;
     // Switch devices only when needed: hipSetDevice is refused inside a
     // stream capture, and calls of one context are captured into graphs.
     int cur = -1;
@@ -403,6 +419,60 @@ int set_device_lens(kvrt_ctx *c, const std::vector<int32_t> &idx) {
     return KVRT_OK;
 }
 
+// The slot's contents were replaced: callers holding its old generation are stale.
+void renew_generation(kvrt_ctx *c, int slot) { c->slot[slot].generation = c->next_generation++; }
+
+bool generation_ok(const kvrt_ctx *c, int slot, uint64_t expected) {
+    return expected == KVRT_ANY_GENERATION || c->slot[slot].generation == expected;
+}
+
+// Set the length word of a slot's device mask record (0 disables the mask).
+int set_prefix_len_device(kvrt_ctx *c, int slot, int len) {
+    SetLenArgs a{};
+    a.lens = reinterpret_cast<int32_t *>(c->d_prefix);
+    a.n = 1;
+    a.idx[0] = slot * (int)(sizeof(PrefixMask) / sizeof(int32_t));
+    a.val[0] = len;
+    c->counters.launches++;
+    if (launch_set_lens(a, c->stream) != hipSuccess) return poison(c);
+    c->slot[slot].prefix_len = len;
+    return KVRT_OK;
+}
+
+// Device masks for a launch over these slots: the context's records when one
+// of them has a mask, else null (the kernels then read no mask at all).
+const PrefixMask *launch_masks(const kvrt_ctx *c, int n, const int32_t *slots) {
+    for (int i = 0; i < n; ++i)
+        if (c->slot[slots[i]].prefix_len > 0) return c->d_prefix;
+    return nullptr;
+}
+
+// Validate a prefix-attention mask tensor of `items` rows ([items, P], or
+// [P] / [1, P] for one row) and fill the pack arguments (except dst/index).
+int prefix_tensor(const kvrt_tensor *m, int items, PrefixPackArgs &a) {
+    if (!m || !m->data) return KVRT_EINVAL;
+    const int es = elem_size(m->dtype);
+    if (m->dtype != KVRT_INT64 && m->dtype != KVRT_INT32 && m->dtype != KVRT_BOOL) return KVRT_EINVAL;
+    int64_t rows, plen, item_stride;
+    if (m->ndim == 1 && items == 1) {
+        rows = 1, plen = m->dims[0], item_stride = 0;
+        if (plen > 1 && m->strides[0] != 1) return KVRT_EINVAL;
+    } else if (m->ndim == 2) {
+        rows = m->dims[0], plen = m->dims[1], item_stride = m->strides[0];
+        if (plen > 1 && m->strides[1] != 1) return KVRT_EINVAL;
+    } else {
+        return KVRT_EINVAL;
+    }
+    if (rows != items || plen < 0 || plen > KVRT_MAX_PREFIX_MASK || item_stride < 0) return KVRT_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(m->data) % (uintptr_t)es) != 0) return KVRT_EINVAL;
+    a.src = static_cast<const uint8_t *>(m->data);
+    a.item_stride = item_stride;
+    a.elem_bytes = es;
+    a.n_items = items;
+    a.plen = (int)plen;
+    return KVRT_OK;
+}
+
 int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt_storage *storage,
                 kvrt_ctx **out) {
     if (!cfg || !specs || !out) return KVRT_EINVAL;
@@ -492,6 +562,11 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     if (launch_zero(c->d_err, 16, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
     if (hipMalloc((void **)&c->d_cnt, kCntWords * 4) != hipSuccess) return fail(KVRT_EDEVICE);
     if (launch_zero(c->d_cnt, kCntWords * 4, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
+    const size_t prefix_bytes = (size_t)cfg->n_slots * sizeof(PrefixMask);
+    if (hipMalloc((void **)&c->d_prefix, prefix_bytes) != hipSuccess) return fail(KVRT_EDEVICE);
+    if (launch_zero(c->d_prefix, prefix_bytes, nullptr) != hipSuccess) return fail(KVRT_EDEVICE);
+    c->slot.assign(cfg->n_slots, SlotState{});
+    for (int i = 0; i < cfg->n_slots; ++i) renew_generation(c, i);
     if (any_paged) {
         c->pt_stride = (cfg->capacity + cfg->block_size - 1) / cfg->block_size;
         c->pt.assign((size_t)cfg->n_slots * c->pt_stride, -1);
@@ -596,15 +671,20 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         from[i] = L;
         if (Lnew < qn) return KVRT_ESTATE;
         if (fused && Lnew > c->cfg.capacity) return KVRT_ESTATE;
-        if (s.layout == KVRT_LAYOUT_PAGED && Lnew - (int)qn - s.window + 1 < c->first_live[slots[i]] * c->cfg.block_size &&
-            (s.window == 0 || c->first_live[slots[i]] > 0))
-            return KVRT_ESTATE;  // the window would read evicted pages
+        if (s.layout == KVRT_LAYOUT_PAGED) {
+            // the oldest key any query of the call sees must be on a live page
+            const int oldest = s.window > 0 ? std::max(0, Lnew - (int)qn - s.window + 1) : 0;
+            if (oldest < c->first_live[slots[i]] * c->cfg.block_size) return KVRT_ESTATE;
+        }
         item_keys[i] = talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn);
         max_keys = std::max<int64_t>(max_keys, item_keys[i]);
     }
     const int R = rows_tile(rows);
     const int64_t bucket_keys = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
-    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys);
+    const PrefixMask *pmask = talker ? nullptr : launch_masks(c, n, slots);
+    // the MFMA kernel's PAGED D 512 variant has no registers for a mask
+    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys) &&
+                      !(pmask && s.layout == KVRT_LAYOUT_PAGED && D >= 512);
     const int n_split = choose_splits(target_wgs(c->cfg, mfma ? KVRT_BF16 : s.dtype), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
     const int Rw = mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial (MFMA tiles are 8 or 16)
@@ -636,6 +716,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     a.advance = fused ? 1 : 0;
     a.n_parts = (mfma || decode_wg_merge(D, R)) ? n_split / kWaves : n_split;
     a.cnt = single_launch_decode(c->cfg.decode_merge, mfma, D, R, rows, a.n_parts) ? c->d_cnt : nullptr;
+    a.pmask = pmask;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     // grid z order: most visible keys first (stable), so that a ragged batch's
@@ -754,16 +835,24 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     return KVRT_OK;
 }
 
-// Floats before the partials in the context-free workspace (error flag).
+// Workspace of the context-free tensor attention, one per (device, stream):
+// calls on one stream share it in stream order, calls on different streams
+// never do. Layout: the error flag (kTensorWsHead floats), the prefix masks
+// of the call's items (kMaxItems records), then the split-K partials.
 constexpr size_t kTensorWsHead = 64;
+constexpr size_t kTensorWsMasks = kMaxItems * sizeof(PrefixMask) / sizeof(float);
 
 struct TensorWorkspace {
-    std::mutex mu;
     float *ptr = nullptr;
     size_t bytes = 0;
-    int device = -1;
 };
-TensorWorkspace g_tensor_ws;
+// One lock for the map and for each call's launches: a decode and its merge
+// kernel are enqueued together, so two host threads on one stream cannot
+// interleave their partials.
+std::mutex g_tensor_mu;
+std::map<std::pair<int, hipStream_t>, TensorWorkspace> g_tensor_ws;
+// Outgrown workspaces: never freed, since a captured graph may still use them.
+std::vector<float *> g_tensor_retired;
 
 }  // namespace
 
@@ -775,7 +864,7 @@ uint32_t kvrt_abi_version(void) { return KVRT_ABI_VERSION; }
 uint64_t kvrt_capabilities(void) {
     return KVRT_CAP_CONTIG | KVRT_CAP_RING | KVRT_CAP_PAGED | KVRT_CAP_INT8 | KVRT_CAP_FUSED_APPEND_ATTEND |
            KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND | KVRT_CAP_PREFILL_MFMA |
-           KVRT_CAP_TALKER_MASK;
+           KVRT_CAP_TALKER_MASK | KVRT_CAP_PREFIX_ATTENTION | KVRT_CAP_SLOT_GENERATION | KVRT_CAP_STREAM_CONFINED;
 }
 
 const char *kvrt_strerror(int code) {
@@ -833,6 +922,7 @@ int kvrt_destroy(kvrt_ctx *c) {
     if (c->d_len) (void)hipFree(c->d_len);
     if (c->d_err) (void)hipFree(c->d_err);
     if (c->d_cnt) (void)hipFree(c->d_cnt);
+    if (c->d_prefix) (void)hipFree(c->d_prefix);
     if (c->d_pt) (void)hipFree(c->d_pt);
     if (c->ws) (void)hipFree(c->ws);
     for (float *w : c->retired_ws) (void)hipFree(w);
@@ -843,7 +933,13 @@ int kvrt_destroy(kvrt_ctx *c) {
 int kvrt_bind_stream(kvrt_ctx *c, void *stream) {
     if (!c) return KVRT_EINVAL;
     if (c->poisoned) return KVRT_EPOISONED;
-    c->stream = static_cast<hipStream_t>(stream);
+    // A new context is bound to the null stream with nothing in flight.
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (c->stream == s) return KVRT_OK;
+    // a switch while the bound stream may still run this context's work
+    // would let two streams share its workspace and arrival counters
+    if (c->dirty) return KVRT_ESTATE;
+    c->stream = s;
     return KVRT_OK;
 }
 
@@ -1005,7 +1101,51 @@ int kvrt_reset_slot_async(kvrt_ctx *c, int32_t slot) {
         }
         c->first_live[slot] = 0;
     }
-    return set_device_lens(c, idx);
+    rc = set_device_lens(c, idx);
+    if (rc != KVRT_OK) return rc;
+    rc = set_prefix_len_device(c, slot, 0);
+    if (rc != KVRT_OK) return rc;
+    renew_generation(c, slot);
+    return KVRT_OK;
+}
+
+int kvrt_set_prefix_attention_async(kvrt_ctx *c, int32_t slot, const kvrt_tensor *mask) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_slot(c, slot)) return KVRT_EINVAL;
+    PrefixPackArgs a{};
+    if (mask != nullptr) {
+        rc = prefix_tensor(mask, 1, a);
+        if (rc != KVRT_OK) return rc;
+    }
+    if (a.plen == 0) return set_prefix_len_device(c, slot, 0);
+    // the masked positions must be in the slot already (the mask comes with
+    // an imported prefix), so that the rewind floor holds from the start
+    for (int l = 0; l < c->cfg.n_layers; ++l)
+        if (c->layers[l].owner == l && c->len_at(slot, l) < a.plen) return KVRT_ESTATE;
+    a.dst = c->d_prefix;
+    a.index[0] = slot;
+    c->counters.launches++;
+    if (launch_prefix_pack(a, c->stream) != hipSuccess) return poison(c);
+    c->slot[slot].prefix_len = a.plen;
+    return KVRT_OK;
+}
+
+int kvrt_slot_info_get(kvrt_ctx *c, int32_t slot, kvrt_slot_info *out) {
+    if (!c || !out || !valid_slot(c, slot)) return KVRT_EINVAL;
+    kvrt_slot_info r{};
+    r.generation = c->slot[slot].generation;
+    r.prefix_len = c->slot[slot].prefix_len;
+    r.min_len = INT32_MAX;
+    r.max_len = 0;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (c->layers[l].owner != l) continue;
+        r.min_len = std::min(r.min_len, c->len_at(slot, l));
+        r.max_len = std::max(r.max_len, c->len_at(slot, l));
+    }
+    if (r.min_len == INT32_MAX) r.min_len = 0;
+    *out = r;
+    return KVRT_OK;
 }
 
 int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,
@@ -1066,10 +1206,12 @@ int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slot
     return KVRT_OK;
 }
 
-int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len) {
+int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation) {
     int rc = begin(c);
     if (rc) return rc;
     if (!valid_slot(c, slot) || layer < -1 || layer >= c->cfg.n_layers || new_len < 0) return KVRT_EINVAL;
+    // identity and the rewind floor: the prefix-attention mask's positions stay
+    if (!generation_ok(c, slot, expected_generation) || new_len < c->slot[slot].prefix_len) return KVRT_ESTATE;
     std::vector<int> targets;
     for (int l = 0; l < c->cfg.n_layers; ++l) {
         if (layer >= 0 && l != layer) continue;
@@ -1165,7 +1307,10 @@ bool same_topology(const kvrt_ctx *a, const kvrt_ctx *b) {
 
 // Copy the first n tokens of every owned layer of (src, src_slot) into
 // (dst, dst_slot), on dst's stream; dst lengths become n.
-int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int n) {
+int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int n, uint64_t src_generation) {
+    if (!generation_ok(src, src_slot, src_generation)) return KVRT_ESTATE;
+    const int src_plen = src->slot[src_slot].prefix_len;
+    if (n < src_plen) return KVRT_ESTATE;  // the copy would end inside the masked prefix
     const int nl = src->cfg.n_layers;
     std::vector<int> lo(nl, 0);
     int page_lo = n;
@@ -1238,27 +1383,41 @@ int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int
     }
     if ((rc = flush()) != KVRT_OK) return rc;
     dst->counters.gathered_bytes += bytes;
-    return set_device_lens(dst, idx);
+    rc = set_device_lens(dst, idx);
+    if (rc != KVRT_OK) return rc;
+    // the prefix-attention mask travels with the rows (a 128-byte record)
+    CopyRowsArgs m{};
+    m.src = reinterpret_cast<const uint8_t *>(src->d_prefix + src_slot);
+    m.dst = reinterpret_cast<uint8_t *>(dst->d_prefix + dst_slot);
+    m.d0 = m.d1 = m.rows = 1;
+    m.row_bytes = sizeof(PrefixMask);
+    dst->counters.launches++;
+    if (launch_copy_rows(m, dst->stream) != hipSuccess) return poison(dst);
+    dst->slot[dst_slot].prefix_len = src_plen;
+    renew_generation(dst, dst_slot);
+    return KVRT_OK;
 }
 
 }  // namespace
 
-int kvrt_copy_prefix_async(kvrt_ctx *c, int32_t src_slot, int32_t dst_slot, int32_t n_tokens) {
+int kvrt_copy_prefix_async(kvrt_ctx *c, int32_t src_slot, int32_t dst_slot, int32_t n_tokens,
+                           uint64_t src_generation) {
     int rc = begin(c);
     if (rc) return rc;
     if (!valid_slot(c, src_slot) || !valid_slot(c, dst_slot) || src_slot == dst_slot || n_tokens < 0)
         return KVRT_EINVAL;
-    return copy_slot_impl(c, dst_slot, c, src_slot, n_tokens);
+    return copy_slot_impl(c, dst_slot, c, src_slot, n_tokens, src_generation);
 }
 
-int kvrt_copy_session_async(kvrt_ctx *dst, int32_t dst_slot, kvrt_ctx *src, int32_t src_slot, int32_t n_tokens) {
+int kvrt_copy_session_async(kvrt_ctx *dst, int32_t dst_slot, kvrt_ctx *src, int32_t src_slot, int32_t n_tokens,
+                            uint64_t src_generation) {
     if (!dst || !src || dst == src) return KVRT_EINVAL;
     if (src->poisoned) return KVRT_EPOISONED;
     int rc = begin(dst);
     if (rc) return rc;
     if (!valid_slot(dst, dst_slot) || !valid_slot(src, src_slot) || n_tokens < 0) return KVRT_EINVAL;
     if (!same_topology(dst, src)) return KVRT_EINVAL;
-    return copy_slot_impl(dst, dst_slot, src, src_slot, n_tokens);
+    return copy_slot_impl(dst, dst_slot, src, src_slot, n_tokens, src_generation);
 }
 
 int kvrt_set_layer_rope(kvrt_ctx *c, int32_t layer, const float *inv_freq, int32_t n_freq, float scaling) {
@@ -1276,6 +1435,7 @@ int kvrt_set_layer_rope(kvrt_ctx *c, int32_t layer, const float *inv_freq, int32
     }
     // pending work may read the current table
     if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    c->dirty = false;
     if (inv_freq == nullptr) {
         if (L.inv_freq) (void)hipFree(L.inv_freq);
         L.inv_freq = nullptr;
@@ -1289,11 +1449,13 @@ int kvrt_set_layer_rope(kvrt_ctx *c, int32_t layer, const float *inv_freq, int32
     return upload_desc(c) == KVRT_OK ? KVRT_OK : poison(c);
 }
 
-int kvrt_rollover_async(kvrt_ctx *c, int32_t slot, int32_t prefix_len, int32_t retained_rows) {
+int kvrt_rollover_async(kvrt_ctx *c, int32_t slot, int32_t prefix_len, int32_t retained_rows,
+                        uint64_t expected_generation) {
     int rc = begin(c);
     if (rc) return rc;
     if (!valid_slot(c, slot) || prefix_len <= 0 || retained_rows <= 0 || retained_rows > KVRT_MAX_ROLLOVER_ROWS)
         return KVRT_EINVAL;
+    if (!generation_ok(c, slot, expected_generation) || prefix_len < c->slot[slot].prefix_len) return KVRT_ESTATE;
     int L = -1, max_heads = 0;
     for (int l = 0; l < c->cfg.n_layers; ++l) {
         if (c->layers[l].owner != l) continue;
@@ -1453,6 +1615,7 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
         }
         if (c->poisoned) return KVRT_EDEVICE;
     }
+    a.pmask = launch_masks(c, n, slots);
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches += a.n_ksplit > 1 ? 2 : 1;
@@ -1463,8 +1626,8 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
 }
 
 int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
-                              const int32_t *device_lengths, const kvrt_tensor *out, float scale, int32_t window,
-                              void *stream) {
+                              const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
+                              const kvrt_tensor *out, float scale, int32_t window, void *stream) {
     if (!device_lengths || window < 0 || !std::isfinite(scale)) return KVRT_EINVAL;
     if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
         return KVRT_EINVAL;
@@ -1482,6 +1645,11 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     const int group = (int)(hq / hkv);
     const int rows = group * (int)qn;
     if (rows_tile(rows) == 0) return KVRT_EINVAL;
+    PrefixPackArgs pk{};
+    if (prefix_attention != nullptr) {
+        const int rc = prefix_tensor(prefix_attention, (int)n, pk);
+        if (rc != KVRT_OK) return rc;
+    }
     DecodeArgs a{};
     a.kv.k = k->data;
     a.kv.v = v->data;
@@ -1510,33 +1678,57 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)i;
     for (int i = 0; i < n; ++i) a.slots[i] = i;
-    const size_t acc_elems = (size_t)n * hkv * a.n_split * R * D;
-    const size_t bytes = (kTensorWsHead + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * R * 8;
-    std::lock_guard<std::mutex> lock(g_tensor_ws.mu);
+    const int Rw = mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial
+    const size_t acc_elems = (size_t)n * hkv * a.n_split * Rw * D;
+    const size_t bytes = (kTensorWsHead + kTensorWsMasks + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * Rw * 8;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(g_tensor_mu);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
-    if (g_tensor_ws.ptr && (g_tensor_ws.bytes < bytes || g_tensor_ws.device != dev)) {
-        if (hipDeviceSynchronize() != hipSuccess) return KVRT_EDEVICE;
-        (void)hipFree(g_tensor_ws.ptr);
-        g_tensor_ws.ptr = nullptr;
-        g_tensor_ws.bytes = 0;
-    }
-    if (!g_tensor_ws.ptr) {
+    TensorWorkspace &ws = g_tensor_ws[{dev, st}];
+    if (ws.bytes < bytes) {
+        // no allocation inside a stream capture: an eager call of the largest
+        // shape sizes the workspace first
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) return KVRT_EDEVICE;
+        if (cs != hipStreamCaptureStatusNone) return KVRT_ESTATE;
+        float *fresh = nullptr;
         const size_t want = std::max(bytes, (size_t)1 << 20);
-        if (hipMalloc(&g_tensor_ws.ptr, want) != hipSuccess) return KVRT_EDEVICE;
-        if (launch_zero(g_tensor_ws.ptr, kTensorWsHead * 4, static_cast<hipStream_t>(stream)) != hipSuccess)
-            return KVRT_EDEVICE;
-        g_tensor_ws.bytes = want;
-        g_tensor_ws.device = dev;
+        if (hipMalloc(&fresh, want) != hipSuccess) return KVRT_EDEVICE;
+        if (launch_zero(fresh, kTensorWsHead * 4, st) != hipSuccess) return KVRT_EDEVICE;
+        if (ws.ptr) g_tensor_retired.push_back(ws.ptr);
+        ws.ptr = fresh;
+        ws.bytes = want;
     }
-    // Head of the workspace: the error flag of this path.
-    a.err = reinterpret_cast<int32_t *>(g_tensor_ws.ptr);
-    a.part_acc = g_tensor_ws.ptr + kTensorWsHead;
-    a.part_ml = reinterpret_cast<float2 *>(g_tensor_ws.ptr + kTensorWsHead + ((acc_elems + 63) / 64) * 64);
-    if ((mfma ? launch_decode_mfma(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream))
-              : launch_decode(a, (int)D, KVRT_BF16, rows, static_cast<hipStream_t>(stream))) != hipSuccess)
+    a.err = reinterpret_cast<int32_t *>(ws.ptr);
+    a.part_acc = ws.ptr + kTensorWsHead + kTensorWsMasks;
+    a.part_ml = reinterpret_cast<float2 *>(a.part_acc + ((acc_elems + 63) / 64) * 64);
+    if (prefix_attention != nullptr && pk.plen > 0) {
+        pk.dst = reinterpret_cast<PrefixMask *>(ws.ptr + kTensorWsHead);
+        for (int i = 0; i < n; ++i) pk.index[i] = i;
+        if (launch_prefix_pack(pk, st) != hipSuccess) return KVRT_EDEVICE;
+        a.pmask = pk.dst;
+    }
+    if ((mfma ? launch_decode_mfma(a, (int)D, KVRT_BF16, rows, st) : launch_decode(a, (int)D, KVRT_BF16, rows, st)) !=
+        hipSuccess)
         return KVRT_EDEVICE;
     return KVRT_OK;
+}
+
+int kvrt_tensors_status(void *stream) {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(g_tensor_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
+    auto it = g_tensor_ws.find({dev, st});
+    if (it == g_tensor_ws.end() || !it->second.ptr) return KVRT_OK;
+    if (hipStreamSynchronize(st) != hipSuccess) return KVRT_EDEVICE;
+    int32_t err = 0;
+    if (hipMemcpy(&err, it->second.ptr, sizeof(err), hipMemcpyDeviceToHost) != hipSuccess) return KVRT_EDEVICE;
+    if (err == 0) return KVRT_OK;
+    if (launch_zero(it->second.ptr, kTensorWsHead * 4, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return KVRT_EDEVICE;
+    return KVRT_EFAULT;
 }
 
 int kvrt_copy_rows_async(const kvrt_tensor *src, const kvrt_tensor *dst, int64_t rows, void *stream) {
@@ -1580,6 +1772,7 @@ int kvrt_sync_lengths(kvrt_ctx *c) {
     if (c->poisoned) return KVRT_EPOISONED;
     if (hipSetDevice(c->device) != hipSuccess) return poison(c);
     if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    c->dirty = false;
     std::vector<int32_t> dev(c->len.size());
     if (hipMemcpy(dev.data(), c->d_len, dev.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return poison(c);
     for (size_t i = 0; i < dev.size(); ++i) {
@@ -1600,6 +1793,7 @@ int kvrt_health(kvrt_ctx *c) {
     if (c->poisoned) return KVRT_EPOISONED;
     if (hipSetDevice(c->device) != hipSuccess) return poison(c);
     if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    c->dirty = false;
     int32_t err = 0;
     if (hipMemcpy(&err, c->d_err, sizeof(err), hipMemcpyDeviceToHost) != hipSuccess) return poison(c);
     if (err != 0) return KVRT_EFAULT;

@@ -10,9 +10,12 @@ from ctypes import POINTER, c_float, c_int32, c_int64, c_uint32, c_uint64, c_voi
 
 from ._build import LIB_PATH
 
+KVRT_ABI_VERSION = 2
 KVRT_MAX_RANK = 4
 KVRT_MAX_ROLLOVER_ROWS = 128
 KVRT_MAX_ITEMS = 64
+KVRT_MAX_PREFIX_MASK = 512
+KVRT_ANY_GENERATION = 0
 
 KVRT_OK = 0
 KVRT_EINVAL = -1
@@ -31,6 +34,7 @@ DT_INT8 = 1
 DT_FP32 = 2
 DT_BOOL = 3
 DT_INT32 = 4
+DT_INT64 = 5
 
 CAP_CONTIG = 1 << 0
 CAP_RING = 1 << 1
@@ -42,6 +46,9 @@ CAP_DEVICE_LENGTHS = 1 << 6
 CAP_TENSOR_ATTEND = 1 << 7
 CAP_PREFILL_MFMA = 1 << 8
 CAP_TALKER_MASK = 1 << 9
+CAP_PREFIX_ATTENTION = 1 << 10
+CAP_SLOT_GENERATION = 1 << 11
+CAP_STREAM_CONFINED = 1 << 12
 
 
 class KvrtTensor(ctypes.Structure):
@@ -110,6 +117,16 @@ class KvrtCounters(ctypes.Structure):
     ]
 
 
+class KvrtSlotInfo(ctypes.Structure):
+    _fields_ = [
+        ("generation", c_uint64),
+        ("prefix_len", c_int32),
+        ("min_len", c_int32),
+        ("max_len", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
 class KvrtTalkerMask(ctypes.Structure):
     _fields_ = [
         ("prefix_start", c_int32),
@@ -141,19 +158,22 @@ SIGNATURES = [
     ("kvrt_append_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T]),
     ("kvrt_write_positions_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T]),
     ("kvrt_reset_slot_async", c_int32, [c_void_p, c_int32]),
+    ("kvrt_set_prefix_attention_async", c_int32, [c_void_p, c_int32, _T]),
+    ("kvrt_slot_info_get", c_int32, [c_void_p, c_int32, POINTER(KvrtSlotInfo)]),
     ("kvrt_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T, _T]),
-    ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
+    ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),
-    ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
-    ("kvrt_copy_session_async", c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32]),
+    ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
+    ("kvrt_copy_session_async", c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_uint64]),
     ("kvrt_set_layer_rope", c_int32, [c_void_p, c_int32, POINTER(c_float), c_int32, c_float]),
-    ("kvrt_rollover_async", c_int32, [c_void_p, c_int32, c_int32, c_int32]),
+    ("kvrt_rollover_async", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
     ("kvrt_attend_decode_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_append_attend_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _T, _T, c_float]),
     ("kvrt_attend_prefill_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float]),
     ("kvrt_attend_talker_async", c_int32,
      [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float, POINTER(KvrtTalkerMask)]),
-    ("kvrt_attend_tensors_async", c_int32, [_T, _T, _T, c_void_p, _T, c_float, c_int32, c_void_p]),
+    ("kvrt_attend_tensors_async", c_int32, [_T, _T, _T, c_void_p, _T, _T, c_float, c_int32, c_void_p]),
+    ("kvrt_tensors_status", c_int32, [c_void_p]),
     ("kvrt_copy_rows_async", c_int32, [_T, _T, c_int64, c_void_p]),
     ("kvrt_session_state", c_int32, [c_void_p, c_int32, c_int32, _I32P]),
     ("kvrt_sync_lengths", c_int32, [c_void_p]),
@@ -180,6 +200,9 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.kvrt_abi_version() != KVRT_ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI {lib.kvrt_abi_version()}, this binding needs {KVRT_ABI_VERSION}; "
+                           "rebuild it")
     _lib = lib
     return lib
 

@@ -110,7 +110,11 @@ class KVRTCache:
         Returns the K/V states an HF attention call would see after the update:
         every stored position (global layers) or the last ``W - 1`` stored
         positions plus the new rows (sliding layers, as HF
-        ``DynamicSlidingWindowLayer.update`` returns them).
+        ``DynamicSlidingWindowLayer.update`` returns them); after a positional
+        write, the slot's whole [1, kv_heads, capacity, D] storage, as
+        ``_SlotKVCache.update`` returns its fixed-size tensors
+        (future_prefix.py:544-565), which is what the [.., capacity] masks of
+        ``get_mask_sizes`` are built for.
         """
         layer_idx = int(layer_idx)
         if key_states.dim() != 4 or key_states.shape[0] != 1:
@@ -145,6 +149,8 @@ class KVRTCache:
                 # _SlotKVCache raises OverflowError here (future_prefix.py:544-549)
                 raise OverflowError(f"slot KV position outside [0, {self.runtime.capacity})")
             self.runtime.write_positions(layer_idx, key_states, value_states, [self.slot], [pos])
+            k_all, v_all, _, _ = rt.storage(layer_idx)  # CONTIG bf16: zero-copy views
+            return k_all[self.slot:self.slot + 1], v_all[self.slot:self.slot + 1]
         if returned is not None and spec.dtype != "int8":
             return returned
         return rt.layer_view(self.slot, layer_idx)
@@ -274,13 +280,16 @@ def append_attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, caches: KVR
 
 
 def attend_padded(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lengths: torch.Tensor, scale: float,
-                  window: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+                  window: int = 0, out: torch.Tensor | None = None,
+                  prefix_attention: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention over a padded batch (the output of :func:`gather`).
 
     ``lengths`` int32 [N] on the device (e.g. ``mask.sum(1)``); query row i of
-    stream b sits at position ``lengths[b] - Q + i``.
+    stream b sits at position ``lengths[b] - Q + i``; ``prefix_attention``
+    [N, P] hides key j < P of stream b where it is 0 (the listener's
+    per-session prefix mask, gemma4_listener_kernels.cuh:517-518).
     """
-    return attend_tensors(q, k, v, lengths, scale, window=window, out=out)
+    return attend_tensors(q, k, v, lengths, scale, window=window, out=out, prefix_attention=prefix_attention)
 
 
 __all__ = ["KVRTCache", "KVRTCacheLayer", "append_attend", "attend", "attend_padded", "gather"]

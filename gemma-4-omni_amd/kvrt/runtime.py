@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 from dataclasses import dataclass
 from typing import Iterable, Sequence
 
@@ -26,6 +27,7 @@ _DTYPE_CODES = {
     torch.float32: L.DT_FP32,
     torch.bool: L.DT_BOOL,
     torch.int32: L.DT_INT32,
+    torch.int64: L.DT_INT64,
 }
 _LAYOUTS = {"contig": L.LAYOUT_CONTIG, "ring": L.LAYOUT_RING, "paged": L.LAYOUT_PAGED}
 
@@ -155,7 +157,16 @@ class KVRuntime:
     (and, forced to "mfma", of int8 ones); ``decode_merge`` ("auto",
     "separate", "last_wg") picks whether a decode's last workgroup per (slot,
     kv head) merges the split-K partials inside the launch or a second kernel
-    does. One stream per context: overlapping calls race on its workspace.
+    does.
+
+    Confinement, as the reference binding's (native_listener_microbatch.py:
+    1128-1131, gemma4_listener_microbatch_impl.inc:445-473): every call must
+    come from the thread that created the runtime, and the context stays on
+    the torch stream of its first call. Moving it to another stream raises
+    ``KVRTError`` (code -2) while its work may still run there;
+    :meth:`synchronize` (or :meth:`health` / :meth:`sync_lengths`) first
+    makes the switch legal. Slots carry generations (:meth:`slot_generation`)
+    that the lifecycle calls can check.
     """
 
     def __init__(
@@ -174,6 +185,7 @@ class KVRuntime:
         device: torch.device | str | None = None,
     ) -> None:
         self.lib = L.load()
+        self._owner_thread = threading.get_ident()
         self.device = torch.device(device if device is not None else "cuda")
         if self.device.type != "cuda" or not torch.cuda.is_available():
             raise RuntimeError("KVRuntime needs a ROCm GPU (torch.cuda); there is no CPU path")
@@ -254,9 +266,18 @@ class KVRuntime:
         src = self.layers[layer].shared_src
         return src if src >= 0 else layer
 
+    def _own(self) -> None:
+        if threading.get_ident() != self._owner_thread:
+            raise RuntimeError("kvrt runtime is confined to the host thread that created it")
+
     def _bind(self) -> None:
-        _check(self.lib.kvrt_bind_stream(self._ctx, ctypes.c_void_p(current_stream_handle(self.device))),
-               "kvrt_bind_stream")
+        """Bind the current torch stream (refused while work is in flight on another)."""
+        self._own()
+        rc = self.lib.kvrt_bind_stream(self._ctx, ctypes.c_void_p(current_stream_handle(self.device)))
+        if rc == L.KVRT_ESTATE:
+            raise KVRTError(rc, "kvrt_bind_stream: the context's work may still run on its bound stream; "
+                                "call synchronize() before using it from another stream")
+        _check(rc, "kvrt_bind_stream")
 
     @staticmethod
     def _slots(slots: Iterable[int]) -> tuple[ctypes.Array, int]:
@@ -277,10 +298,12 @@ class KVRuntime:
         return self._free_slots.pop()
 
     def release_slot(self, slot: int) -> None:
-        """Return a slot to the free list; its lengths drop to 0 (no bytes move)."""
+        """Return a slot to the free list; its prefix mask is cleared and its
+        lengths drop to 0 (no bytes move)."""
         slot = int(slot)
         if not 0 <= slot < self.n_slots or slot in self._free_slots:
             raise ValueError(f"kvrt: slot {slot} is not in use")
+        self.set_prefix_attention(slot, None)
         self.truncate(slot, 0)
         self._free_slots.append(slot)
         self._free_slots.sort(reverse=True)
@@ -327,10 +350,48 @@ class KVRuntime:
                                                    ctypes.byref(vd)),
                "kvrt_write_positions_async")
 
-    def reset_slot(self, slot: int) -> None:
-        """Zero every stored row of a slot and set its lengths to 0."""
+    def reset_slot(self, slot: int) -> int:
+        """Zero every stored row of a slot, set its lengths to 0, clear its prefix
+        mask; returns the slot's new generation (the start of a session)."""
         self._bind()
         _check(self.lib.kvrt_reset_slot_async(self._ctx, int(slot)), "kvrt_reset_slot_async")
+        return self.slot_generation(slot)
+
+    def set_prefix_attention(self, slot: int, mask: torch.Tensor | None) -> None:
+        """Prefix-attention mask of a slot: key position k < P is visible only where
+        ``mask[..., k] != 0`` (int64 / int32 / bool, [1, P] or [P], P <= 512);
+        ``None`` clears it. The listener's per-session ``prefix_attention``
+        (native_listener_microbatch.py:1340-1414; gemma4_listener_kernels.cuh:517-518).
+        """
+        self._bind()
+        if mask is None:
+            _check(self.lib.kvrt_set_prefix_attention_async(self._ctx, int(slot), None),
+                   "kvrt_set_prefix_attention_async")
+            return
+        if not mask.is_cuda:
+            mask = mask.to(self.device)
+        mask = mask.contiguous()
+        md = tensor_desc(mask)
+        _check(self.lib.kvrt_set_prefix_attention_async(self._ctx, int(slot), ctypes.byref(md)),
+               "kvrt_set_prefix_attention_async")
+        # the mask is read on the stream: keep it alive until that work has run
+        mask.record_stream(torch.cuda.current_stream(self.device))
+
+    def import_session(self, slot: int, layers: Sequence[tuple[torch.Tensor, torch.Tensor]],
+                       prefix_attention: torch.Tensor | None = None) -> int:
+        """Start a session in ``slot``: reset it, import one HF layer view
+        [1, kv_heads, S, D] per non-shared layer (``layers[i]`` for layer i;
+        shared layers' entries are ignored) and set its prefix mask. Returns
+        the slot's generation. Mirrors gemma4_listener_batch_import_cache_async
+        (gemma4_listener_microbatch_impl.inc:2590-2640)."""
+        gen = self.reset_slot(slot)
+        for i, kv in enumerate(layers):
+            if self._owner(i) != i:
+                continue
+            self.import_(slot, i, kv[0], kv[1])
+        if prefix_attention is not None:
+            self.set_prefix_attention(slot, prefix_attention)
+        return gen
 
     # Query rows per kv head (g * Q) above which attention runs on the MFMA
     # prefill kernel instead of the split-K decode kernel.
@@ -443,26 +504,39 @@ class KVRuntime:
                "kvrt_gather_async")
         return out_k, out_v, mask
 
-    def truncate(self, slot: int, new_len: int, layer: int = -1) -> None:
-        """Rollback to new_len positions: a length edit, no KV bytes move."""
+    def truncate(self, slot: int, new_len: int, layer: int = -1, generation: int = L.KVRT_ANY_GENERATION) -> None:
+        """Rollback to new_len positions: a length edit, no KV bytes move.
+
+        Refused (``KVRTError`` code -2, nothing changes) below the slot's prefix
+        mask or, with a nonzero ``generation``, when the slot has been
+        replaced since (rewind_session_async's identity check, impl.inc:3588-3618)."""
         self._bind()
-        _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len)), "kvrt_truncate")
+        _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len), int(generation)), "kvrt_truncate")
 
     def evict(self, slot: int, keep_from: int) -> None:
+        self._own()
         _check(self.lib.kvrt_evict(self._ctx, slot, int(keep_from)), "kvrt_evict")
 
-    def copy_prefix(self, src_slot: int, dst_slot: int, n_tokens: int) -> None:
-        """Clone the first n_tokens positions of src_slot into dst_slot (all layers, one launch)."""
+    def copy_prefix(self, src_slot: int, dst_slot: int, n_tokens: int,
+                    generation: int = L.KVRT_ANY_GENERATION) -> int:
+        """Clone the first n_tokens positions of src_slot (and its prefix mask) into
+        dst_slot (all layers, one launch); returns dst_slot's new generation.
+        A nonzero ``generation`` must be src_slot's current one."""
         self._bind()
-        _check(self.lib.kvrt_copy_prefix_async(self._ctx, src_slot, dst_slot, int(n_tokens)),
+        _check(self.lib.kvrt_copy_prefix_async(self._ctx, src_slot, dst_slot, int(n_tokens), int(generation)),
                "kvrt_copy_prefix_async")
+        return self.slot_generation(dst_slot)
 
-    def copy_session(self, dst_slot: int, src: "KVRuntime", src_slot: int, n_tokens: int) -> None:
+    def copy_session(self, dst_slot: int, src: "KVRuntime", src_slot: int, n_tokens: int,
+                     generation: int = L.KVRT_ANY_GENERATION) -> int:
         """Copy the first n_tokens positions of ``src``'s src_slot into dst_slot of this
-        runtime (identical topology), on this runtime's current stream."""
+        runtime (identical topology), on this runtime's current stream; returns
+        dst_slot's new generation."""
         self._bind()
-        _check(self.lib.kvrt_copy_session_async(self._ctx, int(dst_slot), src._ctx, int(src_slot), int(n_tokens)),
+        _check(self.lib.kvrt_copy_session_async(self._ctx, int(dst_slot), src._ctx, int(src_slot), int(n_tokens),
+                                                int(generation)),
                "kvrt_copy_session_async")
+        return self.slot_generation(dst_slot)
 
     def set_layer_rope(self, layer: int, inv_freq: Sequence[float] | None, scaling: float = 1.0) -> None:
         """RoPE inverse frequencies (head_dim / 2 fp32 values) of a layer for rollover."""
@@ -474,22 +548,36 @@ class KVRuntime:
         arr = (ctypes.c_float * max(1, len(vals)))(*vals)
         _check(self.lib.kvrt_set_layer_rope(self._ctx, layer, arr, len(vals), float(scaling)), "kvrt_set_layer_rope")
 
-    def rollover(self, slot: int, prefix_len: int, retained_rows: int) -> None:
+    def rollover(self, slot: int, prefix_len: int, retained_rows: int,
+                 generation: int = L.KVRT_ANY_GENERATION) -> None:
         """Keep the prefix, move the newest retained_rows rows behind it and
         rotate their keys by the position shift (layers with a RoPE table)."""
         self._bind()
-        _check(self.lib.kvrt_rollover_async(self._ctx, int(slot), int(prefix_len), int(retained_rows)),
+        _check(self.lib.kvrt_rollover_async(self._ctx, int(slot), int(prefix_len), int(retained_rows),
+                                            int(generation)),
                "kvrt_rollover_async")
 
     # ---- state -----------------------------------------------------------------
+    def slot_info(self, slot: int) -> dict[str, int]:
+        """generation, prefix_len, min_len and max_len of a slot."""
+        self._own()
+        info = L.KvrtSlotInfo()
+        _check(self.lib.kvrt_slot_info_get(self._ctx, int(slot), ctypes.byref(info)), "kvrt_slot_info_get")
+        return {name: int(getattr(info, name)) for name, _ in L.KvrtSlotInfo._fields_ if name != "reserved"}
+
+    def slot_generation(self, slot: int) -> int:
+        return self.slot_info(slot)["generation"]
+
     def seq_length(self, slot: int, layer: int = 0) -> int:
+        self._own()
         out = ctypes.c_int32()
         _check(self.lib.kvrt_session_state(self._ctx, slot, layer, ctypes.byref(out)), "kvrt_session_state")
         return int(out.value)
 
     def sync_lengths(self) -> None:
-        """Reload host lengths from the device (after HIP graph replays)."""
-        self._bind()
+        """Synchronise the bound stream and reload host lengths from the device
+        (after HIP graph replays)."""
+        self._own()
         _check(self.lib.kvrt_sync_lengths(self._ctx), "kvrt_sync_lengths")
 
     def counters(self) -> dict[str, int]:
@@ -498,10 +586,13 @@ class KVRuntime:
         return {name: int(getattr(c, name)) for name, _ in L.KvrtCounters._fields_}
 
     def health(self) -> int:
-        """Synchronise and return the kvrt status code (0 = healthy)."""
-        # A poisoned context refuses the rebind; kvrt_health reports it.
-        self.lib.kvrt_bind_stream(self._ctx, ctypes.c_void_p(current_stream_handle(self.device)))
+        """Synchronise the bound stream and return the kvrt status code (0 = healthy)."""
+        self._own()
         return int(self.lib.kvrt_health(self._ctx))
+
+    def synchronize(self) -> None:
+        """Wait for the context's work; afterwards it may move to another stream."""
+        _check(self.health(), "kvrt_health")
 
     def layer_view(self, slot: int, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
         """HF-shaped [1, kv_heads, L, D] views of a slot's logical K/V.
@@ -530,11 +621,13 @@ class KVRuntime:
 
 
 def attend_tensors(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lengths: torch.Tensor,
-                   scale: float, window: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+                   scale: float, window: int = 0, out: torch.Tensor | None = None,
+                   prefix_attention: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention over caller-owned K/V [n, kv_heads, Lmax, D] with per-item lengths.
 
     q [n, Hq, Q, D] bf16; lengths int32 [n] on the device. Query row i of item
-    b sits at position lengths[b] - Q + i.
+    b sits at position lengths[b] - Q + i. ``prefix_attention`` [n, P]
+    (int64 / int32 / bool, P <= 512) hides key j < P of item b where it is 0.
     """
     lib = L.load()
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (lengths, "lengths")):
@@ -543,11 +636,23 @@ def attend_tensors(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lengths: t
     lengths = lengths.to(torch.int32).contiguous()
     out = torch.empty_like(q) if out is None else out
     qd, kd, vd, od = tensor_desc(q), tensor_desc(k), tensor_desc(v), tensor_desc(out)
+    pd = None
+    if prefix_attention is not None:
+        require_cuda(prefix_attention, "prefix_attention")
+        prefix_attention = prefix_attention.contiguous()
+        pd = ctypes.byref(tensor_desc(prefix_attention))
     _check(lib.kvrt_attend_tensors_async(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd),
-                                         ctypes.c_void_p(lengths.data_ptr()), ctypes.byref(od), float(scale),
+                                         ctypes.c_void_p(lengths.data_ptr()), pd, ctypes.byref(od), float(scale),
                                          int(window), ctypes.c_void_p(current_stream_handle(q.device))),
            "kvrt_attend_tensors_async")
     return out
+
+
+def tensors_status(device: torch.device | str | None = None) -> int:
+    """Synchronise the current stream; report and clear the error flag of its
+    tensor-attention workspace (0, or -6 when a length was clamped)."""
+    dev = torch.device(device if device is not None else "cuda")
+    return int(L.load().kvrt_tensors_status(ctypes.c_void_p(current_stream_handle(dev))))
 
 
 def copy_rows(src: torch.Tensor, dst: torch.Tensor, rows: int) -> None:

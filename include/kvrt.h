@@ -23,11 +23,16 @@
  *     borrowed for the duration of the enqueued work; KV storage is owned by
  *     the context unless the caller binds its own storage at create time.
  *   - every mutating call is asynchronous on the stream bound with
- *     kvrt_bind_stream (default: the null stream). Lengths are tracked on the
+ *     kvrt_bind_stream (default: the null stream). A context stays on its
+ *     bound stream: binding another one is refused while work enqueued by the
+ *     context may still run (see kvrt_bind_stream). Lengths are tracked on the
  *     host (authoritative, used for validation) and mirrored in device memory
  *     where the kernels read them.
  *   - one owner host thread per context; calls on one context are not
- *     thread-safe.
+ *     thread-safe (the Python binding asserts its creating thread).
+ *   - every slot carries a generation, renewed whenever the slot's contents
+ *     are replaced (reset, clone / copy into it); the lifecycle calls take
+ *     the generation the caller last saw and refuse a stale one.
  *
  * Stream handles are passed as void* (a hipStream_t) so that the header
  * needs no HIP or torch types.
@@ -42,11 +47,13 @@
 extern "C" {
 #endif
 
-#define KVRT_ABI_VERSION 1u
+#define KVRT_ABI_VERSION 2u
 #define KVRT_MAX_RANK 4
 #define KVRT_MAX_ITEMS 64      /* slots per batched call                 */
 #define KVRT_MAX_POSITIONS 128 /* rows per kvrt_write_positions_async call */
 #define KVRT_MAX_ROLLOVER_ROWS 128 /* rows kept by one kvrt_rollover_async    */
+#define KVRT_MAX_PREFIX_MASK 512   /* positions a prefix-attention mask covers  */
+#define KVRT_ANY_GENERATION 0ull   /* expected_generation: skip the slot check  */
 
 /* ---- return codes ------------------------------------------------------ */
 #define KVRT_OK 0
@@ -68,6 +75,9 @@ extern "C" {
 #define KVRT_CAP_TENSOR_ATTEND (1ull << 7)
 #define KVRT_CAP_PREFILL_MFMA (1ull << 8)
 #define KVRT_CAP_TALKER_MASK (1ull << 9)
+#define KVRT_CAP_PREFIX_ATTENTION (1ull << 10)
+#define KVRT_CAP_SLOT_GENERATION (1ull << 11)
+#define KVRT_CAP_STREAM_CONFINED (1ull << 12)
 
 /* ---- enums ------------------------------------------------------------- */
 enum kvrt_layout {
@@ -82,6 +92,7 @@ enum kvrt_dtype {
     KVRT_FP32 = 2,
     KVRT_BOOL = 3, /* 1 byte: 0 / 1 */
     KVRT_INT32 = 4,
+    KVRT_INT64 = 5,
 };
 
 /* ---- descriptors --------------------------------------------------------- */
@@ -198,8 +209,16 @@ int kvrt_layer_storage_bytes(const kvrt_config *config, const kvrt_layer_spec *l
                              uint64_t *kv_bytes, uint64_t *scale_bytes);
 /* Replaces gemma4_cache_destroy (gemma4_listener_cache.cu:463-475). */
 int kvrt_destroy(kvrt_ctx *ctx);
-/* Replaces the bound-stream contract of the batch API
- * (gemma4_listener_microbatch_impl.inc:445-473). */
+/* Bind the stream every later call of the context enqueues on. Binding the
+ * bound stream again is a no-op. Binding a different stream returns
+ * KVRT_ESTATE (nothing changes) while work the context enqueued may still be
+ * running: kvrt_health or kvrt_sync_lengths synchronise the bound stream and
+ * then allow the switch. A context's split-K workspace and arrival counters
+ * are shared by its calls, so two streams in flight on one context would
+ * race on them.
+ * Replaces the bound-stream contract of the batch API
+ * (gemma4_listener_microbatch_impl.inc:445-473: a second stream is refused
+ * with -6; gemma4_listener.cu:2053). */
 int kvrt_bind_stream(kvrt_ctx *ctx, void *hip_stream);
 /* Device pointers of a layer's storage (shared layers report their source). */
 int kvrt_layer_storage(kvrt_ctx *ctx, int32_t layer, kvrt_storage *out);
@@ -243,11 +262,52 @@ int kvrt_append_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *sl
 int kvrt_write_positions_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
                                const int32_t *positions, const kvrt_tensor *k, const kvrt_tensor *v);
 
-/* Zero every stored row of a slot (all layers), set its lengths to 0 and
- * release its pages (PAGED layers). Replaces _SlotKVCache.reset
- * (duplex_kernel/future_prefix.py:582-586) and the arena memset before a
- * talker prefix import (native/qwen_talker/qwen_talker.cu:1060-1110). */
+/* Zero every stored row of a slot (all layers), set its lengths to 0,
+ * release its pages (PAGED layers), clear its prefix-attention mask and give
+ * it a new generation (the start of a session in the slot). Replaces
+ * _SlotKVCache.reset (duplex_kernel/future_prefix.py:582-586) and the arena
+ * memset before a talker prefix import (native/qwen_talker/
+ * qwen_talker.cu:1060-1110). */
 int kvrt_reset_slot_async(kvrt_ctx *ctx, int32_t slot);
+
+/* Per-slot prefix-attention mask: key position k < P is visible only where
+ * mask[k] != 0; positions >= P are unaffected. Applies on every layer of the
+ * slot, on top of causal and window visibility, in kvrt_attend_decode_async,
+ * kvrt_append_attend_async and kvrt_attend_prefill_async. mask is a DEVICE
+ * tensor [1, P] or [P] of KVRT_INT64 (the reference's dtype), KVRT_INT32 or
+ * KVRT_BOOL, 0 <= P <= KVRT_MAX_PREFIX_MASK; NULL or P = 0 clears the mask.
+ * It is read on the bound stream, so the caller keeps it alive until the
+ * call's work has run. Clones and copies carry the mask; kvrt_truncate
+ * refuses lengths below P; kvrt_rollover_async keeps positions
+ * below its prefix_len, which must be >= P. A captured HIP graph reads the
+ * masks of its slots at replay time, but only if its slots had a mask when
+ * it was captured.
+ * Replaces the prefix_attention argument of
+ * gemma4_listener_batch_import_cache_async
+ * (native/gemma4_listener_microbatch/gemma4_listener_microbatch_impl.inc:
+ * 2590-2621; bound at duplex_kernel/native_listener_microbatch.py:1340-1414)
+ * and its use in every listener attention path (prefix_valid in
+ * gemma4_listener_kernels.cuh:517-518, :595-597, :743-745,
+ * gemma4_listener_attention_ordered.cu:96-101, impl.inc:2659-2660); the
+ * canonical default mask (34 positions, only 0 and 33 visible) is
+ * kernel_set_canonical_prefix_mask (gemma4_listener_kernels.cuh:111-118). */
+int kvrt_set_prefix_attention_async(kvrt_ctx *ctx, int32_t slot, const kvrt_tensor *mask);
+
+/* Identity and state of one slot. generation is renewed by
+ * kvrt_reset_slot_async and by a clone / copy into the slot (never 0);
+ * prefix_len is the length of its prefix-attention mask (0: none); min_len /
+ * max_len the smallest / largest length over its non-shared layers.
+ * Replaces the slot record of the batch API (session_generation,
+ * prefix_len, current_position: gemma4_listener_microbatch_impl.inc:8-21)
+ * and gemma4_listener_batch_get_session_state (:3920-3950). */
+typedef struct kvrt_slot_info {
+    uint64_t generation;
+    int32_t prefix_len;
+    int32_t min_len;
+    int32_t max_len;
+    int32_t reserved;
+} kvrt_slot_info;
+int kvrt_slot_info_get(kvrt_ctx *ctx, int32_t slot, kvrt_slot_info *out);
 
 /* Gather n slots of one layer into a zero-padded batch:
  * out_k, out_v [n, kv_heads, Lmax, D] (bf16 for bf16 layers, fp32
@@ -264,13 +324,19 @@ int kvrt_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *sl
 
 /* Turn-local rollback: set the length of (slot, layer) to new_len
  * (layer = -1: every layer). Moves no KV bytes. Fails with KVRT_ESTATE when
- * new_len exceeds the current length, or when a RING layer would need rows
- * already overwritten (L > ring_rows and new_len - window + 1 < L - ring_rows,
- * i.e. a rollback deeper than ring_rows - window + 1 positions).
+ * the slot's generation is not expected_generation (KVRT_ANY_GENERATION
+ * skips the check), when new_len exceeds the current length or lies below
+ * the slot's prefix-attention mask (the rewind floor), or when a RING layer
+ * would need rows already overwritten (L > ring_rows and new_len - window + 1
+ * < L - ring_rows, i.e. a rollback deeper than ring_rows - window + 1
+ * positions). Nothing changes when it fails.
  * Replaces TurnKVState.truncate_to_prefix / _slice_kv
- * (duplex_kernel/kv_cache.py:99-104, :205-216) and gemma4_cache_truncate_async
- * (gemma4_listener_cache.cu:409-421). */
-int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len);
+ * (duplex_kernel/kv_cache.py:99-104, :205-216), gemma4_cache_truncate_async
+ * (gemma4_listener_cache.cu:409-421) and the identity-checked
+ * gemma4_listener_batch_rewind_session_async
+ * (gemma4_listener_microbatch_impl.inc:3588-3618: stale identity or a target
+ * below prefix_len -> -2). */
+int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation);
 
 /* PAGED: release every page of slot wholly below position keep_from (all
  * layers share one page table per slot). Positions below keep_from must not
@@ -279,17 +345,21 @@ int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len);
 int kvrt_evict(kvrt_ctx *ctx, int32_t slot, int32_t keep_from);
 
 /* Copy the first n_tokens positions of every non-shared layer from src_slot
- * to dst_slot in one launch (dst lengths become n_tokens). CONTIG layers copy
+ * to dst_slot in one launch (dst lengths become n_tokens), with src_slot's
+ * prefix-attention mask; dst_slot gets a new generation. CONTIG layers copy
  * all n_tokens rows; RING layers the rows still in the ring; PAGED layers
  * (bf16 or int8 with scales) the rows on live pages, into freshly mapped
  * pages of dst_slot (its previous pages are released first). KVRT_ESTATE if
- * a key the next query would see is no longer resident in src_slot,
- * KVRT_ENOMEM (nothing changed) if the pool cannot hold the copy.
+ * src_slot's generation is not src_generation (KVRT_ANY_GENERATION skips
+ * the check), if n_tokens lies below src_slot's prefix mask, or if a key the
+ * next query would see is no longer resident in src_slot; KVRT_ENOMEM
+ * (nothing changed) if the pool cannot hold the copy.
  * Replaces copy_static_cache_prefix (duplex_kernel/thinker_cache.py:83-190),
  * gemma4_cache_copy_async (gemma4_listener_cache.cu:306-345) and the KV part
  * of gemma4_listener_batch_clone_session_slot_async
  * (gemma4_listener_microbatch_impl.inc:4046-4119). */
-int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, int32_t n_tokens);
+int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, int32_t n_tokens,
+                           uint64_t src_generation);
 
 /* The same copy between two contexts of identical topology (layer specs,
  * aliasing, block size, device), enqueued on dst's stream; work on src's
@@ -297,7 +367,7 @@ int kvrt_copy_prefix_async(kvrt_ctx *ctx, int32_t src_slot, int32_t dst_slot, in
  * Replaces the KV part of gemma4_listener_batch_copy_session_cache_async
  * (gemma4_listener_microbatch_impl.inc:4121-4172). */
 int kvrt_copy_session_async(kvrt_ctx *dst, int32_t dst_slot, kvrt_ctx *src, int32_t src_slot,
-                            int32_t n_tokens);
+                            int32_t n_tokens, uint64_t src_generation);
 
 /* RoPE table of one non-shared bf16 layer for kvrt_rollover_async:
  * inv_freq[head_dim / 2] (host, fp32; 0 leaves a pair unrotated) and the
@@ -317,13 +387,16 @@ int kvrt_set_layer_rope(kvrt_ctx *ctx, int32_t layer, const float *inv_freq, int
  * for the pair (x1, x2) = (dim i, dim i + D/2). Lengths become prefix_len +
  * retained_rows. Requires CONTIG or PAGED bf16 layers (a RING drops the prefix
  * rows the next window needs), equal lengths L over the slot's layers,
- * L > prefix_len + retained_rows, 0 < retained_rows <= KVRT_MAX_ROLLOVER_ROWS
- * and, for PAGED, no evicted page.
+ * L > prefix_len + retained_rows, 0 < retained_rows <= KVRT_MAX_ROLLOVER_ROWS,
+ * prefix_len >= the slot's prefix-attention mask (which stays as it is),
+ * the slot's generation equal to expected_generation (KVRT_ANY_GENERATION
+ * skips the check) and, for PAGED, no evicted page.
  * Replaces gemma4_cache_rebase_async (native/gemma4_listener/
  * gemma4_listener_cache.cu:303-351) and the per-layer kernel_rope_rebase_bf16
  * launches of gemma4_listener_batch_rollover_async
  * (gemma4_listener_microbatch_impl.inc:3835-3895). */
-int kvrt_rollover_async(kvrt_ctx *ctx, int32_t slot, int32_t prefix_len, int32_t retained_rows);
+int kvrt_rollover_async(kvrt_ctx *ctx, int32_t slot, int32_t prefix_len, int32_t retained_rows,
+                        uint64_t expected_generation);
 
 /* GQA decode attention over the last Q positions of n slots of one layer:
  * q [n, Hq, Q, D] bf16 contiguous, out [n, Hq, Q, D] bf16 contiguous.
@@ -405,13 +478,31 @@ int kvrt_attend_talker_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
 /* ---- context-free tensor kernels ------------------------------------------ */
 /* Decode attention over caller-owned HF-shaped K/V: k, v [n, kv_heads, Lmax, D]
  * bf16 (strided, last dim contiguous), lengths int32[n] in DEVICE memory,
- * q/out [n, Hq, Q, D]; window as above (0 = global). Used for the padded
- * batch produced by kvrt_gather_async and for HF cache objects.
+ * q/out [n, Hq, Q, D]; window as above (0 = global); row j of item b is key
+ * position j. prefix_attention (may be NULL) is a DEVICE tensor [n, P] of
+ * KVRT_INT64 / KVRT_INT32 / KVRT_BOOL, P <= KVRT_MAX_PREFIX_MASK: key j < P
+ * of item b is visible only where prefix_attention[b, j] != 0. Used for the
+ * padded batch produced by kvrt_gather_async and for HF cache objects.
+ * The split-K partials live in a workspace the library keeps per (device,
+ * stream): calls on one stream share it in stream order, calls on different
+ * streams never do. A call that would need a larger workspace while its
+ * stream is being captured returns KVRT_ESTATE (make one eager call of the
+ * largest shape first); outgrown workspaces are kept until the process ends,
+ * since captured graphs may still use them. Lengths beyond Lmax are clamped
+ * and raise the stream's error flag (kvrt_tensors_status).
  * Replaces sdpa_attention_forward on padded K/V + mask
- * (shape_stable_listener.py:232-251). */
+ * (shape_stable_listener.py:232-251) and the listener's prefix_valid term
+ * (gemma4_listener_kernels.cuh:517-518). */
 int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
-                              const int32_t *device_lengths, const kvrt_tensor *out,
-                              float scale, int32_t window, void *hip_stream);
+                              const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
+                              const kvrt_tensor *out, float scale, int32_t window, void *hip_stream);
+
+/* Synchronise hip_stream, then report and clear the error flag of the
+ * stream's kvrt_attend_tensors_async workspace: KVRT_OK, KVRT_EFAULT (a
+ * length beyond its K/V rows was clamped) or KVRT_EDEVICE. KVRT_OK when the
+ * stream has no workspace yet. Replaces the talker's device error flag check
+ * (native/qwen_talker/qwen_talker_kernels.cu:243-246) for this path. */
+int kvrt_tensors_status(void *hip_stream);
 
 /* Row copy between two 4-D strided tensors of the same element size
  * (2 or 4 bytes) over dims (d0, d1, rows, D): dst[:, :, :rows] = src[:, :, :rows].

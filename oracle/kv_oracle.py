@@ -23,8 +23,18 @@ tree; HF = transformers.cache_utils, a third-party dependency pinned at
 * attend  — ``F.scaled_dot_product_attention`` over ``repeat_kv``'d K/V with
   fp32 softmax (shape_stable_listener.py:241-251); visibility as
   kernel_build_explicit_sdpa_mask (gemma4_listener_kernels.cuh:500-525):
-  key k visible to query position p iff k <= p and, for window W > 0,
-  k >= p - W + 1; GQA q head h reads kv head h // (Hq / Hkv).
+  key k visible to query position p iff prefix_valid (k >= P or
+  prefix_attention[k] != 0, :517-518; P = 0 without a mask), k <= p and,
+  for window W > 0, k >= p - W + 1; GQA q head h reads kv head
+  h // (Hq / Hkv). The same prefix term gates every listener attention path
+  (kernel_stream_sdpa_q4_bf16 :595-597, kernel_prefill_sdpa_bf16 :743-745,
+  gemma4_listener_attention_ordered.cu:96-101,
+  gemma4_listener_microbatch_impl.inc:2659-2660).
+* canonical prefix mask — kernel_set_canonical_prefix_mask
+  (gemma4_listener_kernels.cuh:111-118): position 0 (BOS) and the last
+  position (BOA) visible, the 32 text slots between them not; 34 positions
+  by default (GEMMA4_CANONICAL_PREFIX_LEN, generated_topology.h:22; the
+  Python side asserts the same mask, duplex_kernel/listener.py:1983-1988).
 * sliding retention — HF ``DynamicSlidingWindowLayer`` keeps the last W-1
   rows after an update (cache_utils.py:229-261); window start of the native
   cache ``base - W + 1`` (gemma4_listener_cache.cu:448-452).
@@ -128,15 +138,39 @@ def dequantize_int8(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
 # attention
 # ---------------------------------------------------------------------------
 
+CANONICAL_PREFIX_LEN = 34  # GEMMA4_CANONICAL_PREFIX_LEN (generated_topology.h:22)
+
+
+def canonical_prefix_mask(length: int = CANONICAL_PREFIX_LEN) -> np.ndarray:
+    """int64 [length]: 1 at position 0 and length - 1, else 0
+    (kernel_set_canonical_prefix_mask, gemma4_listener_kernels.cuh:111-118)."""
+    idx = np.arange(length)
+    return ((idx == 0) | (idx == length - 1)).astype(np.int64)
+
+
+def prefix_valid(key_positions: np.ndarray, prefix_attention: np.ndarray | None) -> np.ndarray:
+    """Boolean per key: k >= P or prefix_attention[k] != 0 (P = its length;
+    no mask: all True), gemma4_listener_kernels.cuh:517-518."""
+    kp = np.asarray(key_positions)
+    if prefix_attention is None:
+        return np.ones(kp.shape, dtype=bool)
+    pm = np.asarray(prefix_attention).reshape(-1)
+    inside = (kp >= 0) & (kp < pm.size)
+    out = np.ones(kp.shape, dtype=bool)
+    out[inside] = pm[kp[inside]] != 0
+    return out
+
 
 def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_positions: np.ndarray, scale: float,
-           window: int = 0, key_positions: np.ndarray | None = None) -> np.ndarray:
+           window: int = 0, key_positions: np.ndarray | None = None,
+           prefix_attention: np.ndarray | None = None) -> np.ndarray:
     """Masked GQA attention, float64 softmax.
 
     q [Hq, Q, D]; k, v [Hkv, L, D] (already dequantised, float32);
     q_positions [Q] absolute query positions; key_positions [L] absolute key
-    positions (default 0..L-1). Returns float32 [Hq, Q, D]; a row with no
-    visible key is 0.
+    positions (default 0..L-1); prefix_attention [P] (or None): key position
+    k < P is visible only where prefix_attention[k] != 0. Returns float32
+    [Hq, Q, D]; a row with no visible key is 0.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -147,13 +181,14 @@ def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_positions: np.ndarray,
         raise ValueError("Hq must be a multiple of Hkv")
     g = hq // hkv
     kp = np.arange(n_keys) if key_positions is None else np.asarray(key_positions)
+    pv = prefix_valid(kp, prefix_attention)
     out = np.zeros((hq, qn, d), dtype=np.float64)
     for h in range(hq):
         kh = h // g  # HF repeat_kv: kv head j serves q heads j*g .. j*g+g-1
         s = (q[h] @ k[kh].T) * float(scale)  # [Q, L]
         for i in range(qn):
             lo, hi = visible_range(int(q_positions[i]), window)
-            vis = (kp >= lo) & (kp <= hi)
+            vis = (kp >= lo) & (kp <= hi) & pv
             if not vis.any():
                 continue
             row = np.where(vis, s[i], -np.inf)
@@ -286,18 +321,20 @@ def gemma_inv_freq(head_dim: int, base: float, rotary_pairs: int | None = None) 
     return out
 
 
-def attend_bruteforce(q, k, v, q_positions, scale, window=0):
+def attend_bruteforce(q, k, v, q_positions, scale, window=0, prefix_attention=None):
     """Pure-Python-loop attention (tiny shapes only): golden-vector generator."""
     hq, qn, d = len(q), len(q[0]), len(q[0][0])
     hkv, n_keys = len(k), len(k[0])
     g = hq // hkv
     out = [[[0.0] * d for _ in range(qn)] for _ in range(hq)]
+    pm = [] if prefix_attention is None else [int(x) for x in prefix_attention]
     import math
     for h in range(hq):
         kh = h // g
         for i in range(qn):
             p_pos = q_positions[i]
-            vis = [j for j in range(n_keys) if j <= p_pos and (window <= 0 or j >= p_pos - window + 1)]
+            vis = [j for j in range(n_keys) if j <= p_pos and (window <= 0 or j >= p_pos - window + 1)
+                   and (j >= len(pm) or pm[j] != 0)]
             if not vis:
                 continue
             scores = {j: sum(q[h][i][t] * k[kh][j][t] for t in range(d)) * scale for j in vis}
@@ -357,6 +394,19 @@ class OracleCache:
     layers: list
     n_slots: int
     rows: dict = field(default_factory=dict)
+    prefix: dict = field(default_factory=dict)  # slot -> prefix_attention [P] (per slot, all layers)
+
+    def set_prefix_attention(self, slot: int, mask) -> None:
+        """The slot's prefix-attention mask (None clears it), imported with the
+        session (gemma4_listener_microbatch_impl.inc:2590-2621)."""
+        if mask is None or np.asarray(mask).size == 0:
+            self.prefix.pop(slot, None)
+        else:
+            self.prefix[slot] = np.asarray(mask).reshape(-1).astype(np.int64).copy()
+
+    def copy_prefix_attention(self, src: int, dst: int) -> None:
+        """Clones carry the source's mask (impl.inc:4100, :4162)."""
+        self.set_prefix_attention(dst, self.prefix.get(src))
 
     def _get(self, slot, layer):
         key = (slot, layer)
@@ -451,7 +501,8 @@ class OracleCache:
         lo = 0 if window <= 0 else max(0, n_keys - qn - window + 1)
         pos = np.arange(n_keys - qn, n_keys)
         # keys below the first query's window are never visible: skip them
-        return attend(q, kk[:, lo:], vv[:, lo:], pos, scale, window, key_positions=np.arange(lo, n_keys))
+        return attend(q, kk[:, lo:], vv[:, lo:], pos, scale, window, key_positions=np.arange(lo, n_keys),
+                      prefix_attention=self.prefix.get(slot))
 
 
 def sliding_retained(length: int, window: int) -> tuple[int, int]:

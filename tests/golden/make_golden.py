@@ -7,6 +7,10 @@
   ``oracle.kv_oracle.attend_bruteforce`` (plain loops, math.exp), which is
   independent of the vectorised numpy oracle the tests check against it.
   head_dim is 64 so that the GPU kernel can run the same cases.
+* ``attention_prefix_small.npz`` — the same kind of cases under a listener
+  prefix-attention mask (key k < P visible only where mask[k] != 0): the
+  canonical 34-position mask, a seeded random mask under a sliding window,
+  and a mask that leaves a single visible key.
 * ``int8_small.npz`` — per-row symmetric int8 quantisation worked out with
   Python's own ``round`` (round half to even) and explicit clamping, on rows
   that include exact ties, an all-zero row and a row with one huge value.
@@ -41,6 +45,23 @@ ATTN_CASES = [
 ]
 
 
+# (name, Hq, Hkv, D, L, Q, window, scale, seed, mask kind, P)
+PREFIX_CASES = [
+    ("canonical34_q2", 8, 1, 64, 40, 2, 0, 0.125, 201, "canonical", 34),
+    ("canonical34_first_query", 4, 1, 64, 35, 1, 0, 0.125, 202, "canonical", 34),
+    ("random40_sliding24_q2", 8, 2, 64, 60, 2, 24, 0.125, 203, "random", 40),
+    ("single_prefix_key", 4, 1, 64, 12, 1, 0, 0.125, 204, "single5", 12),
+]
+
+
+def prefix_mask(kind: str, p: int, gen: torch.Generator) -> list[int]:
+    if kind == "canonical":  # kernel_set_canonical_prefix_mask: positions 0 and p - 1
+        return [1 if i in (0, p - 1) else 0 for i in range(p)]
+    if kind == "random":
+        return [int(x) for x in torch.randint(0, 2, (p,), generator=gen).tolist()]
+    return [1 if i == 5 else 0 for i in range(p)]
+
+
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
     return t.to(torch.bfloat16).contiguous().view(torch.int16).numpy().view(np.uint16)
 
@@ -61,6 +82,27 @@ def make_attention() -> None:
         arrays[f"{name}.meta"] = np.asarray([hq, hkv, d, n_keys, qn, window], dtype=np.int64)
         arrays[f"{name}.scale"] = np.asarray([scale], dtype=np.float64)
     np.savez_compressed(OUT / "attention_small.npz", **arrays)
+
+
+def make_attention_prefix() -> None:
+    arrays = {}
+    for name, hq, hkv, d, n_keys, qn, window, scale, seed, kind, plen in PREFIX_CASES:
+        gen = torch.Generator().manual_seed(seed)
+        k = torch.randn((hkv, n_keys, d), generator=gen).to(torch.bfloat16)
+        v = torch.randn((hkv, n_keys, d), generator=gen).to(torch.bfloat16)
+        q = (0.5 * torch.randn((hq, qn, d), generator=gen)).to(torch.bfloat16)
+        mask = prefix_mask(kind, plen, gen)
+        pos = list(range(n_keys - qn, n_keys))
+        out = attend_bruteforce(q.float().tolist(), k.float().tolist(), v.float().tolist(), pos, scale, window,
+                                prefix_attention=mask)
+        arrays[f"{name}.q"] = bf16_bits(q)
+        arrays[f"{name}.k"] = bf16_bits(k)
+        arrays[f"{name}.v"] = bf16_bits(v)
+        arrays[f"{name}.mask"] = np.asarray(mask, dtype=np.int64)
+        arrays[f"{name}.out"] = np.asarray(out, dtype=np.float64)
+        arrays[f"{name}.meta"] = np.asarray([hq, hkv, d, n_keys, qn, window], dtype=np.int64)
+        arrays[f"{name}.scale"] = np.asarray([scale], dtype=np.float64)
+    np.savez_compressed(OUT / "attention_prefix_small.npz", **arrays)
 
 
 def quantise_row(row: list[float]) -> tuple[list[int], float]:
@@ -133,6 +175,12 @@ REFERENCE_KATS = {
         "source": "tests/kernel/test_qwen_native_audio_q1.py:267-277",
         "start": 127, "frames": 40,
     },
+    "canonical_prefix_mask": {
+        "source": "native/gemma4_listener_microbatch/gemma4_listener_kernels.cuh:111-118 "
+                  "(kernel_set_canonical_prefix_mask), generated_topology.h:22 (GEMMA4_CANONICAL_PREFIX_LEN), "
+                  "duplex_kernel/listener.py:1983-1988 (BOS + 32 slots + BOA)",
+        "length": 34, "visible": [0, 33],
+    },
     "slot_kv_cache": {
         "source": "tests/kernel/test_future_prefix_slot_kv_cache.py:24-86",
         "joint_writes": [[[0, 1], 2], [[2, 4], 5], [[3, 5], 6]],
@@ -144,6 +192,7 @@ REFERENCE_KATS = {
 
 def main() -> None:
     make_attention()
+    make_attention_prefix()
     make_int8()
     (OUT / "reference_kats.json").write_text(json.dumps(REFERENCE_KATS, indent=1) + "\n")
     print("golden vectors written to", OUT)

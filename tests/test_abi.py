@@ -46,10 +46,11 @@ def test_every_declared_function_is_exported_and_bound():
 
 def test_version_capabilities_and_error_strings():
     L, lib = _lib()
-    assert lib.kvrt_abi_version() == 1
+    assert lib.kvrt_abi_version() == L.KVRT_ABI_VERSION == 2
     caps = lib.kvrt_capabilities()
     for bit in (L.CAP_CONTIG, L.CAP_RING, L.CAP_PAGED, L.CAP_INT8, L.CAP_FUSED_APPEND_ATTEND, L.CAP_GATHER,
-                L.CAP_DEVICE_LENGTHS, L.CAP_TENSOR_ATTEND, L.CAP_PREFILL_MFMA, L.CAP_TALKER_MASK):
+                L.CAP_DEVICE_LENGTHS, L.CAP_TENSOR_ATTEND, L.CAP_PREFILL_MFMA, L.CAP_TALKER_MASK,
+                L.CAP_PREFIX_ATTENTION, L.CAP_SLOT_GENERATION, L.CAP_STREAM_CONFINED):
         assert caps & bit
     assert L.strerror(0) == "ok"
     for code in range(-1, -7, -1):
@@ -79,15 +80,19 @@ int main(void) {
   F(kvrt_talker_mask, prefix_start); F(kvrt_talker_mask, audio_start); F(kvrt_talker_mask, prefix_position);
   F(kvrt_talker_mask, audio_position); F(kvrt_talker_mask, prefix_attention_mode);
   F(kvrt_talker_mask, visible_prefix_count); F(kvrt_talker_mask, prefix_log_gate);
+  F(kvrt_slot_info, generation); F(kvrt_slot_info, prefix_len); F(kvrt_slot_info, min_len);
+  F(kvrt_slot_info, max_len); F(kvrt_slot_info, reserved);
   printf("\"const.KVRT_DECODE_AUTO\": [%d, 0], \"const.KVRT_DECODE_VALU\": [%d, 0], \"const.KVRT_DECODE_MFMA\": [%d, 0],\n",
          KVRT_DECODE_AUTO, KVRT_DECODE_VALU, KVRT_DECODE_MFMA);
   printf("\"const.KVRT_MERGE_AUTO\": [%d, 0], \"const.KVRT_MERGE_SEPARATE\": [%d, 0], \"const.KVRT_MERGE_LAST_WG\": [%d, 0],\n",
          KVRT_MERGE_AUTO, KVRT_MERGE_SEPARATE, KVRT_MERGE_LAST_WG);
+  printf("\"const.KVRT_MAX_PREFIX_MASK\": [%d, 0], \"const.KVRT_ANY_GENERATION\": [%d, 0], \"const.DT_INT64\": [%d, 0],\n",
+         KVRT_MAX_PREFIX_MASK, (int)KVRT_ANY_GENERATION, (int)KVRT_INT64);
   printf("\"sizeof.kvrt_tensor\": [%zu, 0], \"sizeof.kvrt_layer_spec\": [%zu, 0], \"sizeof.kvrt_config\": [%zu, 0],"
          " \"sizeof.kvrt_storage\": [%zu, 0], \"sizeof.kvrt_counters\": [%zu, 0],"
-         " \"sizeof.kvrt_talker_mask\": [%zu, 0]\n}\n",
+         " \"sizeof.kvrt_talker_mask\": [%zu, 0], \"sizeof.kvrt_slot_info\": [%zu, 0]\n}\n",
          sizeof(kvrt_tensor), sizeof(kvrt_layer_spec), sizeof(kvrt_config), sizeof(kvrt_storage),
-         sizeof(kvrt_counters), sizeof(kvrt_talker_mask));
+         sizeof(kvrt_counters), sizeof(kvrt_talker_mask), sizeof(kvrt_slot_info));
   return 0;
 }
 """
@@ -104,7 +109,8 @@ def test_ctypes_structs_match_the_c_header_layout(tmp_path):
     subprocess.run([gcc, "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
     layout = json.loads(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
     structs = {"kvrt_tensor": L.KvrtTensor, "kvrt_layer_spec": L.KvrtLayerSpec, "kvrt_config": L.KvrtConfig,
-               "kvrt_storage": L.KvrtStorage, "kvrt_counters": L.KvrtCounters, "kvrt_talker_mask": L.KvrtTalkerMask}
+               "kvrt_storage": L.KvrtStorage, "kvrt_counters": L.KvrtCounters, "kvrt_talker_mask": L.KvrtTalkerMask,
+               "kvrt_slot_info": L.KvrtSlotInfo}
     for key, (off, size) in layout.items():
         sname, field = key.split(".")
         if sname == "const":
@@ -176,12 +182,17 @@ def test_create_rejects_invalid_configs_before_touching_the_device(bad):
 def test_null_context_calls_fail_with_einval():
     L, lib = _lib()
     slots = (ctypes.c_int32 * 1)(0)
-    assert lib.kvrt_truncate(None, 0, 0, 0) == L.KVRT_EINVAL
+    assert lib.kvrt_truncate(None, 0, 0, 0, 0) == L.KVRT_EINVAL
     assert lib.kvrt_append_async(None, 0, 1, slots, None, None) == L.KVRT_EINVAL
     assert lib.kvrt_health(None) == L.KVRT_EINVAL
     assert lib.kvrt_destroy(None) == L.KVRT_EINVAL
-    assert lib.kvrt_attend_tensors_async(None, None, None, None, None, 1.0, 0, None) == L.KVRT_EINVAL
+    assert lib.kvrt_attend_tensors_async(None, None, None, None, None, None, 1.0, 0, None) == L.KVRT_EINVAL
     assert lib.kvrt_attend_talker_async(None, 0, 1, slots, None, None, 1.0, None) == L.KVRT_EINVAL
+    assert lib.kvrt_set_prefix_attention_async(None, 0, None) == L.KVRT_EINVAL
+    assert lib.kvrt_slot_info_get(None, 0, None) == L.KVRT_EINVAL
+    assert lib.kvrt_copy_prefix_async(None, 0, 1, 4, 0) == L.KVRT_EINVAL
+    assert lib.kvrt_rollover_async(None, 0, 4, 4, 0) == L.KVRT_EINVAL
+    assert lib.kvrt_bind_stream(None, None) == L.KVRT_EINVAL
 
 
 def test_runtime_refuses_to_start_without_a_gpu():

@@ -280,3 +280,117 @@ def test_bruteforce_and_vectorised_oracles_agree_on_random_tiny_cases():
         a = O.attend(q, k, v, np.array(pos), 0.7, w)
         b = np.asarray(O.attend_bruteforce(q.tolist(), k.tolist(), v.tolist(), pos, 0.7, w))
         assert math.isclose(float(np.abs(a - b).max()), 0.0, abs_tol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# listener prefix-attention mask (gemma4_listener_kernels.cuh:517-518)
+# ---------------------------------------------------------------------------
+PREFIX_GOLD = np.load(GOLDEN / "attention_prefix_small.npz")
+PREFIX_CASES = sorted({k.split(".")[0] for k in PREFIX_GOLD.files})
+
+
+def test_canonical_prefix_mask_matches_reference_known_answer():
+    kat = KATS["canonical_prefix_mask"]
+    m = O.canonical_prefix_mask(kat["length"])
+    assert m.dtype == np.int64 and m.shape == (kat["length"],)
+    assert list(np.flatnonzero(m)) == kat["visible"]
+    # the same rule at other lengths: first and last position only
+    assert list(np.flatnonzero(O.canonical_prefix_mask(7))) == [0, 6]
+
+
+def _prefix_case(name):
+    g = PREFIX_GOLD
+    hq, hkv, d, n_keys, qn, window = (int(x) for x in g[f"{name}.meta"])
+    q = _bits_to_f32(g[f"{name}.q"])
+    k = _bits_to_f32(g[f"{name}.k"])
+    v = _bits_to_f32(g[f"{name}.v"])
+    return q, k, v, g[f"{name}.mask"], np.arange(n_keys - qn, n_keys), window, float(g[f"{name}.scale"][0]), \
+        g[f"{name}.out"]
+
+
+@pytest.mark.parametrize("name", PREFIX_CASES)
+def test_prefix_attend_matches_bruteforce_golden(name):
+    q, k, v, mask, pos, window, scale, want = _prefix_case(name)
+    got = O.attend(q, k, v, pos, scale, window, prefix_attention=mask)
+    np.testing.assert_allclose(got, want, atol=1e-6, rtol=0)
+
+
+def test_prefix_attend_is_attention_over_the_visible_key_subset():
+    """Closed form: masking keys is attention over the keys that remain
+    (torch SDPA in fp64 over the subset, repeat_kv GQA)."""
+    gen = torch.Generator().manual_seed(5)
+    hq, hkv, d, n_keys = 8, 2, 32, 50
+    q = torch.randn(hq, 1, d, generator=gen, dtype=torch.float64)
+    k = torch.randn(hkv, n_keys, d, generator=gen, dtype=torch.float64)
+    v = torch.randn(hkv, n_keys, d, generator=gen, dtype=torch.float64)
+    mask = torch.randint(0, 2, (20,), generator=gen).numpy()
+    keep = [j for j in range(n_keys) if j >= 20 or mask[j]]
+    ref = F.scaled_dot_product_attention(q[None], k[:, keep].repeat_interleave(hq // hkv, 0)[None],
+                                         v[:, keep].repeat_interleave(hq // hkv, 0)[None], scale=0.2)[0]
+    got = O.attend(q.numpy(), k.numpy(), v.numpy(), np.array([n_keys - 1]), 0.2, prefix_attention=mask)
+    np.testing.assert_allclose(got, ref.numpy(), atol=1e-6)
+
+
+def test_prefix_attend_closed_forms():
+    gen = torch.Generator().manual_seed(6)
+    q = torch.randn(4, 1, 16, generator=gen).numpy()
+    k = torch.randn(1, 40, 16, generator=gen).numpy()
+    v = torch.randn(1, 40, 16, generator=gen).numpy()
+    # an all-ones mask changes nothing
+    np.testing.assert_array_equal(O.attend(q, k, v, np.array([39]), 0.3, prefix_attention=np.ones(34, np.int64)),
+                                  O.attend(q, k, v, np.array([39]), 0.3))
+    # one visible key inside the prefix, query at the prefix's last position: o = v[j]
+    one = np.zeros(34, np.int64)
+    one[9] = 1
+    out = O.attend(q, k[:, :34], v[:, :34], np.array([33]), 0.3, prefix_attention=one)
+    np.testing.assert_allclose(out, np.broadcast_to(v[0, 9], out.shape), atol=1e-6)
+    # a zero mask hides the whole prefix: attention over keys P.. only
+    zero = np.zeros(34, np.int64)
+    np.testing.assert_allclose(O.attend(q, k, v, np.array([39]), 0.3, prefix_attention=zero),
+                               O.attend(q, k[:, 34:], v[:, 34:], np.array([39]), 0.3,
+                                        key_positions=np.arange(34, 40)), atol=1e-6)
+    # the canonical mask with the first query after it: keys {0, 33, 34}
+    out = O.attend(q, k[:, :35], v[:, :35], np.array([34]), 0.3, prefix_attention=O.canonical_prefix_mask())
+    sub = [0, 33, 34]
+    np.testing.assert_allclose(out, O.attend(q, k[:, sub], v[:, sub], np.array([34]), 0.3,
+                                             key_positions=np.array(sub)), atol=1e-6)
+    # a key below P is hidden from every query, also one whose window starts before it
+    w_out = O.attend(q, k, v, np.array([39]), 0.3, window=8, prefix_attention=np.zeros(34, np.int64))
+    np.testing.assert_allclose(w_out, O.attend(q, k[:, 34:], v[:, 34:], np.array([39]), 0.3, window=8,
+                                               key_positions=np.arange(34, 40)), atol=1e-6)
+
+
+@pytest.mark.parametrize("slip", ["polarity", "shifted", "inclusive_end", "ignored"])
+def test_planted_prefix_slips_fail_the_golden_vectors(slip):
+    """Plausible mistakes in the prefix term each change a golden output."""
+    failed = 0
+    for name in PREFIX_CASES:
+        q, k, v, mask, pos, window, scale, want = _prefix_case(name)
+        if slip == "polarity":
+            m = 1 - mask
+        elif slip == "shifted":
+            m = np.roll(mask, 1)
+        elif slip == "inclusive_end":  # key P consulted as if masked
+            m = np.concatenate([mask, [0]])
+        else:
+            m = None
+        got = O.attend(q, k, v, pos, scale, window, prefix_attention=m)
+        failed += not np.allclose(got, want, atol=1e-3)
+    assert failed > 0, f"slip {slip} passed every golden case"
+
+
+def test_oracle_cache_carries_the_prefix_mask_through_copies():
+    cache = O.OracleCache([O.OracleLayer(1, 16)], 3)
+    gen = torch.Generator().manual_seed(8)
+    k = torch.randn(1, 40, 16, generator=gen).numpy()
+    v = torch.randn(1, 40, 16, generator=gen).numpy()
+    q = torch.randn(2, 1, 16, generator=gen).numpy()
+    cache.append(0, 0, k, v)
+    cache.set_prefix_attention(0, O.canonical_prefix_mask())
+    cache.copy_prefix(0, 1, 0, 40)
+    cache.copy_prefix_attention(0, 1)
+    np.testing.assert_array_equal(cache.attend(1, 0, q, 0.25), cache.attend(0, 0, q, 0.25))
+    want = O.attend(q, k, v, np.array([39]), 0.25, prefix_attention=O.canonical_prefix_mask())
+    np.testing.assert_allclose(cache.attend(0, 0, q, 0.25), want, atol=0)
+    cache.set_prefix_attention(0, None)
+    np.testing.assert_allclose(cache.attend(0, 0, q, 0.25), O.attend(q, k, v, np.array([39]), 0.25), atol=0)

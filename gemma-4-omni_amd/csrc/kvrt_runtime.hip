@@ -22,6 +22,15 @@
 
 using namespace kvrt;
 
+// Scratch of kvrt_attend_tensors_noalloc_async: the split-K partials, mask
+// records and error flag of one call, laid out as a per-stream workspace of
+// kvrt_attend_tensors_async. Every GPU the library runs on holds its own copy
+// until the process ends. In host code the name is not a device address:
+// each device's copy is looked up once with hipGetSymbolAddress and only that
+// pointer reaches the kernels.
+constexpr size_t kScratchBytes = KVRT_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
 
 struct Layer {
@@ -854,6 +863,117 @@ std::map<std::pair<int, hipStream_t>, TensorWorkspace> g_tensor_ws;
 // Outgrown workspaces: never freed, since a captured graph may still use them.
 std::vector<float *> g_tensor_retired;
 
+// One context-free tensor attention call, validated and laid out: the decode
+// arguments (workspace pointers unset), the prefix masks to pack, and the
+// workspace bytes it needs.
+struct TensorCall {
+    DecodeArgs a{};
+    PrefixPackArgs pk{};
+    bool masked = false;
+    bool mfma = false;
+    int D = 0, rows = 0;
+    size_t acc_elems = 0;
+    size_t bytes = 0;
+};
+
+int tensor_call_setup(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v, const int32_t *device_lengths,
+                      const kvrt_tensor *prefix_attention, const kvrt_tensor *out, float scale, int32_t window,
+                      int target, TensorCall &tc) {
+    if (!device_lengths || window < 0 || !std::isfinite(scale)) return KVRT_EINVAL;
+    if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
+        return KVRT_EINVAL;
+    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    for (int i = 0; i < 4; ++i)
+        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i] || out->dims[i] != q->dims[i])
+            return KVRT_EINVAL;
+    const int64_t n = q->dims[0], hq = q->dims[1], qn = q->dims[2], D = q->dims[3];
+    const int64_t hkv = k->dims[1], lmax = k->dims[2];
+    if (n <= 0 || n > kMaxItems || k->dims[0] != n || k->dims[3] != D || hkv <= 0 || hkv > 64 || hq % hkv != 0 ||
+        qn <= 0 || qn > 64)
+        return KVRT_EINVAL;
+    if (D != 64 && D != 128 && D != 256 && D != 512) return KVRT_EINVAL;
+    if (k->strides[2] != D) return KVRT_EINVAL;
+    const int group = (int)(hq / hkv);
+    const int rows = group * (int)qn;
+    if (rows_tile(rows) == 0) return KVRT_EINVAL;
+    if (prefix_attention != nullptr) {
+        const int rc = prefix_tensor(prefix_attention, (int)n, tc.pk);
+        if (rc != KVRT_OK) return rc;
+        tc.masked = tc.pk.plen > 0;
+    }
+    DecodeArgs &a = tc.a;
+    a.kv.k = k->data;
+    a.kv.v = v->data;
+    a.kv.layout = KVRT_LAYOUT_CONTIG;
+    a.kv.kv_heads = (int)hkv;
+    a.kv.rows = (int)lmax;
+    a.kv.slot_stride = k->strides[0];
+    a.kv.head_stride = k->strides[1];
+    a.kv.row_stride = k->strides[2];
+    a.len.lens = const_cast<int32_t *>(device_lengths);
+    a.len.stride = 1;
+    a.len.offset = 0;
+    a.q = static_cast<const uint16_t *>(q->data);
+    a.out = static_cast<uint16_t *>(out->data);
+    a.n_items = (int)n;
+    a.group = group;
+    a.qn = (int)qn;
+    a.window = window;
+    const int R = rows_tile(rows);
+    const int64_t keys = window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax;
+    tc.mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D,
+                              (keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket);
+    a.n_split = choose_splits(target, (int)n, (int)hkv, keys,
+                              tc.mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
+    a.n_parts = (tc.mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)i;
+    for (int i = 0; i < n; ++i) a.slots[i] = i;
+    const int Rw = tc.mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial
+    tc.D = (int)D;
+    tc.rows = rows;
+    tc.acc_elems = (size_t)n * hkv * a.n_split * Rw * D;
+    tc.bytes = (kTensorWsHead + kTensorWsMasks + tc.acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * Rw * 8;
+    return KVRT_OK;
+}
+
+// Device address of the scratch array on device dev (the current device),
+// looked up on the device's first call and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_pointer(int dev, float **out) {
+    if (dev < 0 || dev >= kMaxDevices) return KVRT_EDEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return KVRT_EDEVICE;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<float *>(g_scratch_ptr[dev]);
+    return KVRT_OK;
+}
+
+// Enqueue a set-up call on workspace ws (at least tc.bytes, laid out as the
+// per-stream workspaces: error flag, masks, partials).
+int tensor_call_launch(TensorCall &tc, float *ws, hipStream_t st) {
+    DecodeArgs &a = tc.a;
+    a.err = reinterpret_cast<int32_t *>(ws);
+    a.part_acc = ws + kTensorWsHead + kTensorWsMasks;
+    a.part_ml = reinterpret_cast<float2 *>(a.part_acc + ((tc.acc_elems + 63) / 64) * 64);
+    if (tc.masked) {
+        tc.pk.dst = reinterpret_cast<PrefixMask *>(ws + kTensorWsHead);
+        for (int i = 0; i < a.n_items; ++i) tc.pk.index[i] = i;
+        if (launch_prefix_pack(tc.pk, st) != hipSuccess) return KVRT_EDEVICE;
+        a.pmask = tc.pk.dst;
+    }
+    if ((tc.mfma ? launch_decode_mfma(a, tc.D, KVRT_BF16, tc.rows, st) : launch_decode(a, tc.D, KVRT_BF16, tc.rows, st)) !=
+        hipSuccess)
+        return KVRT_EDEVICE;
+    return KVRT_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1628,91 +1748,54 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
 int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
                               const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
                               const kvrt_tensor *out, float scale, int32_t window, void *stream) {
-    if (!device_lengths || window < 0 || !std::isfinite(scale)) return KVRT_EINVAL;
-    if (!tensor_ok(q, KVRT_BF16, 4) || !tensor_ok(out, KVRT_BF16, 4) || !is_contiguous(q) || !is_contiguous(out))
-        return KVRT_EINVAL;
-    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
-    for (int i = 0; i < 4; ++i)
-        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i] || out->dims[i] != q->dims[i])
-            return KVRT_EINVAL;
-    const int64_t n = q->dims[0], hq = q->dims[1], qn = q->dims[2], D = q->dims[3];
-    const int64_t hkv = k->dims[1], lmax = k->dims[2];
-    if (n <= 0 || n > kMaxItems || k->dims[0] != n || k->dims[3] != D || hkv <= 0 || hkv > 64 || hq % hkv != 0 || qn <= 0 ||
-        qn > 64)
-        return KVRT_EINVAL;
-    if (D != 64 && D != 128 && D != 256 && D != 512) return KVRT_EINVAL;
-    if (k->strides[2] != D) return KVRT_EINVAL;
-    const int group = (int)(hq / hkv);
-    const int rows = group * (int)qn;
-    if (rows_tile(rows) == 0) return KVRT_EINVAL;
-    PrefixPackArgs pk{};
-    if (prefix_attention != nullptr) {
-        const int rc = prefix_tensor(prefix_attention, (int)n, pk);
-        if (rc != KVRT_OK) return rc;
-    }
-    DecodeArgs a{};
-    a.kv.k = k->data;
-    a.kv.v = v->data;
-    a.kv.layout = KVRT_LAYOUT_CONTIG;
-    a.kv.kv_heads = (int)hkv;
-    a.kv.rows = (int)lmax;
-    a.kv.slot_stride = k->strides[0];
-    a.kv.head_stride = k->strides[1];
-    a.kv.row_stride = k->strides[2];
-    a.len.lens = const_cast<int32_t *>(device_lengths);
-    a.len.stride = 1;
-    a.len.offset = 0;
-    a.q = static_cast<const uint16_t *>(q->data);
-    a.out = static_cast<uint16_t *>(out->data);
-    a.n_items = (int)n;
-    a.group = group;
-    a.qn = (int)qn;
-    a.window = window;
-    const int R = rows_tile(rows);
-    const int64_t keys = window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax;
-    const bool mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D,
-                                      (keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket);
-    a.n_split = choose_splits(target_wgs(kvrt_config{}), (int)n, (int)hkv, keys,
-                              mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
-    a.n_parts = (mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;
-    a.scale_log2 = scale * 1.4426950408889634f;
-    for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)i;
-    for (int i = 0; i < n; ++i) a.slots[i] = i;
-    const int Rw = mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial
-    const size_t acc_elems = (size_t)n * hkv * a.n_split * Rw * D;
-    const size_t bytes = (kTensorWsHead + kTensorWsMasks + acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * Rw * 8;
+    TensorCall tc;
+    int rc = tensor_call_setup(q, k, v, device_lengths, prefix_attention, out, scale, window, target_wgs(kvrt_config{}),
+                               tc);
+    if (rc != KVRT_OK) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     std::lock_guard<std::mutex> lock(g_tensor_mu);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
     TensorWorkspace &ws = g_tensor_ws[{dev, st}];
-    if (ws.bytes < bytes) {
+    if (ws.bytes < tc.bytes) {
         // no allocation inside a stream capture: an eager call of the largest
         // shape sizes the workspace first
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess) return KVRT_EDEVICE;
         if (cs != hipStreamCaptureStatusNone) return KVRT_ESTATE;
         float *fresh = nullptr;
-        const size_t want = std::max(bytes, (size_t)1 << 20);
+        const size_t want = std::max(tc.bytes, (size_t)1 << 20);
         if (hipMalloc(&fresh, want) != hipSuccess) return KVRT_EDEVICE;
         if (launch_zero(fresh, kTensorWsHead * 4, st) != hipSuccess) return KVRT_EDEVICE;
         if (ws.ptr) g_tensor_retired.push_back(ws.ptr);
         ws.ptr = fresh;
         ws.bytes = want;
     }
-    a.err = reinterpret_cast<int32_t *>(ws.ptr);
-    a.part_acc = ws.ptr + kTensorWsHead + kTensorWsMasks;
-    a.part_ml = reinterpret_cast<float2 *>(a.part_acc + ((acc_elems + 63) / 64) * 64);
-    if (prefix_attention != nullptr && pk.plen > 0) {
-        pk.dst = reinterpret_cast<PrefixMask *>(ws.ptr + kTensorWsHead);
-        for (int i = 0; i < n; ++i) pk.index[i] = i;
-        if (launch_prefix_pack(pk, st) != hipSuccess) return KVRT_EDEVICE;
-        a.pmask = pk.dst;
+    return tensor_call_launch(tc, ws.ptr, st);
+}
+
+int kvrt_attend_tensors_noalloc_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
+                                      const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
+                                      const kvrt_tensor *out, float scale, int32_t window, void *stream) {
+    // the split count of kvrt_attend_tensors_async, halved until the partials
+    // fit the scratch (one workgroup per (item, kv head) at the least)
+    int target = target_wgs(kvrt_config{});
+    TensorCall tc;
+    int rc = tensor_call_setup(q, k, v, device_lengths, prefix_attention, out, scale, window, target, tc);
+    if (rc != KVRT_OK) return rc;
+    while (tc.bytes > kScratchBytes && target > 1) {
+        target /= 2;
+        tc = TensorCall{};
+        rc = tensor_call_setup(q, k, v, device_lengths, prefix_attention, out, scale, window, target, tc);
+        if (rc != KVRT_OK) return rc;
     }
-    if ((mfma ? launch_decode_mfma(a, (int)D, KVRT_BF16, rows, st) : launch_decode(a, (int)D, KVRT_BF16, rows, st)) !=
-        hipSuccess)
-        return KVRT_EDEVICE;
-    return KVRT_OK;
+    if (tc.bytes > kScratchBytes) return KVRT_EINVAL;  // beyond KVRT_NOALLOC_SCRATCH_BYTES
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KVRT_EDEVICE;
+    float *ws = nullptr;
+    rc = scratch_pointer(dev, &ws);
+    if (rc != KVRT_OK) return rc;
+    return tensor_call_launch(tc, ws, static_cast<hipStream_t>(stream));
 }
 
 int kvrt_tensors_status(void *stream) {

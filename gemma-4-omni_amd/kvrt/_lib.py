@@ -16,6 +16,7 @@ KVRT_MAX_ROLLOVER_ROWS = 128
 KVRT_MAX_ITEMS = 64
 KVRT_MAX_PREFIX_MASK = 512
 KVRT_ANY_GENERATION = 0
+KVRT_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 KVRT_OK = 0
 KVRT_EINVAL = -1
@@ -173,6 +174,7 @@ SIGNATURES = [
     ("kvrt_attend_talker_async", c_int32,
      [c_void_p, c_int32, c_int32, _I32P, _T, _T, c_float, POINTER(KvrtTalkerMask)]),
     ("kvrt_attend_tensors_async", c_int32, [_T, _T, _T, c_void_p, _T, _T, c_float, c_int32, c_void_p]),
+    ("kvrt_attend_tensors_noalloc_async", c_int32, [_T, _T, _T, c_void_p, _T, _T, c_float, c_int32, c_void_p]),
     ("kvrt_tensors_status", c_int32, [c_void_p]),
     ("kvrt_copy_rows_async", c_int32, [_T, _T, c_int64, c_void_p]),
     ("kvrt_session_state", c_int32, [c_void_p, c_int32, c_int32, _I32P]),

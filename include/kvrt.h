@@ -497,6 +497,25 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
                               const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
                               const kvrt_tensor *out, float scale, int32_t window, void *hip_stream);
 
+/* The same attention with no allocation: the split-K partials go to a
+ * scratch array the library holds on each GPU (KVRT_NOALLOC_SCRATCH_BYTES, set
+ * up on the device's first call) instead of an allocated workspace, and the
+ * call makes no hipMalloc / hipFree or allocating library call. Same
+ * arguments, checks and results as kvrt_attend_tensors_async, except: a call
+ * whose partials would not fit uses fewer split-K workgroups (results then
+ * differ from kvrt_attend_tensors_async in fp32 rounding only), and one that
+ * does not fit even with one workgroup per (item, kv head) returns
+ * KVRT_EINVAL; lengths beyond Lmax are clamped without a report. Every call on
+ * a GPU shares that GPU's scratch: calls that overlap on one GPU (two
+ * streams, or two host threads) race, so callers serialise them.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+#define KVRT_NOALLOC_SCRATCH_BYTES (16u << 20)
+int kvrt_attend_tensors_noalloc_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
+                                      const int32_t *device_lengths, const kvrt_tensor *prefix_attention,
+                                      const kvrt_tensor *out, float scale, int32_t window, void *hip_stream);
+
 /* Synchronise hip_stream, then report and clear the error flag of the
  * stream's kvrt_attend_tensors_async workspace: KVRT_OK, KVRT_EFAULT (a
  * length beyond its K/V rows was clamped) or KVRT_EDEVICE. KVRT_OK when the

@@ -46,14 +46,19 @@ __device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int hea
 }
 
 // Prefix-attention mask of a slot as a wave holds it: its length plen (0: no
-// mask) and, in every lane, mask word (lane & 15). The record is read only
-// when the launch carries masks, so launches without them load nothing.
+// mask; wave-uniform, in an SGPR) and, in every lane, mask word (lane & 15).
+// The record is read only when the launch carries masks, so launches without
+// them load nothing. Both values are waited for here, so callers issue this
+// next to their length load (one memory round trip for both) and before any
+// LDS DMA: the compiler does not count inline-assembly DMAs, and a wait it
+// placed for these loads inside a DMA-pipelined loop would drain the ring.
 __device__ __forceinline__ void load_prefix(const PrefixMask *pm, int slot, int lane, int &plen, uint32_t &pw) {
     plen = 0;
     pw = 0xffffffffu;
     if (pm != nullptr) {
-        plen = pm[slot].len;
+        plen = __builtin_amdgcn_readfirstlane(pm[slot].len);
         pw = pm[slot].bits[lane & (kPrefixWords - 1)];
+        asm volatile("" ::"v"(pw));  // the word is in its register from here on
     }
 }
 // Mask bit of key position key (0 <= key < KVRT_MAX_PREFIX_MASK): the word
@@ -448,6 +453,9 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    int plen = 0;          // prefix-attention mask (listener slots); the talker has its own masks
+    uint32_t pw = ~0u;
+    if constexpr (!TALK) load_prefix(a.pmask, slot, lane, plen, pw);
     const int Qn = a.qn;
     const int rows = a.group * Qn;
     const bool fused = (KDT == KVRT_BF16) && a.k_new != nullptr;
@@ -466,9 +474,6 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     chunk = (chunk + KPW - 1) / KPW * KPW;
     const int ws = kstart + split * chunk;
     const int we = min(kend, ws + chunk);
-    int plen = 0;          // prefix-attention mask (listener slots); the talker has its own masks
-    uint32_t pw = ~0u;
-    if constexpr (!TALK) load_prefix(a.pmask, slot, lane, plen, pw);
 
     if constexpr (KDT == KVRT_BF16) {
         // Fused append: workgroup 0 of every (item, kv head) stores the new
@@ -937,6 +942,13 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    // Prefix-attention mask of the slot. PAGED rows at D 512 use every
+    // register: launches with masks run that shape on decode_kernel instead
+    // (launch_decode_mfma refuses them), so this variant has no mask code.
+    constexpr bool PMASK = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
+    int plen = 0;
+    uint32_t pw = ~0u;
+    if constexpr (PMASK) load_prefix(a.pmask, slot, lane, plen, pw);
     const int Qn = a.qn;
     const int rows = a.group * Qn;
     const bool fused = !I8 && a.k_new != nullptr;  // int8 rows are quantised by the append kernel
@@ -952,13 +964,6 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     chunk = (chunk + T - 1) / T * T;
     const int ws = kstart + split * chunk;
     const int we = min(kend, ws + chunk);
-    // Prefix-attention mask of the slot. PAGED rows at D 512 use every
-    // register: launches with masks run that shape on decode_kernel instead
-    // (launch_decode_mfma refuses them), so this variant has no mask code.
-    constexpr bool PMASK = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
-    int plen = 0;
-    uint32_t pw = ~0u;
-    if constexpr (PMASK) load_prefix(a.pmask, slot, lane, plen, pw);
 
     // Fused append: workgroup 0 of every (item, kv head) stores the new rows;
     // no workgroup of this launch reads them from the cache.

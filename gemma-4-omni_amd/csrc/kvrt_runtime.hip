@@ -1063,6 +1063,110 @@ int kvrt_bind_stream(kvrt_ctx *c, void *stream) {
     return KVRT_OK;
 }
 
+int kvrt_grow_slots(kvrt_ctx *c, int32_t n_slots, const kvrt_storage *storage) {
+    if (!c) return KVRT_EINVAL;
+    if (c->poisoned) return KVRT_EPOISONED;
+    const int old_n = c->cfg.n_slots;
+    if (n_slots <= old_n) return n_slots > 0 ? KVRT_OK : KVRT_EINVAL;
+    if (n_slots > (1 << 20)) return KVRT_EINVAL;
+    bool owns = true, slot_major = false;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        if (c->layers[l].owner != l || c->layers[l].spec.layout == KVRT_LAYOUT_PAGED) continue;
+        slot_major = true;
+        owns = owns && c->layers[l].owned;
+    }
+    // caller-owned contexts pass the new storage; library-owned ones must not
+    if (slot_major && owns == (storage != nullptr)) return KVRT_EINVAL;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess) return poison(c);
+    if (cs != hipStreamCaptureStatusNone) return KVRT_ESTATE;
+    kvrt_config nc = c->cfg;
+    nc.n_slots = n_slots;
+    // the new storage of every slot-major layer, checked before anything changes
+    struct Grown { int layer; void *k, *v; uint64_t bytes, old_bytes; };
+    std::vector<Grown> grown;
+    for (int l = 0; l < c->cfg.n_layers; ++l) {
+        Layer &L = c->layers[l];
+        if (L.owner != l || L.spec.layout == KVRT_LAYOUT_PAGED) continue;
+        uint64_t kvb = 0, scb = 0;
+        if (kvrt_layer_storage_bytes(&nc, &L.spec, &kvb, &scb) != KVRT_OK) return KVRT_EINVAL;
+        Grown g{l, nullptr, nullptr, kvb, L.kv_bytes};
+        if (storage) {
+            g.k = storage[l].k;
+            g.v = storage[l].v;
+            if (!g.k || !g.v || ((reinterpret_cast<uintptr_t>(g.k) | reinterpret_cast<uintptr_t>(g.v)) & 15u)) {
+                return KVRT_EINVAL;
+            }
+        }
+        grown.push_back(g);
+    }
+    // nothing of the context may run while its buffers move
+    if (hipSetDevice(c->device) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    c->dirty = false;
+    for (Grown &g : grown) {
+        if (!storage && (hipMalloc(&g.k, g.bytes) != hipSuccess || hipMalloc(&g.v, g.bytes) != hipSuccess))
+            return poison(c);
+        const Layer &L = c->layers[g.layer];
+        // slot-major rows: the old slots are the first old_bytes, the new ones start zeroed
+        if (hipMemcpyAsync(g.k, L.k, g.old_bytes, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
+            hipMemcpyAsync(g.v, L.v, g.old_bytes, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
+            return poison(c);
+        const uint64_t tail = g.bytes - g.old_bytes;
+        if (launch_zero(static_cast<uint8_t *>(g.k) + g.old_bytes, tail, c->stream) != hipSuccess ||
+            launch_zero(static_cast<uint8_t *>(g.v) + g.old_bytes, tail, c->stream) != hipSuccess)
+            return poison(c);
+    }
+    // lengths [slot, layer], page table [slot, page] and masks [slot]: slot-major, new rows appended
+    int32_t *d_len = nullptr, *d_pt = nullptr;
+    PrefixMask *d_prefix = nullptr;
+    const size_t len_old = c->len.size() * 4, len_new = (size_t)n_slots * c->cfg.n_layers * 4;
+    const size_t len_alloc = ((len_new + 15) / 16) * 16;
+    if (hipMalloc((void **)&d_len, len_alloc) != hipSuccess || launch_zero(d_len, len_alloc, c->stream) != hipSuccess ||
+        hipMemcpyAsync(d_len, c->d_len, len_old, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
+        return poison(c);
+    if (hipMalloc((void **)&d_prefix, (size_t)n_slots * sizeof(PrefixMask)) != hipSuccess ||
+        launch_zero(d_prefix, (size_t)n_slots * sizeof(PrefixMask), c->stream) != hipSuccess ||
+        hipMemcpyAsync(d_prefix, c->d_prefix, (size_t)old_n * sizeof(PrefixMask), hipMemcpyDeviceToDevice,
+                       c->stream) != hipSuccess)
+        return poison(c);
+    if (c->paged) {
+        std::vector<int32_t> pt = c->pt;
+        pt.resize((size_t)n_slots * c->pt_stride, -1);
+        const size_t pt_bytes = ((pt.size() * 4 + 15) / 16) * 16;
+        if (hipMalloc((void **)&d_pt, pt_bytes) != hipSuccess ||
+            hipMemcpy(d_pt, pt.data(), pt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return poison(c);
+        c->pt = std::move(pt);
+        c->first_live.resize(n_slots, 0);
+    }
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return poison(c);
+    for (Grown &g : grown) {
+        Layer &L = c->layers[g.layer];
+        if (L.owned) {
+            (void)hipFree(L.k);
+            (void)hipFree(L.v);
+        }
+        L.k = g.k;
+        L.v = g.v;
+        L.kv_bytes = g.bytes;
+    }
+    (void)hipFree(c->d_len);
+    (void)hipFree(c->d_prefix);
+    c->d_len = d_len;
+    c->d_prefix = d_prefix;
+    if (c->paged) {
+        (void)hipFree(c->d_pt);
+        c->d_pt = d_pt;
+    }
+    c->len.resize((size_t)n_slots * c->cfg.n_layers, 0);
+    c->slot.resize(n_slots, SlotState{});
+    for (int i = old_n; i < n_slots; ++i) renew_generation(c, i);
+    c->cfg.n_slots = n_slots;
+    if (upload_desc(c) != KVRT_OK) return poison(c);
+    if (ensure_workspace(c, workspace_bound(c)) != KVRT_OK) return poison(c);
+    return hipDeviceSynchronize() == hipSuccess ? KVRT_OK : poison(c);
+}
+
 int kvrt_layer_storage(kvrt_ctx *c, int32_t layer, kvrt_storage *out) {
     if (!c || !out || !valid_layer(c, layer)) return KVRT_EINVAL;
     const Layer &L = c->layers[c->layers[layer].owner];

@@ -154,6 +154,7 @@ SIGNATURES = [
      [POINTER(KvrtConfig), POINTER(KvrtLayerSpec), POINTER(c_uint64), POINTER(c_uint64)]),
     ("kvrt_destroy", c_int32, [c_void_p]),
     ("kvrt_bind_stream", c_int32, [c_void_p, c_void_p]),
+    ("kvrt_grow_slots", c_int32, [c_void_p, c_int32, POINTER(KvrtStorage)]),
     ("kvrt_layer_storage", c_int32, [c_void_p, c_int32, POINTER(KvrtStorage)]),
     ("kvrt_import_async", c_int32, [c_void_p, c_int32, c_int32, _T, _T, c_int32]),
     ("kvrt_append_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T]),

@@ -221,40 +221,38 @@ class KVRuntime:
         self._store: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None] | None] = []
         with torch.cuda.device(self.device):
             for i, spec in enumerate(self.layers):
-                if spec.shared_src >= 0:
-                    self._store.append(None)
-                    continue
-                kvb, scb = ctypes.c_uint64(), ctypes.c_uint64()
-                _check(self.lib.kvrt_layer_storage_bytes(ctypes.byref(cfg), ctypes.byref(specs[i]),
-                                                         ctypes.byref(kvb), ctypes.byref(scb)),
-                       "kvrt_layer_storage_bytes")
-                shape = self._storage_shape(spec)
-                dt = torch.int8 if spec.dtype == "int8" else torch.bfloat16
-                es = 1 if dt == torch.int8 else 2
-                pad = kvb.value // es
-                k = torch.zeros(pad, dtype=dt, device=self.device)
-                v = torch.zeros(pad, dtype=dt, device=self.device)
-                n_el = math.prod(shape)
-                kv_views = (k[:n_el].view(shape), v[:n_el].view(shape))
-                ks = vs = None
-                storage[i].k = k.data_ptr()
-                storage[i].v = v.data_ptr()
-                if spec.dtype == "int8":
-                    ks_flat = torch.zeros(scb.value // 4, dtype=torch.float32, device=self.device)
-                    vs_flat = torch.zeros(scb.value // 4, dtype=torch.float32, device=self.device)
-                    n_sc = math.prod(shape[:-1])
-                    ks, vs = ks_flat[:n_sc].view(shape[:-1]), vs_flat[:n_sc].view(shape[:-1])
-                    storage[i].k_scale = ks_flat.data_ptr()
-                    storage[i].v_scale = vs_flat.data_ptr()
-                    self._keep = getattr(self, "_keep", []) + [ks_flat, vs_flat]
-                self._keep = getattr(self, "_keep", []) + [k, v]
-                self._store.append((kv_views[0], kv_views[1], ks, vs))
+                self._store.append(None if spec.shared_src >= 0 else self._alloc_layer(i, storage[i], zero=True))
             torch.cuda.synchronize(self.device)
             _check(self.lib.kvrt_create_with_storage(ctypes.byref(cfg), specs, storage, ctypes.byref(self._ctx)),
                    "kvrt_create_with_storage")
         self._free_slots = list(range(self.n_slots - 1, -1, -1))
 
     # ---- helpers -------------------------------------------------------------
+    def _alloc_layer(self, i: int, entry: L.KvrtStorage, zero: bool):
+        """Torch storage of layer i at the current slot count: typed views, with
+        the base pointers written to ``entry`` (the views keep the buffers alive)."""
+        spec = self.layers[i]
+        kvb, scb = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(self.lib.kvrt_layer_storage_bytes(ctypes.byref(self._cfg), ctypes.byref(self._specs[i]),
+                                                 ctypes.byref(kvb), ctypes.byref(scb)),
+               "kvrt_layer_storage_bytes")
+        shape = self._storage_shape(spec)
+        dt = torch.int8 if spec.dtype == "int8" else torch.bfloat16
+        es = 1 if dt == torch.int8 else 2
+        make = torch.zeros if zero else torch.empty
+        k = make(kvb.value // es, dtype=dt, device=self.device)
+        v = make(kvb.value // es, dtype=dt, device=self.device)
+        n_el = math.prod(shape)
+        entry.k, entry.v = k.data_ptr(), v.data_ptr()
+        ks = vs = None
+        if spec.dtype == "int8":
+            ks_flat = make(scb.value // 4, dtype=torch.float32, device=self.device)
+            vs_flat = make(scb.value // 4, dtype=torch.float32, device=self.device)
+            n_sc = math.prod(shape[:-1])
+            ks, vs = ks_flat[:n_sc].view(shape[:-1]), vs_flat[:n_sc].view(shape[:-1])
+            entry.k_scale, entry.v_scale = ks_flat.data_ptr(), vs_flat.data_ptr()
+        return k[:n_el].view(shape), v[:n_el].view(shape), ks, vs
+
     def _storage_shape(self, spec: LayerSpec) -> tuple[int, ...]:
         if spec.layout == "contig":
             return (self.n_slots, spec.kv_heads, self.capacity, spec.head_dim)
@@ -291,6 +289,37 @@ class KVRuntime:
         return st
 
     # ---- slots -----------------------------------------------------------------
+    def ensure_capacity(self, n_slots: int) -> int:
+        """Grow to at least ``n_slots`` slots; returns the slot count. Existing
+        slots keep their rows, lengths, masks and generations; the new ones are
+        empty and join the free list. Waits for the context's work; graphs
+        captured earlier must be captured again. Mirrors
+        NativeGemmaListenerMicrobatch.ensure_capacity
+        (duplex_kernel/native_listener_microbatch.py:1217-1268)."""
+        self._own()
+        n = int(n_slots)
+        if n <= self.n_slots:
+            return self.n_slots
+        old = self.n_slots
+        self.n_slots = n
+        self._cfg.n_slots = n
+        storage = (L.KvrtStorage * len(self.layers))()
+        fresh = {}
+        try:
+            with torch.cuda.device(self.device):
+                for i, spec in enumerate(self.layers):
+                    if spec.shared_src < 0 and spec.layout != "paged":
+                        fresh[i] = self._alloc_layer(i, storage[i], zero=False)  # the library fills them
+                _check(self.lib.kvrt_grow_slots(self._ctx, n, storage if fresh else None), "kvrt_grow_slots")
+        except Exception:
+            self.n_slots = old
+            self._cfg.n_slots = old
+            raise
+        for i, views in fresh.items():
+            self._store[i] = views  # the old buffers are released with their views
+        self._free_slots = sorted(set(self._free_slots) | set(range(old, n)), reverse=True)
+        return n
+
     def acquire_slot(self) -> int:
         """Take the lowest free slot (session/stream id); raise when none is left."""
         if not self._free_slots:

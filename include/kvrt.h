@@ -220,6 +220,20 @@ int kvrt_destroy(kvrt_ctx *ctx);
  * (gemma4_listener_microbatch_impl.inc:445-473: a second stream is refused
  * with -6; gemma4_listener.cu:2053). */
 int kvrt_bind_stream(kvrt_ctx *ctx, void *hip_stream);
+/* Grow the context to n_slots slots (no-op when it already has as many):
+ * every slot-major layer (CONTIG / RING) moves to storage for n_slots slots,
+ * the existing slots' rows, lengths, pages, masks and generations unchanged
+ * and the new slots empty (zero rows, new generations); PAGED pools keep
+ * their pages. A context created with kvrt_create allocates the new storage
+ * itself (storage = NULL); one created with kvrt_create_with_storage passes
+ * it (storage[l] for every layer l, sized by kvrt_layer_storage_bytes at the
+ * new slot count; PAGED and shared entries ignored) and may free its old
+ * storage once this returns. Synchronous: waits for the bound stream first.
+ * KVRT_ESTATE inside a stream capture; graphs captured before the call use
+ * the old buffers and must be captured again.
+ * Replaces gemma4_listener_batch_ensure_capacity (bound at
+ * duplex_kernel/native_listener_microbatch.py:1217-1268). */
+int kvrt_grow_slots(kvrt_ctx *ctx, int32_t n_slots, const kvrt_storage *storage);
 /* Device pointers of a layer's storage (shared layers report their source). */
 int kvrt_layer_storage(kvrt_ctx *ctx, int32_t layer, kvrt_storage *out);
 

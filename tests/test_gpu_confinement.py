@@ -150,3 +150,91 @@ def test_full_attention_paged_decode_refuses_evicted_pages():
     with pytest.raises(KVRTError):
         rt.append_attend(0, q, k, k, [0], 0.1)
     assert rt.seq_length(0) == 100 and rt.health() == 0
+
+
+def test_slot_growth_keeps_every_slot_and_adds_empty_ones():
+    """ensure_capacity / kvrt_grow_slots (gemma4_listener_batch_ensure_capacity,
+    native_listener_microbatch.py:1217-1268): rows, lengths, masks, pages and
+    generations of the existing slots survive; the new slots are empty with
+    new generations and take sessions like the others."""
+    from kvrt import KVRuntime, LayerSpec
+    from oracle import kv_oracle as O
+    from tests.helpers import to_np
+
+    gen = torch.Generator().manual_seed(6)
+    specs = [LayerSpec(kv_heads=2, head_dim=128), LayerSpec(kv_heads=1, head_dim=256, layout="ring", window=64,
+                                                             ring_rows=65),
+             LayerSpec(kv_heads=2, head_dim=128, layout="paged"), LayerSpec(kv_heads=2, head_dim=128, shared_src=0)]
+    rt = KVRuntime(specs, 2, 400, max_q=2, block_size=16, pool_pages=100, device="cuda")
+    orc = O.OracleCache([O.OracleLayer(2, 128), O.OracleLayer(1, 256, 64), O.OracleLayer(2, 128)], 6)
+    mask = O.canonical_prefix_mask()
+    for slot, n in ((0, 300), (1, 90)):
+        for layer, s in enumerate(specs[:3]):
+            k, v = randn_bf16(gen, (1, s.kv_heads, n, s.head_dim)), randn_bf16(gen, (1, s.kv_heads, n, s.head_dim))
+            rt.import_(slot, layer, k.cuda(), v.cuda())
+            orc.append(slot, layer, to_np(k[0]), to_np(v[0]))
+    rt.set_prefix_attention(1, torch.from_numpy(mask).cuda())
+    orc.set_prefix_attention(1, mask)
+    before = {s: rt.slot_info(s) for s in (0, 1)}
+    rows = {(s, l): rt.gather(l, [s], mask_dtype=None)[:2] for s in (0, 1) for l in range(3)}
+    torch.cuda.synchronize()
+    assert rt.ensure_capacity(5) == 5 and rt.ensure_capacity(3) == 5
+    assert {s: rt.slot_info(s) for s in (0, 1)} == before
+    for (s, l), (k, v) in rows.items():
+        k2, v2, _ = rt.gather(l, [s], mask_dtype=None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(k2), bits(k))
+        np.testing.assert_array_equal(bits(v2), bits(v))
+    gens = {rt.slot_generation(s) for s in range(5)}
+    assert len(gens) == 5
+    for s in (2, 3, 4):
+        assert rt.slot_info(s)["max_len"] == 0 and rt.slot_info(s)["prefix_len"] == 0
+        assert float(rt.storage(0)[0][s].abs().max()) == 0.0
+    for layer, s in enumerate(specs[:3]):
+        k, v = randn_bf16(gen, (1, s.kv_heads, 150, s.head_dim)), randn_bf16(gen, (1, s.kv_heads, 150, s.head_dim))
+        rt.import_(4, layer, k.cuda(), v.cuda())
+        orc.append(4, layer, to_np(k[0]), to_np(v[0]))
+    worst = 0.0
+    for layer, s in enumerate(specs):
+        hq = 4 if s.head_dim == 128 else 8
+        q = randn_bf16(gen, (3, hq, 2, s.head_dim), 1.0 / s.head_dim ** 0.5)
+        out = rt.attend(layer, q.cuda(), [0, 1, 4], 1.0)
+        torch.cuda.synchronize()
+        for i, slot in enumerate((0, 1, 4)):
+            ref = orc.attend(slot, min(layer, 2) if layer < 3 else 0, to_np(q[i]), 1.0)
+            worst = max(worst, float(np.abs(to_np(out[i]) - ref).max()))
+    assert worst <= 1e-2
+    assert rt.health() == 0
+
+
+def test_library_owned_context_grows_through_the_c_abi():
+    from kvrt import _lib as L
+    from kvrt.runtime import current_stream_handle, tensor_desc
+
+    lib = L.load()
+    gen = torch.Generator().manual_seed(8)
+    cfg = L.KvrtConfig()
+    cfg.struct_size = ctypes.sizeof(L.KvrtConfig)
+    cfg.n_layers, cfg.n_slots, cfg.capacity, cfg.block_size, cfg.pool_pages, cfg.max_q = 1, 2, 256, 16, 0, 1
+    spec = L.KvrtLayerSpec(L.LAYOUT_CONTIG, L.DT_BF16, 2, 128, 0, 0, -1, 0)
+    ctx = ctypes.c_void_p()
+    assert lib.kvrt_create(ctypes.byref(cfg), ctypes.byref(spec), ctypes.byref(ctx)) == 0
+    try:
+        assert lib.kvrt_bind_stream(ctx, ctypes.c_void_p(current_stream_handle(torch.device("cuda")))) == 0
+        k = randn_bf16(gen, (1, 2, 200, 128)).cuda()
+        kd = tensor_desc(k)
+        assert lib.kvrt_import_async(ctx, 1, 0, ctypes.byref(kd), ctypes.byref(kd), 0) == 0
+        st = (L.KvrtStorage * 1)()
+        assert lib.kvrt_grow_slots(ctx, 4, st) == L.KVRT_EINVAL  # the context owns its storage
+        assert lib.kvrt_grow_slots(ctx, 4, None) == 0
+        out = torch.empty((1, 2, 200, 128), dtype=torch.bfloat16, device="cuda")
+        od = tensor_desc(out)
+        slots = (ctypes.c_int32 * 1)(1)
+        assert lib.kvrt_gather_async(ctx, 0, 1, slots, None, ctypes.byref(od), ctypes.byref(od), None) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(out), bits(k))
+        length = ctypes.c_int32()
+        assert lib.kvrt_session_state(ctx, 3, 0, ctypes.byref(length)) == 0 and length.value == 0
+        assert lib.kvrt_health(ctx) == 0
+    finally:
+        lib.kvrt_destroy(ctx)

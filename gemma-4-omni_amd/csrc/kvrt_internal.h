@@ -244,6 +244,7 @@ struct PrefillArgs {
     int32_t qn;             // Q (query rows per item)
     int32_t window;
     int32_t heads_per_wg;   // q heads of the group served by one workgroup (divides group)
+    int32_t key_parts;      // waves per head splitting every tile's keys (1, 2 or 4; prefill_key_parts)
     int32_t n_ksplit;       // key ranges per query block; > 1: partials to part_o / part_ml
     float *part_o;          // [n, Hq, Q, n_ksplit, D] unnormalised outputs
     float2 *part_ml;        // [n, Hq, Q, n_ksplit] (running max in log2 units, sum)
@@ -315,6 +316,10 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
 // Most q heads one prefill workgroup computes (one wave each); a larger GQA
 // group is served by several workgroups.
 constexpr int kPfMaxHeads = 8;
+// Most waves per head (key parts) a prefill workgroup's tile buffers allow:
+// each part needs its own 32-key sub-tile, double-buffered in LDS.
+constexpr int kPfKeys = 32;  // keys per LDS sub-tile of the prefill kernel
+constexpr int prefill_max_parts(int head_dim) { return head_dim >= 512 ? 1 : head_dim >= 256 ? 2 : 4; }
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
 hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,
                             hipStream_t s);

@@ -68,6 +68,19 @@ __device__ __forceinline__ bool prefix_bit(uint32_t pw, int key) {
     const uint32_t w = (uint32_t)__shfl((int)pw, (key >> 5) & (kPrefixWords - 1));
     return ((w >> (key & 31)) & 1u) != 0;
 }
+// Mask bits of the 8 keys k0 .. k0 + 7 (k0 >= 0; bit j: key k0 + j passes
+// the mask of length plen), branch-free: the two words they span come from
+// the lanes that hold them, keys at or past plen pass. Every lane of the wave
+// must call this together.
+__device__ __forceinline__ uint32_t prefix_bits8(uint32_t pw, int k0, int plen) {
+    const int w = k0 >> 5;
+    const uint32_t lo = (uint32_t)__shfl((int)pw, w & (kPrefixWords - 1));
+    const uint32_t hi = (uint32_t)__shfl((int)pw, (w + 1) & (kPrefixWords - 1));
+    const uint32_t bits = (uint32_t)((((uint64_t)hi << 32) | lo) >> (k0 & 31)) & 0xffu;
+    const int past = plen - k0;  // keys j >= past are beyond the mask
+    const uint32_t open = past <= 0 ? 0xffu : past >= 8 ? 0u : (0xffu << past) & 0xffu;
+    return bits | open;
+}
 
 
 // PAGED row offset with the page taken from a wave's window of page-table
@@ -1297,7 +1310,6 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // with P split into two bf16 terms for the second product and everything
 // accumulated in fp32. MFMA lane layouts (16x16x32): A[row l%16][k 8(l/16)+j],
 // B[k 8(l/16)+j][col l%16], D[row 4(l/16)+v][col l%16].
-constexpr int kPfKeys = 32;  // keys per LDS tile
 
 // Key (within a tile) of row i of S^T block b. Chosen so that lane group G
 // (lanes 16G..16G+15) ends up with the scores of keys 8G..8G+7 across the two
@@ -1344,10 +1356,10 @@ __device__ __forceinline__ int64_t pf_row_offset(const KVView &kv, int slot, int
     }
 }
 
-template <int D, int LAYOUT>
+template <int D, int LAYOUT, int TK>
 __device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend, int c,
                                               u32x4_t &kx, u32x4_t &vx, bool &bad) {
-    constexpr int UNITS = kPfKeys * (D / 8);
+    constexpr int UNITS = TK * (D / 8);
     const uint16_t *kg = static_cast<const uint16_t *>(kv.k);
     const uint16_t *vg = static_cast<const uint16_t *>(kv.v);
     const int cc = c < UNITS ? c : 0;
@@ -1368,50 +1380,64 @@ constexpr int pf_pitch() { return D >= 128 ? D + 16 : D + 8; }
 template <int D>
 __device__ __forceinline__ int pf_swz(int r) { return D >= 128 ? (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1) : 0; }
 
-template <int D>
+// EXACT: every thread's unit is in the tile (UNITS a multiple of the block),
+// so no lane is masked off: a branch here would make the compiler wait for
+// every outstanding load at its join, the next tile's prefetch included.
+template <int D, int TK, bool EXACT>
 __device__ __forceinline__ void pf_stage_unit(uint16_t *sk, uint16_t *sv, int c, const u32x4_t &kx, const u32x4_t &vx) {
-    constexpr int UNITS = kPfKeys * (D / 8);
+    constexpr int UNITS = TK * (D / 8);
     constexpr int KP = pf_pitch<D>();
-    if (c < UNITS) {
+    if (EXACT || c < UNITS) {
         const int kr = c / (D / 8), ks = (c % (D / 8)) ^ pf_swz<D>(c / (D / 8));
         *reinterpret_cast<u32x4_t *>(&sk[kr * KP + 8 * ks]) = kx;
         *reinterpret_cast<u32x4_t *>(&sv[kr * KP + 8 * ks]) = vx;
     }
 }
 
-// A whole tile of KU units per thread: unit u of thread t is c = t + u * blockDim.
-template <int D, int LAYOUT, int KU>
+// A whole tile of TK keys, KU units per thread: unit u of thread t is
+// c = t + u * blockDim (the rows of a tile of KS sub-tiles are consecutive).
+template <int D, int LAYOUT, int TK, int KU, int NT>
 __device__ __forceinline__ void pf_fetch(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend,
                                          u32x4_t (&kreg)[KU], u32x4_t (&vreg)[KU], bool &bad) {
     StaticFor<0, KU>::run([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        pf_fetch_unit<D, LAYOUT>(kv, slot, kvh, t0, kstart, kend, threadIdx.x + u * (int)blockDim.x, kreg[u], vreg[u],
-                                 bad);
+        pf_fetch_unit<D, LAYOUT, TK>(kv, slot, kvh, t0, kstart, kend, threadIdx.x + u * NT, kreg[u], vreg[u], bad);
     });
 }
 
-template <int D, int KU>
+template <int D, int TK, int KU, int NT>
 __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4_t (&kreg)[KU], const u32x4_t (&vreg)[KU]) {
+    constexpr bool EXACT = (TK * (D / 8)) % NT == 0;
     StaticFor<0, KU>::run([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        pf_stage_unit<D>(sk, sv, threadIdx.x + u * (int)blockDim.x, kreg[u], vreg[u]);
+        pf_stage_unit<D, TK, EXACT>(sk, sv, threadIdx.x + u * NT, kreg[u], vreg[u]);
     });
 }
 
-template <int D, int LAYOUT, int NW, bool PF>
+template <int D, int LAYOUT, int NW, bool PF, int KS>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = pf_pitch<D>();  // K / V tile row pitch (bf16)
-    constexpr int UNITS = kPfKeys * (D / 8);  // 16-B units of a K (or V) tile
+    constexpr int TK = kPfKeys * KS;   // keys per iteration: KS sub-tiles of 32
+    constexpr int UNITS = TK * (D / 8);  // 16-B units of a K (or V) tile
     constexpr int KU = (UNITS + 64 * NW - 1) / (64 * NW);  // units per thread
     constexpr int PD = KU <= 2 ? 4 : 2;                      // tiles in flight with PF
     // two K/V tile buffers, so tile t + 1 is staged while tile t is computed
     constexpr int NBUF = 2;
-    constexpr int TILE = kPfKeys * KP;  // bf16 elements of one K (or V) tile buffer
+    constexpr int SUB = kPfKeys * KP;   // bf16 elements of one 32-key sub-tile
+    constexpr int TILE = KS * SUB;      // bf16 elements of one K (or V) tile buffer
+    static_assert(PF || KS == 1, "the LDS DMA path stages 32-key tiles");
+    // the KS - 1 upper parts' accumulators fit the tile buffers for the final combine
+    static_assert((KS - 1) * (NW / KS) * 16 * D * 4 <= NBUF * TILE * 2, "part combine fits LDS");
     __shared__ __align__(16) uint16_t sk[NBUF * TILE];
     __shared__ __align__(16) uint16_t sv[NBUF * TILE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
+    // Wave w computes head w % hw over key part w / hw: within every tile,
+    // part p takes the 32-key sub-tile p, and the parts' accumulators are
+    // combined at the end (KS > 1 puts 2 or 4 waves on one head and query
+    // block without staging any tile twice).
+    const int hidx = wave % hw, part = wave / hw;
     // Dispatch order: workgroups start in linear id order, so the id maps to
     // (query block, key range, head part, item) with the query block most
     // significant and the last blocks first. Without a window the last blocks
@@ -1427,8 +1453,8 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int item = (lin / (nks * gridDim.y)) % gridDim.z;
     const int kvh = by / nhb, hkv = gridDim.y / nhb;
     const int g = a.group, hq = hkv * g;
-    const bool computes = wave < hw;
-    const int head = kvh * g + (by % nhb) * hw + (computes ? wave : 0);
+    const bool computes = wave < hw * KS;
+    const int head = kvh * g + (by % nhb) * hw + (computes ? hidx : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     int plen;  // prefix-attention mask of the slot
@@ -1466,6 +1492,10 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool bad = false;
+    // keys this lane's query sees in the block's range: [klo, khi] (none if
+    // the lane has no query)
+    const int khi = qvalid ? min(kend - 1, pq) : -1;
+    const int klo = lo_q;
 
     // The MFMA work on the tile staged in LDS, keys t0 .. t0 + 31.
     // V^T operand rows through gfx950's LDS transpose read: in each group of
@@ -1477,8 +1507,11 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     // blocks b with bit 2 clear read 64 elements further when grp is odd, the
     // others 64 nearer)
     const int vd = D >= 128 ? (grp & 1) * 64 : 0;
+    // this wave's sub-tile of every tile buffer (key part `part`)
+    const uint16_t *sk_w = sk + part * SUB;
     const uint16_t *sv_base =
-        &sv[(8 * grp + (col >> 2)) * KP + 8 * (((col & 3) >> 1) ^ (D >= 128 ? grp >> 1 : 0)) + 4 * (col & 1)];
+        &sv[part * SUB + (8 * grp + (col >> 2)) * KP + 8 * (((col & 3) >> 1) ^ (D >= 128 ? grp >> 1 : 0)) +
+            4 * (col & 1)];
     const uint16_t *sv_lo = sv_base + vd, *sv_hi = sv_base - vd;
     auto read_vt = [&](const uint16_t *p) __attribute__((always_inline)) {
         typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -1506,29 +1539,32 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             // elements further when s3 is set, the others 64 nearer
             const int kr = pf_key(b, col);
             const int kd = D >= 128 ? ((kr >> 3) & 1) * 64 : 0;
-            const uint16_t *kp = &sk[BO + kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
+            const uint16_t *kp = &sk_w[BO + kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
 #pragma unroll
             for (int c = 0; c < D / 32; ++c)
                 s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd)), qop[c], s[b]);
         }
-        // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile
-        uint32_t pvis = 0xffu;  // bit j: key 8grp + j passes the prefix mask
-        if (t0 < plen) {        // the tile reaches into the prefix mask (wave-uniform)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = t0 + 8 * grp + j;
-                if (key < plen && !prefix_bit(pw, key)) pvis &= ~(1u << j);
-            }
-        }
+        // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile.
+        // Tiles every query sees whole take no per-key test; the others a
+        // branch-free one: key in [klo, khi] and passing the prefix mask.
         float sc[8];
         float tmax = -INFINITY;
+        if (all_visible) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int key = t0 + 8 * grp + j;
-            const float raw = j < 4 ? s[0][j] : s[1][j - 4];
-            const bool vis = all_visible || (qvalid && key < kend && key <= pq && key >= lo_q && ((pvis >> j) & 1u));
-            sc[j] = vis ? raw * a.scale_log2 : -INFINITY;
-            tmax = fmaxf(tmax, sc[j]);
+            for (int j = 0; j < 8; ++j) {
+                sc[j] = (j < 4 ? s[0][j] : s[1][j - 4]) * a.scale_log2;
+                tmax = fmaxf(tmax, sc[j]);
+            }
+        } else {
+            const int k0 = t0 + 8 * grp;
+            const uint32_t pvis = t0 < plen ? prefix_bits8(pw, k0, plen) : 0xffu;  // bit j: key k0 + j
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = k0 + j;
+                const bool vis = (key <= khi) & (key >= klo) & (((pvis >> j) & 1u) != 0);
+                sc[j] = vis ? (j < 4 ? s[0][j] : s[1][j - 4]) * a.scale_log2 : -INFINITY;
+                tmax = fmaxf(tmax, sc[j]);
+            }
         }
         tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
         lazy_rescale<D / 16>(tmax, m, l, o);
@@ -1568,23 +1604,28 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         u32x4_t kreg[PD][KU], vreg[PD][KU];
         StaticFor<0, PD>::run([&](auto pc) {
             constexpr int p = decltype(pc)::value;
-            pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, kstart + p * kPfKeys, kstart, kend, kreg[p], vreg[p], bad);
+            pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + p * TK, kstart, kend, kreg[p], vreg[p], bad);
         });
-        pf_stage<D, KU>(sk, sv, kreg[0], vreg[0]);
-        pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, kstart + PD * kPfKeys, kstart, kend, kreg[0], vreg[0], bad);
-        for (int t0 = kstart; t0 < kend; t0 += PD * kPfKeys) {
+        pf_stage<D, TK, KU, 64 * NW>(sk, sv, kreg[0], vreg[0]);
+        pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + PD * TK, kstart, kend, kreg[0], vreg[0], bad);
+        for (int t0 = kstart; t0 < kend; t0 += PD * TK) {
             StaticFor<0, PD>::run([&](auto pc) {
                 constexpr int p = decltype(pc)::value;
                 constexpr int pn = (p + 1) % PD;  // ring slot of the next tile
-                const int tt = t0 + p * kPfKeys;
+                const int tt = t0 + p * TK;
                 if (tt < kend) {
                     __syncthreads();
-                    if (tt + kPfKeys < kend) {
-                        pf_stage<D, KU>(sk + (pn % 2) * TILE, sv + (pn % 2) * TILE, kreg[pn], vreg[pn]);
-                        pf_fetch<D, LAYOUT, KU>(a.kv, slot, kvh, tt + kPfKeys + PD * kPfKeys, kstart, kend, kreg[pn],
-                                                vreg[pn], bad);
-                    }
-                    if (computes) compute_tile(tt, std::integral_constant<int, p % 2>{});
+                    // Staged and refetched unconditionally (past kend the
+                    // rows are clamped reads, never computed): a conditional
+                    // load here leaves the compiler unsure which loads are
+                    // still in flight, and it then waits for all of them
+                    // (the next tiles' prefetches included) before staging.
+                    pf_stage<D, TK, KU, 64 * NW>(sk + (pn % 2) * TILE, sv + (pn % 2) * TILE, kreg[pn], vreg[pn]);
+                    pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, tt + TK + PD * TK, kstart, kend, kreg[pn],
+                                                         vreg[pn], bad);
+                    // this wave's 32 keys of the tile (wave-uniform)
+                    const int st = tt + part * kPfKeys;
+                    if (computes && st < kend) compute_tile(st, std::integral_constant<int, p % 2>{});
                 }
             });
         }
@@ -1623,8 +1664,51 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         }
     }
     if (bad) a.err[0] = 1;
-    if (!computes) return;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));
+    if constexpr (KS > 1) {
+        // Combine the key parts of each head in a fixed order: parts 1 ..
+        // KS - 1 leave (m, l) per query and their o in the drained tile
+        // buffers; part 0 rescales everything to the common max and adds.
+        __syncthreads();  // every wave is done with the tile buffers
+        float *xo = reinterpret_cast<float *>(sk);    // [(part - 1) * hw + hidx][16 queries][D]
+        float2 *xml = reinterpret_cast<float2 *>(sv);  // [(part - 1) * hw + hidx][16 queries]
+        if (computes && part > 0) {
+            const int e = (part - 1) * hw + hidx;
+            float *dst = xo + ((int64_t)e * 16 + col) * D + 4 * grp;
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b)
+                *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+            if (grp == 0) xml[e * 16 + col] = make_float2(m, l);
+        }
+        __syncthreads();
+        if (!computes || part > 0) return;
+        float M = m;
+#pragma unroll
+        for (int q = 1; q < KS; ++q) M = fmaxf(M, xml[((q - 1) * hw + hidx) * 16 + col].x);
+        const float w0 = __builtin_amdgcn_exp2f(m - M);
+        l *= w0;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) o[b] *= w0;
+#pragma unroll
+        for (int q = 1; q < KS; ++q) {
+            const int e = (q - 1) * hw + hidx;
+            const float2 ml = xml[e * 16 + col];
+            const float w = __builtin_amdgcn_exp2f(ml.x - M);
+            l = fmaf(ml.y, w, l);
+            const float *src = xo + ((int64_t)e * 16 + col) * D + 4 * grp;
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b) {
+                const float4 x = *reinterpret_cast<const float4 *>(src + 16 * b);
+                o[b][0] = fmaf(x.x, w, o[b][0]);
+                o[b][1] = fmaf(x.y, w, o[b][1]);
+                o[b][2] = fmaf(x.z, w, o[b][2]);
+                o[b][3] = fmaf(x.w, w, o[b][3]);
+            }
+        }
+        m = M;
+    } else if (!computes) {
+        return;
+    }
     if (!qvalid) return;
     if (nks > 1) {  // this key range's partial: o unnormalised, (m, l)
         const int64_t pi = (((int64_t)item * hq + head) * Qn + qr) * nks + ks;
@@ -2027,16 +2111,34 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int hw = a.heads_per_wg;
     if (hw <= 0 || a.group % hw != 0 || hw > kPfMaxHeads) return hipErrorInvalidValue;
     if (a.n_ksplit < 1 || (a.n_ksplit > 1 && (!a.part_o || !a.part_ml))) return hipErrorInvalidValue;
+    const int ks = a.key_parts;
+    if ((ks != 1 && ks != 2 && ks != 4) || ks > prefill_max_parts(head_dim) || hw * ks > 8) return hipErrorInvalidValue;
+    if (a.kv.layout == KVRT_LAYOUT_RING && a.kv.rows < kPfKeys * ks) return hipErrorInvalidValue;  // one wrap per tile
     dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
-    // 4 or 8 waves; D = 512 keeps no tile in flight across the MFMAs (registers)
-    if (hw > 4) {
-        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
-            hipLaunchKernelGGL((prefill_kernel<HD, LY, 8, (HD < 512)>), grid, dim3(512), 0, s, a)));
-    } else {
-        KVRT_DISPATCH_D(head_dim, KVRT_DISPATCH_LAYOUT(a.kv.layout,
-            hipLaunchKernelGGL((prefill_kernel<HD, LY, 4, (HD < 512)>), grid, dim3(256), 0, s, a)));
-    }
-    hipError_t e = hipGetLastError();
+    // 4 or 8 waves (hw * ks compute); D = 512 keeps no tile in flight across
+    // the MFMAs (registers)
+    const bool w8 = hw * ks > 4;
+    auto go = [&](auto nw_c, auto ks_c) -> hipError_t {
+        constexpr int NW = decltype(nw_c)::value, KS = decltype(ks_c)::value;
+        KVRT_DISPATCH_D(head_dim, {
+            if constexpr (KS <= prefill_max_parts(HD)) {
+                KVRT_DISPATCH_LAYOUT(a.kv.layout, hipLaunchKernelGGL((prefill_kernel<HD, LY, NW, (HD < 512), KS>),
+                                                                     grid, dim3(64 * NW), 0, s, a));
+                return hipGetLastError();
+            } else {
+                return hipErrorInvalidValue;
+            }
+        });
+        return hipErrorInvalidValue;
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    using I8 = std::integral_constant<int, 8>;
+    hipError_t e;
+    if (ks == 1) e = w8 ? go(I8{}, I1{}) : go(I4{}, I1{});
+    else if (ks == 2) e = w8 ? go(I8{}, I2{}) : go(I4{}, I2{});
+    else e = w8 ? go(I8{}, I4{}) : go(I4{}, I4{});
     if (e != hipSuccess || a.n_ksplit == 1) return e;
     const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
     hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim, outs);

@@ -1813,6 +1813,19 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     for (int d = 1; d <= std::min({group, kPfMaxHeads, hw_cap}); ++d)
         if (group % d == 0) hw = d;
     a.heads_per_wg = hw;
+    // Key parts: up to 8 waves per workgroup, hw heads x key_parts waves each
+    // splitting every tile's keys (the tile buffers bound the parts: 2 at
+    // D 256, 4 below, 1 at D 512; a ring needs a tile's keys to wrap at most
+    // once). More waves on each query block shorten the latency-bound chain
+    // of tiles of a short chunk: 2 parts took thinker sliding Q 291 from 36.9
+    // to 29.6 us, talker Q 512 from 33.6 to 29.7 us and thinker Q 2048 from
+    // 93.2 to 67.2 us; 4 parts (talker: 147 KB of LDS, one workgroup per CU)
+    // 43.9 us for the talker. KVRT_PF_KEY_PARTS caps it.
+    static const int parts_env = env_int("KVRT_PF_KEY_PARTS", 2);
+    int parts = std::min({parts_env, prefill_max_parts(D), 8 / hw});
+    parts = parts >= 4 ? 4 : parts >= 2 ? 2 : 1;
+    while (parts > 1 && s.layout == KVRT_LAYOUT_RING && s.ring_rows < kPfKeys * parts) parts /= 2;
+    a.key_parts = parts;
     // Key split: when the query blocks give fewer than 128 workgroups (a short
     // chunk over a long context: thinker full layers, Q 291 over 2048 keys,
     // 76 workgroups on 256 CUs), each block's keys are cut into n_ksplit

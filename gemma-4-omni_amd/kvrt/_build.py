@@ -30,6 +30,9 @@ HIPCC_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Wall",
     "-Wno-unused-function",
+    # flowing off the end of a value-returning function is undefined (a
+    # launcher lambda that did so crashed the host): refuse to build it
+    "-Werror=return-type",
 ]
 
 

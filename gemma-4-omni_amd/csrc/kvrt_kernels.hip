@@ -1379,6 +1379,14 @@ template <int D>
 constexpr int pf_pitch() { return D >= 128 ? D + 16 : D + 8; }
 template <int D>
 __device__ __forceinline__ int pf_swz(int r) { return D >= 128 ? (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1) : 0; }
+// Chunk swizzle of the unpadded DMA-ring stages (rows of D bf16, 16-B chunk c
+// of row r at c ^ pf_rswz(r), r < 32): bits 0, 1, 3 and 4 of the row move
+// chunk bits 1, 2, 3 and 0. With 64 banks of 4 B, the 16 rows x 16 B of one
+// S^T A-operand read (keys pf_key(b, 0..15)) land on 16 distinct 16-B bank
+// groups and the 8 rows x 2 chunks of a half-wave V^T transposed read on 16
+// (found by enumerating XOR maps of the row bits); bit 2 is unused, so rows
+// r and r + 4 (the two halves of a transposed read) share the swizzle.
+__device__ __forceinline__ int pf_rswz(int r) { return ((r & 3) << 1) | (((r >> 3) & 1) << 3) | ((r >> 4) & 1); }
 
 // EXACT: every thread's unit is in the tile (UNITS a multiple of the block),
 // so no lane is masked off: a branch here would make the compiler wait for
@@ -1414,7 +1422,7 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
     });
 }
 
-template <int D, int LAYOUT, int NW, bool PF, int KS>
+template <int D, int LAYOUT, int NW, bool PF, int KS, int G = 0>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = pf_pitch<D>();  // K / V tile row pitch (bf16)
     constexpr int TK = kPfKeys * KS;   // keys per iteration: KS sub-tiles of 32
@@ -1425,11 +1433,19 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int NBUF = 2;
     constexpr int SUB = kPfKeys * KP;   // bf16 elements of one 32-key sub-tile
     constexpr int TILE = KS * SUB;      // bf16 elements of one K (or V) tile buffer
+    // G > 0: the LDS DMA ring (bf16 CONTIG / RING, D 128 / 256): NS = KS * G
+    // unpadded, swizzled 32-key stages (pf_rswz), G - 1 groups of KS in flight
+    constexpr bool RG = G > 0;
+    constexpr int NS = KS * (RG ? G : 1);
+    constexpr int RSUB = kPfKeys * D;   // bf16 elements of one ring stage (K or V)
+    constexpr int LDS_ELEMS = RG ? NS * RSUB : NBUF * TILE;
     static_assert(PF || KS == 1, "the LDS DMA path stages 32-key tiles");
+    static_assert(!RG || (PF && (D == 128 || D == 256) && LAYOUT != KVRT_LAYOUT_PAGED && G >= 2 &&
+                          (D / 8) % NW == 0), "DMA ring: bf16 CONTIG / RING, D 128 / 256");
     // the KS - 1 upper parts' accumulators fit the tile buffers for the final combine
-    static_assert((KS - 1) * (NW / KS) * 16 * D * 4 <= NBUF * TILE * 2, "part combine fits LDS");
-    __shared__ __align__(16) uint16_t sk[NBUF * TILE];
-    __shared__ __align__(16) uint16_t sv[NBUF * TILE];
+    static_assert((KS - 1) * (NW / KS) * 16 * D * 4 <= LDS_ELEMS * 2, "part combine fits LDS");
+    __shared__ __align__(16) uint16_t sk[LDS_ELEMS];
+    __shared__ __align__(16) uint16_t sv[LDS_ELEMS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
@@ -1522,8 +1538,10 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         return make_uint4(l2.x, l2.y, h2.x, h2.y);
     };
-    auto compute_tile = [&](int t0, auto buf_c) __attribute__((always_inline)) {
-        constexpr int BO = decltype(buf_c)::value * TILE;  // the tile's buffer
+    // The work on one staged 32-key tile: kop(b, c) is key row pf_key(b, col)'s
+    // A operand of reduction step c, vop(b) the V^T operand of dims 16b ..
+    // 16b + 15 (both read from LDS).
+    auto tile_core = [&](int t0, auto kop, auto vop) __attribute__((always_inline)) {
         // every key of the tile visible to all 16 queries of the block (the
         // block's first query sees up to its own position, the last one's
         // window starts at or before t0): no per-key mask
@@ -1537,12 +1555,8 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             // chunk grp + 4c of key row kr sits at (grp ^ s0) + 4 * (c ^ 2 s3)
             // (s0, s3: bits 4 and 3 of kr): slices c with bit 1 clear read 64
             // elements further when s3 is set, the others 64 nearer
-            const int kr = pf_key(b, col);
-            const int kd = D >= 128 ? ((kr >> 3) & 1) * 64 : 0;
-            const uint16_t *kp = &sk_w[BO + kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
 #pragma unroll
-            for (int c = 0; c < D / 32; ++c)
-                s[b] = mfma16(*reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd)), qop[c], s[b]);
+            for (int c = 0; c < D / 32; ++c) s[b] = mfma16(kop(b, c), qop[c], s[b]);
         }
         // mask and scale; this lane holds keys 8grp .. 8grp+7 of the tile.
         // Tiles every query sees whole take no per-key test; the others a
@@ -1585,15 +1599,106 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // O^T += V^T P^T: A row i = d (16b + col), k = keys 8grp .. +7
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) {
-            const uint4 va = read_vt(((b >> 2) & 1 ? sv_hi : sv_lo) + BO + 16 * b);
+            const uint4 va = vop(b);
             o[b] = mfma16(va, pop_lo, mfma16(va, pop_hi, o[b]));
         }
+    };
+    // the padded, chunk-swizzled tile buffers of the register-staged paths
+    auto compute_tile = [&](int t0, auto buf_c) __attribute__((always_inline)) {
+        constexpr int BO = decltype(buf_c)::value * TILE;  // the tile's buffer
+        tile_core(
+            t0,
+            [&](int b, int c) __attribute__((always_inline)) {
+                // chunk grp + 4c of key row kr sits at (grp ^ s0) + 4 * (c ^ 2 s3)
+                // (s0, s3: bits 4 and 3 of kr): slices c with bit 1 clear read 64
+                // elements further when s3 is set, the others 64 nearer
+                const int kr = pf_key(b, col);
+                const int kd = D >= 128 ? ((kr >> 3) & 1) * 64 : 0;
+                const uint16_t *kp = &sk_w[BO + kr * KP + 8 * (grp ^ (D >= 128 ? (kr >> 4) & 1 : 0))];
+                return *reinterpret_cast<const uint4 *>(kp + 32 * c + ((c >> 1) & 1 ? -kd : kd));
+            },
+            [&](int b) __attribute__((always_inline)) {
+                return read_vt(((b >> 2) & 1 ? sv_hi : sv_lo) + BO + 16 * b);
+            });
     };
     // Q is in registers before the first prefetch is issued: inside the loop
     // the compiler then waits only for each tile's own loads, not for the
     // prefetches behind it (vmcnt counts in order).
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    if constexpr (PF) {
+    if constexpr (RG) {
+        // LDS DMA ring: 32-key tile j (keys kstart + 32 j ..) goes to stage
+        // j % NS, K and V rows unpadded and chunk-swizzled (pf_rswz), by
+        // global_load_lds_dwordx4 (a 1 KiB row range per instruction, lane l
+        // fetching the logical chunk that lands on physical chunk l), the
+        // instructions of a tile spread over the waves. Groups of KS tiles
+        // are computed one after another (part p takes tile it * KS + p)
+        // while the next G - 1 groups are in flight; no registers hold them,
+        // and every wait is an explicit vmcnt on this wave's own DMAs (loads
+        // complete in issue order) followed by one barrier per group.
+        constexpr int RPI = 1024 / (2 * D);   // key rows per DMA instruction
+        constexpr int IPT = kPfKeys / RPI;    // instructions per K (or V) tile
+        constexpr int DPW = 2 * IPT / NW;     // instructions per wave and tile
+        static_assert((2 * IPT) % NW == 0, "a tile's DMAs split evenly over the waves");
+        const uint16_t *kg = static_cast<const uint16_t *>(a.kv.k);
+        const uint16_t *vg = static_cast<const uint16_t *>(a.kv.v);
+        const uint32_t sk_a = lds_addr(sk), sv_a = lds_addr(sv);
+        const int ntiles = kend > kstart ? (kend - kstart + kPfKeys - 1) / kPfKeys : 0;
+        const int ngroups = (ntiles + KS - 1) / KS;
+        const int lrow = lane / (D / 8), pchunk = lane % (D / 8);
+        auto issue_tile = [&](int j) __attribute__((always_inline)) {
+            const int t0 = kstart + j * kPfKeys;
+            const uint32_t stage = (uint32_t)((j % NS) * RSUB) * 2;
+#pragma unroll
+            for (int i = 0; i < DPW; ++i) {
+                const int q = wave + i * NW;      // < IPT: K instruction q, else V instruction q - IPT
+                const int ins = q % IPT;
+                const int r = ins * RPI + lrow;   // key row of this lane
+                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, r, bad);
+                const uint16_t *gp = (q < IPT ? kg : vg) + off + 8 * (pchunk ^ pf_rswz(r));
+                const uint32_t dst = (q < IPT ? sk_a : sv_a) + stage + (uint32_t)ins * 1024u;
+                dma_load16_cached(gp, __builtin_amdgcn_readfirstlane(dst));
+            }
+        };
+        int issued = min((G - 1) * KS, ntiles);
+        for (int j = 0; j < issued; ++j) issue_tile(j);
+        // this lane's rows and swizzles in a stage: S^T A operand of key
+        // pf_key(b, col) (logical chunk 4c + grp), V^T row 8grp + col/4 (+4)
+        // with logical chunk 2b + (col & 3) / 2 and half col & 1
+        const int kr0 = pf_key(0, col), kr1 = pf_key(1, col);
+        const int ksw0 = grp ^ pf_rswz(kr0), ksw1 = grp ^ pf_rswz(kr1);
+        const int rv = 8 * grp + (col >> 2);
+        const int vsw = ((col & 3) >> 1) ^ pf_rswz(rv);
+        const int voff = rv * D + 4 * (col & 1);
+        for (int it = 0; it < ngroups; ++it) {
+            // tiles issued after this group's: their DMAs may stay in flight
+            const int later = issued - min((it + 1) * KS, ntiles);
+            wait_vmem_steps<DPW, (G - 1) * KS>(later);
+            __syncthreads();  // every wave's DMAs of group it have landed; group it - 1 is done
+            const int next = min((it + G) * KS, ntiles);
+            for (int j = issued; j < next; ++j) issue_tile(j);  // into group it - 1's stages
+            issued = next;
+            const int j = it * KS + part;  // this wave's tile (wave-uniform)
+            if (computes && j < ntiles) {
+                const int sb = (j % NS) * RSUB;
+                tile_core(
+                    kstart + j * kPfKeys,
+                    [&](int b, int c) __attribute__((always_inline)) {
+                        const int kr = b ? kr1 : kr0, ksw = b ? ksw1 : ksw0;
+                        return *reinterpret_cast<const uint4 *>(&sk[sb + kr * D + 8 * ((4 * c) ^ ksw)]);
+                    },
+                    [&](int b) __attribute__((always_inline)) {
+                        typedef short v4s_t __attribute__((ext_vector_type(4)));
+                        const uint16_t *p = &sv[sb + voff + 8 * ((2 * b) ^ vsw)];
+                        const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (v4s_t __attribute__((address_space(3))) *)(p));
+                        const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (v4s_t __attribute__((address_space(3))) *)(p + 4 * D));
+                        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                        return make_uint4(l2.x, l2.y, h2.x, h2.y);
+                    });
+            }
+        }
+    } else if constexpr (PF) {
         // PD tiles in flight in registers (ring slot s holds tiles s, s + PD,
         // ...; keys past kend read row kstart: in bounds, never visible) and
         // two tile buffers in LDS (tile i in buffer i % 2; PD is even). Per
@@ -2114,6 +2219,42 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int ks = a.key_parts;
     if ((ks != 1 && ks != 2 && ks != 4) || ks > prefill_max_parts(head_dim) || hw * ks > 8) return hipErrorInvalidValue;
     if (a.kv.layout == KVRT_LAYOUT_RING && a.kv.rows < kPfKeys * ks) return hipErrorInvalidValue;  // one wrap per tile
+    if (a.ring_groups) {
+        // DMA ring: hw * ks waves (at least 2), every one computing
+        const int g = a.ring_groups;
+        if (!prefill_ring_ok(head_dim, a.kv.layout, ks, g) || hw * ks > 8) return hipErrorInvalidValue;
+        dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
+        const int nw = hw * ks < 2 ? 2 : hw * ks;
+        auto ring = [&](auto d_c, auto ks_c) -> hipError_t {
+            constexpr int HD = decltype(d_c)::value, KS = decltype(ks_c)::value;
+            constexpr int G = kPfRingGroups;
+            auto go = [&](auto nw_c) {
+                constexpr int NW = decltype(nw_c)::value;
+                if (a.kv.layout == KVRT_LAYOUT_RING)
+                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_RING, NW, true, KS, G>), grid, dim3(64 * NW),
+                                       0, s, a);
+                else
+                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_CONTIG, NW, true, KS, G>), grid, dim3(64 * NW),
+                                       0, s, a);
+            };
+            if (nw == 2) go(std::integral_constant<int, 2>{});
+            else if (nw == 4) go(std::integral_constant<int, 4>{});
+            else go(std::integral_constant<int, 8>{});
+            return hipGetLastError();
+        };
+        using C128 = std::integral_constant<int, 128>;
+        using C256 = std::integral_constant<int, 256>;
+        using K1 = std::integral_constant<int, 1>;
+        using K2 = std::integral_constant<int, 2>;
+        hipError_t e;
+        if (head_dim == 256) e = ks == 1 ? ring(C256{}, K1{}) : ring(C256{}, K2{});
+        else e = ks == 1 ? ring(C128{}, K1{}) : ring(C128{}, K2{});
+        if (e != hipSuccess || a.n_ksplit == 1) return e;
+        const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
+        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim,
+                           outs);
+        return hipGetLastError();
+    }
     dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
     // 4 or 8 waves (hw * ks compute); D = 512 keeps no tile in flight across
     // the MFMAs (registers)

@@ -1822,10 +1822,23 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     // 93.2 to 67.2 us; 4 parts (talker: 147 KB of LDS, one workgroup per CU)
     // 43.9 us for the talker. KVRT_PF_KEY_PARTS caps it.
     static const int parts_env = env_int("KVRT_PF_KEY_PARTS", 2);
+    const int64_t wgs_grid = (int64_t)((qn + 15) / 16) * hkv * (group / hw) * n;
     int parts = std::min({parts_env, prefill_max_parts(D), 8 / hw});
+    if (wgs_grid >= 512) parts = 1;  // a grid of two workgroups per CU needs no more waves per block
     parts = parts >= 4 ? 4 : parts >= 2 ? 2 : 1;
     while (parts > 1 && s.layout == KVRT_LAYOUT_RING && s.ring_rows < kPfKeys * parts) parts /= 2;
     a.key_parts = parts;
+    // LDS DMA ring (bf16 CONTIG / RING, D 128 / 256) instead of tiles staged
+    // through registers: KVRT_PF_RING = 1 / 0 forces it on / off
+    static const int ring_env = [] {
+        const char *e = std::getenv("KVRT_PF_RING");
+        return e && *e ? std::atoi(e) : -1;
+    }();
+    const bool ring_default = D == 128;
+    a.ring_groups = 0;
+    if ((ring_env > 0 || (ring_env < 0 && ring_default)) && prefill_ring_ok(D, s.layout, parts, kPfRingGroups) &&
+        (s.layout != KVRT_LAYOUT_RING || s.ring_rows >= kPfKeys))
+        a.ring_groups = kPfRingGroups;
     // Key split: when the query blocks give fewer than 128 workgroups (a short
     // chunk over a long context: thinker full layers, Q 291 over 2048 keys,
     // 76 workgroups on 256 CUs), each block's keys are cut into n_ksplit

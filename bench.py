@@ -237,16 +237,20 @@ def time_dominant_kernel(model: Model, reps: int) -> dict:
             "single": central_mean(single)}
 
 
-def pmc_traffic() -> tuple[int | None, str | None]:
+def pmc_traffic() -> dict | None:
     """HBM bytes per launch of the dominant launch, from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a 256 MiB
-    copy); None when that summary is absent."""
+    copy; counter runs cannot share a process with the timed run), with the
+    algorithmic bytes of the same dispatches; None when that summary is
+    absent."""
     path = ROOT / "profiles" / "pmc_traffic.json"
     try:
         data = json.loads(path.read_text())
-        return int(data["traffic_bytes_per_launch"]), str(data["source"])
+        return {"bytes": int(data["traffic_bytes_per_launch"]), "source": str(data["source"]),
+                "algorithmic": int(data["algorithmic_bytes_same_dispatches"]),
+                "ratio": float(data["traffic_over_algorithmic"])}
     except (OSError, KeyError, ValueError):
-        return None, None
+        return None
 
 
 def cpu_baseline(args) -> dict | None:
@@ -990,7 +994,7 @@ def main() -> int:
         b.copy_(a)
         torch.cuda.synchronize()
     cpu = cpu_baseline(args)
-    traffic, traffic_src = pmc_traffic()
+    traffic = pmc_traffic()
     out = {
         "metric": "KV append+decode-attn tokens/s, HBM GB/s (% of peak), 1 MI355X",
         "value": round(tokens_per_step * args.steps / elapsed, 2),
@@ -1032,8 +1036,11 @@ def main() -> int:
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": traffic,
-            "traffic_source": traffic_src,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
+            # the counter runs' dispatches (lengths 4096-4106) against their own algorithmic bytes
+            "traffic_algorithmic_same_dispatches": traffic["algorithmic"] if traffic else None,
+            "traffic_over_algorithmic": traffic["ratio"] if traffic else None,
             "avg_launch_us": round(k_time * 1e6, 3),
             "timing": f"HIP events around the talker's {TALKER['layers']} layer launches back to back, per launch",
             "single_launch_us": round(dom["single"] * 1e6, 3),

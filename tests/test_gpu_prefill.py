@@ -76,6 +76,11 @@ def _check(rt, orc, q, scale, prefill=True):
         # workgroups and the partials merged (8 and 2 key ranges)
         (8, 1, 512, 0, "contig", [2000, 900], 64),
         (4, 2, 128, 600, "paged", [1500], 40),
+        # the talker's whole-response prefill: a grid of 1024 workgroups, one
+        # wave per head (LDS DMA ring, two waves per workgroup)
+        (16, 8, 128, 0, "contig", [0, 0, 0, 0], 512),
+        # LDS DMA ring over a wrapped ring layout, two waves per head
+        (8, 2, 128, 200, "ring", [900, 64], 77),
     ],
 )
 def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):

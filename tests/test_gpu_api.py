@@ -80,7 +80,12 @@ def test_positional_writes_follow_the_slot_kv_cache_contract():
 
     def write(layer, positions, value=1.0):
         x = torch.full((1, 1, len(positions), 64), value, dtype=torch.bfloat16, device="cuda")
-        cache.update(x, x, layer, {"cache_position": torch.tensor(positions, dtype=torch.long)})
+        k_all, v_all = cache.update(x, x, layer, {"cache_position": torch.tensor(positions, dtype=torch.long)})
+        # like _SlotKVCache.update (future_prefix.py:544-565): the slot's whole
+        # [1, H, max_cache_len, D] storage, matching masks built at capacity
+        assert tuple(k_all.shape) == tuple(v_all.shape) == (1, 1, 16, 64)
+        assert k_all.data_ptr() == rt.storage(layer)[0][cache.slot].data_ptr()  # zero-copy view of the slot
+        return k_all
 
     write(0, [0, 1])
     assert cache.get_seq_length() == 2

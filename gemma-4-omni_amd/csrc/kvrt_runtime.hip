@@ -219,6 +219,17 @@ bool tensor_ok(const kvrt_tensor *t, int dtype, int ndim) {
     return true;
 }
 
+// tensor_ok, or an empty tensor of that dtype and rank (torch gives those a
+// null data pointer); for calls that launch nothing when a dimension is 0.
+bool tensor_ok_or_empty(const kvrt_tensor *t, int dtype, int ndim) {
+    if (!t || t->dtype != dtype || t->ndim != ndim) return false;
+    for (int i = 0; i < ndim; ++i)
+        if (t->dims[i] < 0) return false;
+    for (int i = 0; i < ndim; ++i)
+        if (t->dims[i] == 0) return true;
+    return tensor_ok(t, dtype, ndim);
+}
+
 bool is_contiguous(const kvrt_tensor *t) {
     int64_t expect = 1;
     for (int i = t->ndim - 1; i >= 0; --i) {
@@ -1184,9 +1195,9 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
     if (!valid_slot(c, slot) || !valid_layer(c, layer)) return KVRT_EINVAL;
     if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // import the source layer instead
     const kvrt_layer_spec &s = c->layers[layer].spec;
-    if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4)) return KVRT_EINVAL;
+    if (!tensor_ok_or_empty(k, KVRT_BF16, 4) || !tensor_ok_or_empty(v, KVRT_BF16, 4)) return KVRT_EINVAL;
     for (int i = 0; i < 4; ++i)
-        if (k->dims[i] != v->dims[i] || k->strides[i] != v->strides[i]) return KVRT_EINVAL;
+        if (k->dims[i] != v->dims[i] || (k->dims[2] > 0 && k->strides[i] != v->strides[i])) return KVRT_EINVAL;
     const int64_t S = k->dims[2];
     if (k->dims[0] != 1 || k->dims[1] != s.kv_heads || k->dims[3] != s.head_dim) return KVRT_EINVAL;
     if (S < 0 || S > c->cfg.capacity || first_pos < 0 || first_pos > S) return KVRT_EINVAL;

@@ -359,6 +359,17 @@ __device__ __forceinline__ void store_agent(float2 *p, float2 v) {
     const uint64_t b = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
     __hip_atomic_store(reinterpret_cast<uint64_t *>(p), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// N consecutive floats, as 8-byte stores where N is even (dst 8-byte aligned).
+template <int N>
+__device__ __forceinline__ void store_agent_n(float *dst, const float (&v)[N]) {
+    if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int e = 0; e < N; e += 2) store_agent(reinterpret_cast<float2 *>(dst + e), make_float2(v[e], v[e + 1]));
+    } else {
+#pragma unroll
+        for (int e = 0; e < N; ++e) store_agent(dst + e, v[e]);
+    }
+}
 __device__ __forceinline__ float load_agent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -373,6 +384,16 @@ __device__ __forceinline__ float2 load_agent(const float2 *p) {
 // them in the merge kernel's order and writes the output; the last of an
 // item's kv heads then advances the item's length. Every workgroup of the
 // grid reaches this point exactly once, which returns the counters to zero.
+// With more outputs than threads, a thread merges EPT outputs of one row per
+// pass, with the partial loads of all EPT outputs issued together: a batch of
+// up to 16 partials costs one dependent memory round trip per pass instead
+// of one per output (8 rows x D 256: 1 pass instead of 8). EPT is 8 where the
+// decode already holds ~200 VGPRs (D >= 256, >= 2048 outputs), 2 elsewhere,
+// so the tail does not raise a lighter kernel's register count. With at most
+// one output per thread (the talker's 2 rows x D 128) each thread merges its
+// own output (one round trip; the paired form measured 0.15 us slower per
+// launch there). Per output the arithmetic is merge_partials<1>'s (batches of
+// 16 in partial order), so both merge paths round identically.
 template <int D, int R>
 __device__ __forceinline__ void decode_merge_tail(const DecodeArgs &a, int item, int kvh, int hkv, int rows) {
     __shared__ uint32_t arrived;
@@ -385,18 +406,75 @@ __device__ __forceinline__ void decode_merge_tail(const DecodeArgs &a, int item,
     const int n_parts = gridDim.x;
     const int Qn = a.qn;
     const int64_t pbase = ((int64_t)item * hkv + kvh) * a.n_split * R;  // part s, row r at pbase + s*R + r
-    for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
-        const int r = idx / D, d = idx % D;
-        const float2 *ml = a.part_ml + pbase + r;
-        const float *acc = a.part_acc + (pbase + r) * D + d;
-        float M = kNegBig, L = 0.f, O = 0.f;
-        merge_partials<1>(0, n_parts, [&](int sp, float2 &m, float &v) {
-            m = load_agent(ml + (int64_t)sp * R);
-            v = load_agent(acc + (int64_t)sp * R * D);
-        }, M, L, O);
-        const int jh = r / Qn, i = r % Qn;
-        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
-            f32_to_bf16(L > 0.f ? O / L : 0.f);
+    if constexpr (R * D <= 256) {
+        const int idx = threadIdx.x;
+        if (idx < rows * D) {
+            const int r = idx / D, d = idx % D;
+            const float2 *ml = a.part_ml + pbase + r;
+            const float *acc = a.part_acc + (pbase + r) * D + d;
+            float M = kNegBig, L = 0.f, O = 0.f;
+            merge_partials<1>(0, n_parts, [&](int sp, float2 &m, float &v) {
+                m = load_agent(ml + (int64_t)sp * R);
+                v = load_agent(acc + (int64_t)sp * R * D);
+            }, M, L, O);
+            const int jh = r / Qn, i = r % Qn;
+            a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
+                f32_to_bf16(L > 0.f ? O / L : 0.f);
+        }
+    } else {
+        constexpr int EPT = (D >= 256 && R * D >= 2048) ? 8 : 2;  // divides D (>= 64)
+        constexpr int B = 16;
+        // The D / EPT threads of a row take float2 columns j, j + D/EPT, ... so
+        // that each load instruction reads whole consecutive runs of a row.
+        constexpr int TPR = D / EPT;  // threads per row
+        for (int e0 = threadIdx.x * EPT; e0 < rows * D; e0 += blockDim.x * EPT) {
+            const int r = e0 / D, j = (e0 % D) / EPT;
+            const float2 *ml = a.part_ml + pbase + r;
+            const float2 *acc = reinterpret_cast<const float2 *>(a.part_acc + (pbase + r) * D) + j;
+            float M = kNegBig, L = 0.f, O[EPT];
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) O[e] = 0.f;
+            for (int s0 = 0; s0 < n_parts; s0 += B) {
+                float2 m[B], v[B][EPT / 2];
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    const int sp = s0 + u;
+                    m[u] = make_float2(kNegBig, 0.f);
+#pragma unroll
+                    for (int h = 0; h < EPT / 2; ++h) v[u][h] = make_float2(0.f, 0.f);
+                    if (sp < n_parts) {
+                        m[u] = load_agent(ml + (int64_t)sp * R);
+#pragma unroll
+                        for (int h = 0; h < EPT / 2; ++h) v[u][h] = load_agent(acc + (int64_t)sp * R * D / 2 + h * TPR);
+                    }
+                }
+                float bm = M;
+#pragma unroll
+                for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
+                const float c = __builtin_amdgcn_exp2f(M - bm);
+                L *= c;
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) O[e] *= c;
+                M = bm;
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    const float w = __builtin_amdgcn_exp2f(m[u].x - M);
+                    L = fmaf(m[u].y, w, L);
+#pragma unroll
+                    for (int h = 0; h < EPT / 2; ++h) {
+                        O[2 * h] = fmaf(v[u][h].x, w, O[2 * h]);
+                        O[2 * h + 1] = fmaf(v[u][h].y, w, O[2 * h + 1]);
+                    }
+                }
+            }
+            const int jh = r / Qn, i = r % Qn;
+            const int64_t orow = (((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D;
+            uint32_t *dst = reinterpret_cast<uint32_t *>(a.out + orow) + j;
+#pragma unroll
+            for (int h = 0; h < EPT / 2; ++h)
+                dst[h * TPR] = (uint32_t)f32_to_bf16(L > 0.f ? O[2 * h] / L : 0.f) |
+                               ((uint32_t)f32_to_bf16(L > 0.f ? O[2 * h + 1] / L : 0.f) << 16);
+        }
     }
     if (threadIdx.x == 0) {
         __hip_atomic_store(hc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -857,8 +935,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
             }
             float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
             if (a.cnt) {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) store_agent(dst + e, o[e]);
+                store_agent_n<EPL>(dst, o);
                 if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
             } else {
 #pragma unroll
@@ -1238,8 +1315,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         }
         float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
         if (a.cnt) {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) store_agent(dst + e, acc[e]);
+            store_agent_n<EPL>(dst, acc);
             if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
         } else {
 #pragma unroll

@@ -1851,14 +1851,17 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // KS - 1 leave (m, l) per query and their o in the drained tile
         // buffers; part 0 rescales everything to the common max and adds.
         __syncthreads();  // every wave is done with the tile buffers
-        float *xo = reinterpret_cast<float *>(sk);    // [(part - 1) * hw + hidx][16 queries][D]
+        // o as each lane holds it, [(part - 1) * hw + hidx][block b][lane]: the
+        // 64 lanes of a write or read touch 1 KiB of consecutive 16-B chunks (no
+        // bank conflicts; a [query][D] layout put the 16 queries of a half-wave
+        // D * 4 B apart, on the same banks)
+        float4 *xo = reinterpret_cast<float4 *>(sk);
         float2 *xml = reinterpret_cast<float2 *>(sv);  // [(part - 1) * hw + hidx][16 queries]
         if (computes && part > 0) {
             const int e = (part - 1) * hw + hidx;
-            float *dst = xo + ((int64_t)e * 16 + col) * D + 4 * grp;
+            float4 *dst = xo + (int64_t)e * (D / 16) * 64 + lane;
 #pragma unroll
-            for (int b = 0; b < D / 16; ++b)
-                *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+            for (int b = 0; b < D / 16; ++b) dst[64 * b] = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
             if (grp == 0) xml[e * 16 + col] = make_float2(m, l);
         }
         __syncthreads();
@@ -1876,10 +1879,10 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             const float2 ml = xml[e * 16 + col];
             const float w = __builtin_amdgcn_exp2f(ml.x - M);
             l = fmaf(ml.y, w, l);
-            const float *src = xo + ((int64_t)e * 16 + col) * D + 4 * grp;
+            const float4 *src = xo + (int64_t)e * (D / 16) * 64 + lane;
 #pragma unroll
             for (int b = 0; b < D / 16; ++b) {
-                const float4 x = *reinterpret_cast<const float4 *>(src + 16 * b);
+                const float4 x = src[64 * b];
                 o[b][0] = fmaf(x.x, w, o[b][0]);
                 o[b][1] = fmaf(x.y, w, o[b][1]);
                 o[b][2] = fmaf(x.z, w, o[b][2]);

@@ -711,6 +711,7 @@ def run_configs(args) -> int:
                for _ in range(pool)]
         kbuf = torch.empty((n, 8, cap, 128), dtype=torch.bfloat16, device="cuda")
         vbuf = torch.empty_like(kbuf)
+        mbuf = torch.empty((n, cap), dtype=torch.bool, device="cuda")  # static padding workspace, as K/V
         outs = [torch.empty((n, 8, 2, 128), dtype=torch.bfloat16, device="cuda") for _ in range(16)]
         dlen = torch.tensor(lens, dtype=torch.int32, device="cuda")
         state = {"lmax": max(lens)}
@@ -722,7 +723,7 @@ def run_configs(args) -> int:
             for layer in range(16):
                 q, k, v = ins[i % pool][layer]
                 rt.append(layer, k, v, slots)
-                kp, vp, _ = rt.gather(layer, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm]))
+                kp, vp, _ = rt.gather(layer, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm]))
                 attend_tensors(q, kp, vp, dlen, 1 / math.sqrt(128), out=outs[layer])
 
         gpu_s = _gpu_timed(c3, steps)

@@ -45,8 +45,20 @@ def _check(code: int, where: str) -> None:
         raise KVRTError(code, where)
 
 
+# Descriptors are a pure function of (data pointer, dtype, shape, strides), so
+# they are cached on that key: a decode loop that reuses its buffers skips the
+# ctypes field writes (~3 us per tensor). The C side reads a descriptor
+# synchronously and never keeps it, and nothing writes one after it is built.
+_DESC_CACHE: dict = {}
+_DESC_CACHE_MAX = 4096
+
+
 def tensor_desc(t: torch.Tensor) -> L.KvrtTensor:
     """Strided descriptor of a device tensor (strides in elements)."""
+    key = (t.data_ptr(), t.dtype, t.shape, t.stride())
+    d = _DESC_CACHE.get(key)
+    if d is not None:
+        return d
     if t.dtype not in _DTYPE_CODES:
         raise TypeError(f"unsupported dtype {t.dtype}")
     if t.dim() > L.KVRT_MAX_RANK:
@@ -58,11 +70,26 @@ def tensor_desc(t: torch.Tensor) -> L.KvrtTensor:
     for i, (n, s) in enumerate(zip(t.shape, t.stride())):
         d.dims[i] = int(n)
         d.strides[i] = int(s)
+    if len(_DESC_CACHE) >= _DESC_CACHE_MAX:
+        _DESC_CACHE.clear()
+    _DESC_CACHE[key] = d
     return d
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def current_stream_handle(device: torch.device) -> int:
+    """The current torch stream of ``device`` as a raw HIP stream handle."""
+    if _RAW_STREAM is not None:  # the handle without building a Stream object
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return int(_RAW_STREAM(idx))
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+# ctypes int32 arrays of slot lists, cached like the descriptors (read-only on
+# the C side).
+_SLOT_ARRAYS: dict = {}
 
 
 def require_cuda(t: torch.Tensor, name: str) -> None:
@@ -279,8 +306,14 @@ class KVRuntime:
 
     @staticmethod
     def _slots(slots: Iterable[int]) -> tuple[ctypes.Array, int]:
-        s = [int(x) for x in slots]
-        return (ctypes.c_int32 * len(s))(*s), len(s)
+        key = tuple(map(int, slots))
+        hit = _SLOT_ARRAYS.get(key)
+        if hit is None:
+            hit = ((ctypes.c_int32 * len(key))(*key), len(key))
+            if len(_SLOT_ARRAYS) >= _DESC_CACHE_MAX:
+                _SLOT_ARRAYS.clear()
+            _SLOT_ARRAYS[key] = hit
+        return hit
 
     def storage(self, layer: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
         """Typed views of a layer's K, V (and INT8 scale) storage."""
@@ -502,7 +535,9 @@ class KVRuntime:
         """Zero-padded batch [n, kv_heads, Lmax, D] (+ mask [n, Lmax]) of n slots.
 
         ``out`` may supply the K and V destinations (strided views with a
-        contiguous last dimension); Lmax is then their third dimension.
+        contiguous last dimension); Lmax is then their third dimension. A third
+        element of ``out`` supplies the mask destination [n, Lmax] (of
+        ``mask_dtype``), which is then returned instead of a new tensor.
         """
         spec = self.layers[self._owner(layer)]
         slots = [int(s) for s in slots]
@@ -516,14 +551,23 @@ class KVRuntime:
                 lens = [min(x, spec.window - 1) for x in lens]
             lmax = max(1, max(lens))
         dt = torch.float32 if spec.dtype == "int8" else torch.bfloat16
+        mask = None
         if out is not None:
-            out_k, out_v = out
+            out_k, out_v = out[0], out[1]
             require_cuda(out_k, "out_k")
             require_cuda(out_v, "out_v")
+            if len(out) > 2 and out[2] is not None:
+                mask = out[2]
+                require_cuda(mask, "out mask")
+                if mask_dtype is not None and mask.dtype != mask_dtype:
+                    raise ValueError(f"out mask dtype {mask.dtype} != mask_dtype {mask_dtype}")
+                if tuple(mask.shape) != (len(slots), lmax):
+                    raise ValueError(f"out mask shape {tuple(mask.shape)} != {(len(slots), lmax)}")
         else:
             out_k = torch.empty((len(slots), spec.kv_heads, lmax, spec.head_dim), dtype=dt, device=self.device)
             out_v = torch.empty_like(out_k)
-        mask = None if mask_dtype is None else torch.empty((len(slots), lmax), dtype=mask_dtype, device=self.device)
+        if mask is None and mask_dtype is not None:
+            mask = torch.empty((len(slots), lmax), dtype=mask_dtype, device=self.device)
         self._bind()
         arr, n = self._slots(slots)
         sp = None if start_pos is None else (ctypes.c_int32 * n)(*[int(x) for x in start_pos])

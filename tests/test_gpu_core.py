@@ -319,6 +319,24 @@ def test_gather_then_attend_tensors_matches_oracle():
         ref = orc.attend(s, 0, to_np(q[i]), 1 / math.sqrt(128))
         assert np.abs(to_np(out[i]) - ref).max() <= ATOL
 
+    # the same gather into caller-owned strided views of larger buffers (a
+    # static padding workspace), mask included: bit-identical, and returned
+    kbuf = torch.full((4, 8, 1100, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    vbuf = torch.full_like(kbuf, -3.0)
+    mbuf = torch.ones((4, 1100), dtype=torch.bool, device="cuda")
+    lm = kpad.shape[2]
+    out3 = (kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm])
+    k2, v2, m2 = rt.gather(0, slots, out=out3)
+    assert m2.data_ptr() == mbuf.data_ptr()
+    np.testing.assert_array_equal(bits(k2), bits(kpad))
+    np.testing.assert_array_equal(bits(v2), bits(vpad))
+    assert torch.equal(m2, mask)
+    assert bool(mbuf[:, lm:].all())  # nothing written past Lmax
+    with pytest.raises(ValueError):
+        rt.gather(0, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm + 1]))
+    with pytest.raises(ValueError):
+        rt.gather(0, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm].float()))
+
 
 def test_copy_prefix_and_copy_rows_bitexact():
     from kvrt import LayerSpec, copy_rows

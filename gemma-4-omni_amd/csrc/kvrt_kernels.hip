@@ -1032,7 +1032,11 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     static_assert(R == 8 || R == 16, "MFMA decode row tiles");
     static_assert(!I8 || LAYOUT == KVRT_LAYOUT_PAGED, "int8 rows are PAGED");
     // the waves' V tiles while streaming, their partials for the merge after
-    constexpr int kTileBytes = kWaves * T * KP * 2, kPartBytes = kWaves * R * D * 4;
+    // partial rows in LDS are PP floats apart: 16 B of padding per row, so the
+    // 16 rows (query columns) of a half-wave's float4 writes start on distinct
+    // banks (with a pitch of D floats they all hit the same ones)
+    constexpr int PP = D + 4;
+    constexpr int kTileBytes = kWaves * T * KP * 2, kPartBytes = kWaves * R * PP * 4;
     __shared__ __align__(16) uint8_t lds_raw[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
     __shared__ float2 lds_ml[kWaves * R];
     uint16_t *sv_all = reinterpret_cast<uint16_t *>(lds_raw);
@@ -1299,7 +1303,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     __syncthreads();  // every wave is done with its V tile
     float *lds_part = reinterpret_cast<float *>(lds_raw);
     if (rvalid) {  // columns >= rows (>= R when R = 8) hold no row of this wave
-        float *dst = lds_part + (wave * R + col) * D + 4 * grp;
+        float *dst = lds_part + (wave * R + col) * PP + 4 * grp;
 #pragma unroll
         for (int b = 0; b < D / 16; ++b)
             *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
@@ -1320,7 +1324,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             const float2 ml = lds_ml[w2 * R + r];
             const float ww = __builtin_amdgcn_exp2f(ml.x - M);
             L = fmaf(ml.y, ww, L);
-            const float *src = lds_part + (w2 * R + r) * D + lane * EPL;
+            const float *src = lds_part + (w2 * R + r) * PP + lane * EPL;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) acc[e] = fmaf(src[e], ww, acc[e]);
         }

@@ -1027,7 +1027,10 @@ __device__ __forceinline__ uint2 i8x4_to_bf16(uint32_t w) {
 template <int D, int R, int LAYOUT, int KDT = KVRT_BF16>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int T = kMfmaDecodeKeys;
-    constexpr int KP = D + 8;  // V tile row pitch (bf16)
+    // V tile row pitch (bf16): rows 32 B apart modulo the 256 B of LDS banks, so
+    // the 4 rows x 4 chunks of 8 B that 16 lanes of a transposed read touch
+    // land on distinct banks (a 16 B shift made rows r and r + 1 overlap)
+    constexpr int KP = D + 16;
     constexpr bool I8 = KDT == KVRT_INT8;
     static_assert(R == 8 || R == 16, "MFMA decode row tiles");
     static_assert(!I8 || LAYOUT == KVRT_LAYOUT_PAGED, "int8 rows are PAGED");

@@ -196,11 +196,23 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // ---------------------------------------------------------------------------
 // gather
 // ---------------------------------------------------------------------------
-// grid (chunks, n_items), 256 threads; thread chunk = 8 elements.
+// grid (ceil(lmax / GatherRows<D>), kv_heads, n_items), 256 threads. A
+// workgroup copies GatherRows<D> padded rows of one (item, head): LPR = D/8
+// lanes per row (8 elements = 16 B each), kGatherUnroll rows per thread, all
+// of whose loads are issued before the first store. Rows past the item's
+// valid length are written as zeros; head 0's workgroups also write the mask
+// entries of their rows. (A flat grid-stride loop over 16-B chunks spent two
+// 64-bit divisions per chunk on the row and head.)
+constexpr int kGatherUnroll = 4;
+template <int D>
+constexpr int gather_rows() { return 256 / (D / 8) * kGatherUnroll; }
 template <int D, int KDT, int LAYOUT>
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     constexpr int LPR = D / 8;
-    const int item = blockIdx.y;
+    constexpr int RPP = 256 / LPR;  // rows per pass of the workgroup
+    constexpr int U = kGatherUnroll;
+    const int item = blockIdx.z;
+    const int h = blockIdx.y;
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     int start;
@@ -208,26 +220,24 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     else if (LAYOUT == KVRT_LAYOUT_RING && a.window > 0) start = max(0, L - (a.window - 1));
     else start = 0;
     const int valid = max(0, L - start);
-    const int64_t chunks = (int64_t)a.kv.kv_heads * a.lmax * LPR;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += step) {
-        const int seg = (int)(c % LPR);
-        const int64_t rowid = c / LPR;
-        const int j = (int)(rowid % a.lmax);
-        const int h = (int)(rowid / a.lmax);
-        const int64_t o = item * a.out_item_stride + h * a.out_head_stride + j * a.out_row_stride + seg * 8;
-        float kf[8], vf[8];
-        uint4 kx = make_uint4(0, 0, 0, 0), vx = make_uint4(0, 0, 0, 0);
+    const int seg = threadIdx.x % LPR;
+    const int j0 = blockIdx.x * (RPP * U) + threadIdx.x / LPR;
+    float kf[U][8], vf[U][8];
+    uint4 kx[U], vx[U];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = vf[i] = 0.f;
-        if (j < valid) {
+    for (int u = 0; u < U; ++u) {
+        kx[u] = vx[u] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[u][i] = vf[u][i] = 0.f;
+        const int j = j0 + u * RPP;
+        if (j < valid && j < a.lmax) {
             int64_t src = row_offset<LAYOUT>(a.kv, slot, h, start + j, D);
             if (LAYOUT == KVRT_LAYOUT_CONTIG && start + j >= a.kv.rows) src = -1;
             if (src < 0) {
                 if (seg == 0) a.err[0] = 1;
             } else if constexpr (KDT == KVRT_BF16) {
-                kx = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.k) + src + seg * 8);
-                vx = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.v) + src + seg * 8);
+                kx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.k) + src + seg * 8);
+                vx[u] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.kv.v) + src + seg * 8);
             } else {
                 const uint2 kq = *reinterpret_cast<const uint2 *>(static_cast<const int8_t *>(a.kv.k) + src + seg * 8);
                 const uint2 vq = *reinterpret_cast<const uint2 *>(static_cast<const int8_t *>(a.kv.v) + src + seg * 8);
@@ -235,33 +245,41 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const uint32_t kw = i < 4 ? kq.x : kq.y, vw = i < 4 ? vq.x : vq.y;
-                    kf[i] = (float)(int8_t)(kw >> (8 * (i & 3))) * ks;
-                    vf[i] = (float)(int8_t)(vw >> (8 * (i & 3))) * vs;
+                    kf[u][i] = (float)(int8_t)(kw >> (8 * (i & 3))) * ks;
+                    vf[u][i] = (float)(int8_t)(vw >> (8 * (i & 3))) * vs;
                 }
             }
         }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = j0 + u * RPP;
+        if (j >= a.lmax) continue;
+        const int64_t o = item * a.out_item_stride + h * a.out_head_stride + j * a.out_row_stride + seg * 8;
         if (a.out_fp32) {
             if constexpr (KDT == KVRT_BF16) {
-                const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w}, vw[4] = {vx.x, vx.y, vx.z, vx.w};
+                const uint32_t kw[4] = {kx[u].x, kx[u].y, kx[u].z, kx[u].w};
+                const uint32_t vw[4] = {vx[u].x, vx[u].y, vx[u].z, vx[u].w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    kf[2 * i] = bf16_lo(kw[i]); kf[2 * i + 1] = bf16_hi(kw[i]);
-                    vf[2 * i] = bf16_lo(vw[i]); vf[2 * i + 1] = bf16_hi(vw[i]);
+                    kf[u][2 * i] = bf16_lo(kw[i]); kf[u][2 * i + 1] = bf16_hi(kw[i]);
+                    vf[u][2 * i] = bf16_lo(vw[i]); vf[u][2 * i + 1] = bf16_hi(vw[i]);
                 }
             }
             float4 *ko = reinterpret_cast<float4 *>(static_cast<float *>(a.out_k) + o);
             float4 *vo = reinterpret_cast<float4 *>(static_cast<float *>(a.out_v) + o);
-            ko[0] = make_float4(kf[0], kf[1], kf[2], kf[3]);
-            ko[1] = make_float4(kf[4], kf[5], kf[6], kf[7]);
-            vo[0] = make_float4(vf[0], vf[1], vf[2], vf[3]);
-            vo[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
+            ko[0] = make_float4(kf[u][0], kf[u][1], kf[u][2], kf[u][3]);
+            ko[1] = make_float4(kf[u][4], kf[u][5], kf[u][6], kf[u][7]);
+            vo[0] = make_float4(vf[u][0], vf[u][1], vf[u][2], vf[u][3]);
+            vo[1] = make_float4(vf[u][4], vf[u][5], vf[u][6], vf[u][7]);
         } else {
-            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_k) + o) = kx;
-            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_v) + o) = vx;
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_k) + o) = kx[u];
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_v) + o) = vx[u];
         }
     }
-    if (a.mask != nullptr) {
-        for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < a.lmax; j += (int)step) {
+    if (a.mask != nullptr && h == 0 && threadIdx.x < RPP * U) {
+        const int j = blockIdx.x * (RPP * U) + threadIdx.x;
+        if (j < a.lmax) {
             const bool ok = j < valid;
             const int64_t mo = item * a.mask_item_stride + j;
             if (a.mask_dtype == KVRT_BOOL) static_cast<uint8_t *>(a.mask)[mo] = ok ? 1 : 0;
@@ -2186,10 +2204,11 @@ hipError_t launch_append(const AppendArgs &a, int head_dim, int dtype, int grid_
 }
 
 hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream_t s) {
-    const int64_t chunks = (int64_t)a.kv.kv_heads * a.lmax * (head_dim / 8);
-    int gx = (int)((chunks + 255) / 256);
-    gx = gx < 1 ? 1 : (gx > 4096 ? 4096 : gx);
-    dim3 grid(gx, a.n_items), block(256);
+    const int rows = head_dim == 64 ? gather_rows<64>() : head_dim == 128 ? gather_rows<128>()
+                   : head_dim == 256 ? gather_rows<256>() : gather_rows<512>();
+    const int gx = (a.lmax + rows - 1) / rows;
+    if (gx < 1 || a.kv.kv_heads < 1 || a.n_items < 1) return hipSuccess;
+    dim3 grid(gx, a.kv.kv_heads, a.n_items), block(256);
     if (dtype == KVRT_INT8) {
         if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
         KVRT_DISPATCH_D(head_dim, hipLaunchKernelGGL((gather_kernel<HD, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a));

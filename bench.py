@@ -580,17 +580,20 @@ def run_configs(args) -> int:
     def host(shape, scale=1.0):
         return (torch.randn(shape, generator=cgen) * scale).to(torch.bfloat16)
 
-    def report(name, desc, tokens, gpu_s, bytes_step, cpu=None, graph_s=None, extra=None):
+    def report(name, desc, tokens, gpu_s, bytes_step, cpu=None, graph_s=None, extra=None, graph_bytes=None,
+               graph_timing="one captured step replayed, host clock around all replays"):
         row = {"config": name, "workload": desc, "tokens_per_step": tokens,
                "gpu": {"ms_per_step": round(gpu_s * 1e3, 4), "tokens_per_s": round(tokens / gpu_s, 1),
                        "algorithmic_bytes_per_step": int(bytes_step),
                        "gbps": round(bytes_step / gpu_s / 1e9, 1), "frac": round(bytes_step / gpu_s / HBM_PEAK, 4),
                        "timing": "eager calls, host clock around all steps"}}
         if graph_s is not None:
+            gb = bytes_step if graph_bytes is None else graph_bytes
             row["gpu_graph"] = {"ms_per_step": round(graph_s * 1e3, 4), "tokens_per_s": round(tokens / graph_s, 1),
-                                "gbps": round(bytes_step / graph_s / 1e9, 1),
-                                "frac": round(bytes_step / graph_s / HBM_PEAK, 4),
-                                "timing": "one captured step replayed, host clock around all replays"}
+                                "algorithmic_bytes_per_step": int(gb),
+                                "gbps": round(gb / graph_s / 1e9, 1),
+                                "frac": round(gb / graph_s / HBM_PEAK, 4),
+                                "timing": graph_timing}
         if cpu is not None:
             cs, n = cpu
             row["cpu_baseline"] = {"ms_per_step": round(cs * 1e3, 3), "tokens_per_s": round(tokens / cs, 2),
@@ -727,6 +730,26 @@ def run_configs(args) -> int:
                 attend_tensors(q, kp, vp, dlen, 1 / math.sqrt(128), out=outs[layer])
 
         gpu_s = _gpu_timed(c3, steps)
+
+        # Shape-stable form (the reference's static padding workspace pads to a
+        # fixed target length, shape_stable_listener.py:28-69): every step
+        # gathers into [n, 8, lt, 128] with lt the longest stream's last length,
+        # so one captured step replays while the device lengths advance.
+        rt.synchronize()
+        for s_, ln in enumerate(lens):
+            rt.truncate(s_, ln)
+        dlen.copy_(torch.tensor(lens, dtype=torch.int32, device="cuda"))
+        lt = max(lens) + 2 * (steps + 1)
+
+        def c3g(i):
+            dlen.add_(2)
+            for layer in range(16):
+                q, k, v = ins[0][layer]
+                rt.append(layer, k, v, slots)
+                kp, vp, _ = rt.gather(layer, slots, out=(kbuf[:, :, :lt], vbuf[:, :, :lt], mbuf[:, :lt]))
+                attend_tensors(q, kp, vp, dlen, 1 / math.sqrt(128), out=outs[layer])
+
+        g3_s = graph_time(rt, c3g, steps)
         sum_l = sum(lens) + n * steps  # mean over the steps (+2 per step, mean +1 ... +2*steps/2)
         lmax_mean = max(lens) + steps
         row = 8 * 128 * 2
@@ -760,9 +783,13 @@ def run_configs(args) -> int:
                                                                      scale=1 / math.sqrt(128))
 
             cpu = _cpu_timed(c3c, steps, budget)
+        b3g = 16 * (2 * row * 2 * n * 2 + 2 * row * sum_l + 2 * row * n * lt + n * lt + 2 * row * sum_l
+                    + 2 * n * 8 * 2 * 128 * 2)  # the padded batch at the fixed target length lt
         report(f"3 (N={n})", f"listener micro-batch: N={n} ragged streams (L0 {lens}), 16 layers, 8 kv heads, "
                "D 128; per step and layer append a Q 2 frame, gather the padded [N, 8, Lmax, 128] batch + mask, "
-               "attend (8 q heads); 500 steps", 2 * n, gpu_s, b3, cpu)
+               "attend (8 q heads); 500 steps", 2 * n, gpu_s, b3, cpu, graph_s=g3_s, graph_bytes=b3g,
+               graph_timing=f"shape-stable: the padded batch at a fixed target length {lt} (static padding "
+                            "workspace), one captured step replayed, host clock around all replays")
         rt.close()
 
     # ---- config 4: talker, 28 layers, Hq 16 / Hkv 8, D 128, 4 sessions, rollback every 25 steps --

@@ -28,6 +28,12 @@ HIPCC_FLAGS = [
     # Packed FP32 VALU forms are kept out of every code object.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # MFMA accumulators live in ordinary VGPRs. With the default AGPR form the
+    # prefill tile loop copied its output accumulators between the two
+    # register files every tile (72 v_accvgpr moves per 32-key tile at D 128);
+    # the VGPR form drops them and raises occupancy of several decode and
+    # prefill instantiations (talker prefill 26.4 -> 23.8 us per launch).
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-function",
     # flowing off the end of a value-returning function is undefined (a

@@ -65,6 +65,9 @@ def parse() -> argparse.Namespace:
                    help="kernel for bf16 decodes of 8 or 16 query rows per kv head (kvrt_config.decode_kernel)")
     p.add_argument("--decode-merge", choices=("auto", "separate", "last_wg"), default="auto",
                    help="how split-K decodes merge their partials (kvrt_config.decode_merge)")
+    p.add_argument("--talker-hq", type=int, default=TALKER["hq"],
+                   help="q heads of the talker (default 16: Hq 16 / Hkv 8, 2 rows per KV head); 8 or 32 time the "
+                        "same K/V bytes at 1 or 4 rows per KV head")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 = skip)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run one 256 MiB device copy (HBM counter calibration for rocprofv3 --pmc)")
@@ -954,6 +957,10 @@ def main() -> int:
         return run_kernels(args)
     if args.mode == "configs":
         return run_configs(args)
+    if args.talker_hq <= 0 or args.talker_hq % TALKER["hkv"] or args.talker_hq // TALKER["hkv"] > 16:
+        print(f"--talker-hq must be a multiple of {TALKER['hkv']} up to {16 * TALKER['hkv']}", file=sys.stderr)
+        return 2
+    TALKER["hq"] = args.talker_hq
     gen = torch.Generator(device="cuda").manual_seed(1)
     margin = args.warmup + args.steps + 2 * args.kernel_reps + 8
     capacity = args.ctx + margin
@@ -1038,7 +1045,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": "north-star step: 4 streams x (thinker 30L [25 ring-512 + 5 global] Hq8/Hkv1 D256 "
-                        "+ talker 28L Hq16/Hkv8 D128), 1 token append + GQA decode per layer, bf16",
+                        f"+ talker 28L Hq{TALKER['hq']}/Hkv8 D128), 1 token append + GQA decode per layer, bf16",
             "streams": args.streams,
             "context_first_step": len0 + 1,
             "context_last_step": len1,

@@ -57,9 +57,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--one-stream", action="store_true",
                    help="run every launch on the caller's stream (default: one stream per model and group)")
     p.add_argument("--kernel-reps", type=int, default=50, help="event-timed repetitions of the dominant kernel (a layer sequence, and one launch alone)")
-    p.add_argument("--talker-wgs", type=int, default=192,
+    p.add_argument("--talker-wgs", type=int, default=224,
                    help="split-K decode workgroups per talker launch (kvrt_config.decode_wgs)")
-    p.add_argument("--thinker-wgs", type=int, default=192,
+    p.add_argument("--thinker-wgs", type=int, default=160,
                    help="split-K decode workgroups per thinker launch (kvrt_config.decode_wgs)")
     p.add_argument("--decode-kernel", choices=("auto", "valu", "mfma"), default="auto",
                    help="kernel for bf16 decodes of 8 or 16 query rows per kv head (kvrt_config.decode_kernel)")
@@ -213,7 +213,8 @@ def time_dominant_kernel(model: Model, reps: int) -> dict:
     n_layers = len(model.bufs)
     seq, single = [], []
     bytes_total = 0
-    launches0 = model.rt.counters()["launches"]
+    c0 = model.rt.counters()
+    launches0 = c0["launches"]
     for _ in range(reps):
         L_before = model.rt.seq_length(0, 0)
         torch.cuda._sleep(20_000_000)
@@ -225,7 +226,9 @@ def time_dominant_kernel(model: Model, reps: int) -> dict:
         e1.synchronize()
         seq.append(e0.elapsed_time(e1) * 1e-3 / n_layers)
         bytes_total += step_bytes(len(model.slots), L_before + 1)["talker_layer"]
-    launches = (model.rt.counters()["launches"] - launches0) // (reps * n_layers)
+    c1 = model.rt.counters()
+    launches = (c1["launches"] - launches0) // (reps * n_layers)
+    mfma = c1["mfma_decodes"] - c0["mfma_decodes"] == reps * n_layers
     q, k, v, o = model.bufs[0]
     for _ in range(reps):
         torch.cuda._sleep(2_000_000)
@@ -237,7 +240,7 @@ def time_dominant_kernel(model: Model, reps: int) -> dict:
         e1.synchronize()
         single.append(e0.elapsed_time(e1) * 1e-3)
     return {"time": central_mean(seq), "bytes": bytes_total // reps, "launches": launches,
-            "single": central_mean(single)}
+            "single": central_mean(single), "mfma": mfma}
 
 
 def pmc_traffic() -> dict | None:
@@ -463,10 +466,15 @@ def run_kernels(args) -> int:
             fn = lambda: rt.append_attend(0, q, kn, vn, slots, sc, out=o)  # noqa: E731
         else:
             fn = lambda: rt.attend(0, q, slots, sc, out=o)  # noqa: E731
-        l0 = rt.counters()["launches"]
+        c0 = rt.counters()
         t = _event_median(fn, w, r)
-        if rt.counters()["launches"] - l0 > w + r:  # the decode did not merge its own partials
+        c1 = rt.counters()
+        if c1["launches"] - c0["launches"] > w + r:  # the decode did not merge its own partials
             kernel += " + merge_kernel"
+        if kernel.startswith("decode_kernel") and c1["mfma_decodes"] - c0["mfma_decodes"] == w + r:
+            raise RuntimeError(f"kernel case {name}: expected the VALU decode, AUTO chose the MFMA kernel")
+        if kernel.startswith("decode_mfma") and c1["mfma_decodes"] - c0["mfma_decodes"] != w + r:
+            raise RuntimeError(f"kernel case {name}: expected the MFMA decode, AUTO chose the VALU kernel")
         if rt.health() != 0:
             raise RuntimeError(f"kvrt health check failed in kernel case {name}")
         row = hkv * d * (1 if dtype == "int8" else 2) + (hkv * 4 if dtype == "int8" else 0)  # K or V bytes per position
@@ -480,7 +488,7 @@ def run_kernels(args) -> int:
 
     # the north-star step's talker and thinker launches at the step's workgroup targets; the
     # other shapes at the runtime default (kvrt_config.decode_wgs = 0)
-    decode_case("decode_talker", "decode_kernel<128,2,bf16,contig> (LDS DMA ring)", 16, 8, 128, 4, 4096,
+    decode_case("decode_talker", "decode_mfma_kernel<128,8,contig> (2 rows, LDS DMA ring)", 16, 8, 128, 4, 4096,
                 wgs=args.talker_wgs)
     decode_case("decode_thinker_global", "decode_mfma_kernel<256,8,contig>", 8, 1, 256, 4, 4096,
                 wgs=args.thinker_wgs)
@@ -1020,6 +1028,8 @@ def main() -> int:
     tokens_per_step = 2 * args.streams
     dom = time_dominant_kernel(talker0, args.kernel_reps)
     k_time, k_bytes, k_launches = dom["time"], dom["bytes"], dom["launches"]
+    k_name = ("kvrt::decode_mfma_kernel<128,8,contig> (2 rows in an 8-row tile, LDS DMA ring)" if dom["mfma"]
+              else "kvrt::decode_kernel<128,2,bf16,contig>")
     if talker0.rt.health() != 0:
         raise RuntimeError("kvrt health check failed after the kernel timing")
     achieved = k_bytes / k_time
@@ -1063,8 +1073,8 @@ def main() -> int:
         "step_algorithmic_bytes": total_bytes // args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"talker layer attention, {n} streams, fused append: kvrt::decode_kernel<128,2,bf16,contig>"
-                      + (" + kvrt::merge_kernel<128,2,1>" if k_launches > 1 else " (merges its own partials)")
+            "kernel": f"talker layer attention, {n} streams, fused append: {k_name}"
+                      + (" + merge kernel" if k_launches > 1 else " (merges its own partials)")
                       + " (one kvrt_append_attend_async call)",
             "launches_per_call": k_launches,
             "achieved": round(achieved / 1e9, 1),

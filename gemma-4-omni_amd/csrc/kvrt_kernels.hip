@@ -1042,6 +1042,23 @@ __device__ __forceinline__ uint2 i8x4_to_bf16(uint32_t w) {
                       pack_bf16x2((float)(int8_t)(w >> 16), (float)(int8_t)(w >> 24)));
 }
 
+// Stages per wave of the MFMA decode's LDS DMA ring (mfma_decode_dma): two
+// at D 128 (72 KB per workgroup; 3 and 4 stages, 104 and 136 KB, lengthened
+// the two-stream step: 0.555 and 0.584 vs 0.542 ms), two at D 256.
+#ifndef KVRT_MFMA_DMA_STAGES_128
+#define KVRT_MFMA_DMA_STAGES_128 2
+#endif
+#ifndef KVRT_MFMA_DMA_STAGES_256
+#define KVRT_MFMA_DMA_STAGES_256 2
+#endif
+// Chunk swizzle of the MFMA decode's DMA tiles: the logical 16-byte chunk c
+// of tile row r sits at chunk c ^ mfma_dswz(r), a permutation of the low 4
+// bits that keeps bit 0 clear on rows 0-7. The K A-operand reads (16 rows,
+// one chunk each, per 16 lanes) and the V^T transposed reads (4 rows x 2
+// chunks x 2 halves per 16 lanes, 32 lanes per pass) then hit distinct
+// banks (rows are 256 or 512 B: every row starts on bank 0).
+__device__ __forceinline__ int mfma_dswz(int r) { return (2 * (r & 7)) ^ ((r >> 3) & 1); }
+
 template <int D, int R, int LAYOUT, int KDT = KVRT_BF16>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int T = kMfmaDecodeKeys;
@@ -1058,7 +1075,18 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     // banks (with a pitch of D floats they all hit the same ones)
     constexpr int PP = D + 4;
     constexpr int kTileBytes = kWaves * T * KP * 2, kPartBytes = kWaves * R * PP * 4;
-    __shared__ __align__(16) uint8_t lds_raw[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
+    // DMA ring: per wave a copy of the tile's q rows (QB) and NSTG stages of
+    // a K and a V tile (TB each), NSTG - 1 tiles in flight while one computes
+    constexpr bool DMA = R == 8 && mfma_decode_dma(D, R, KDT, LAYOUT);
+    constexpr int NSTG = D == 128 ? KVRT_MFMA_DMA_STAGES_128 : KVRT_MFMA_DMA_STAGES_256;
+    constexpr int TB = T * D * 2, QB = R * D * 2;
+    constexpr int DPT = 2 * TB / 1024;  // DMA instructions per tile (K and V)
+    constexpr int kRingBytes = DMA ? kWaves * (QB + NSTG * 2 * TB) : 0;
+    static_assert(!DMA || (NSTG >= 1 && DPT * NSTG < 64 && kRingBytes + kWaves * R * 8 <= 160 * 1024),
+                  "DMA ring: outstanding loads fit vmcnt, the rings fit LDS");
+    constexpr int kLdsBytes = kTileBytes > kPartBytes ? (kTileBytes > kRingBytes ? kTileBytes : kRingBytes)
+                                                      : (kPartBytes > kRingBytes ? kPartBytes : kRingBytes);
+    __shared__ __align__(16) uint8_t lds_raw[kLdsBytes];
     __shared__ float2 lds_ml[kWaves * R];
     uint16_t *sv_all = reinterpret_cast<uint16_t *>(lds_raw);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1121,7 +1149,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const int hq = hkv * a.group;
     const bool rvalid = col < rows;
     uint4 qop[D / 32];
-    {
+    if constexpr (!DMA) {
         // every lane loads (rows past the tile's real rows read row 0), then
         // those lanes zero their operand: no branch around the loads
         const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
@@ -1218,6 +1246,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             }
         }
     };
+    if constexpr (!DMA) {
     // Software pipeline over the wave's tiles: tile t + 1's K is loaded into
     // the A-operand registers as soon as tile t's S MFMAs have read them, and
     // its V as soon as tile t's V is in LDS, so both are in flight during tile
@@ -1316,6 +1345,110 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     int t0 = ws;
     for (; t0 + T < we; t0 += T) tile(t0, std::true_type{});
     if (t0 < we) tile(t0, std::false_type{});
+    } else {
+    // LDS DMA ring: each wave streams its q rows and then its 16-key K and V
+    // tiles into its own LDS with global_load_lds_dwordx4 (16 B per lane,
+    // 1 KiB = RPI rows per instruction; lane l fetches the logical chunk that
+    // lands at chunk l % CPR of its row, see mfma_dswz), NSTG stages deep, so
+    // that NSTG - 1 tiles stay in flight while one is computed and no
+    // register holds them. The DMAs are invisible to the compiler's wait
+    // counts: every wait is an explicit vmcnt on the wave's own DMAs, which
+    // complete in issue order (q, tile 0, tile 1, ...). Rows past the wave's
+    // range read row ws and are masked; fused rows come from k_new / v_new.
+    constexpr int CPR = D / 8;     // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;  // rows per DMA instruction
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t ring = lds_addr(lds_raw) + wave_u * (kRingBytes / kWaves);
+    const uint8_t *ring_p = lds_raw + wave_u * (kRingBytes / kWaves);
+    const int ntiles = __builtin_amdgcn_readfirstlane(we > ws ? (we - ws + T - 1) / T : 0);
+    auto dma_tile = [&](int j, int st) __attribute__((always_inline)) {
+        const uint32_t kd = __builtin_amdgcn_readfirstlane(ring + QB + st * 2 * TB);
+#pragma unroll
+        for (int i = 0; i < TB / 1024; ++i) {
+            const int row = RPI * i + lane / CPR;
+            const int lc = (lane % CPR) ^ mfma_dswz(row);
+            const uint16_t *kp, *vp;
+            key_rows(ws + j * T + row, kp, vp);
+            dma_load16(kp + 8 * lc, kd + i * 1024);
+            dma_load16(vp + 8 * lc, kd + TB + i * 1024);
+        }
+    };
+    {
+        // q rows of the tile (rows past the real ones read row 0 and are
+        // zeroed below), swizzled like the K tiles
+#pragma unroll
+        for (int i = 0; i < QB / 1024; ++i) {
+            const int row = RPI * i + lane / CPR;
+            const int lc = (lane % CPR) ^ mfma_dswz(row);
+            const int rq = row < rows ? row : 0;
+            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + rq / Qn) * Qn + rq % Qn) * D;
+            dma_load16(qp + 8 * lc, __builtin_amdgcn_readfirstlane(ring + i * 1024));
+        }
+    }
+    const int pro = min(NSTG, ntiles);
+    for (int j = 0; j < pro; ++j) dma_tile(j, j);
+    wait_vmem_steps<DPT, NSTG>(pro);  // q has landed
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+        const int r8 = col & 7;  // columns >= R read row col - 8 and are zeroed
+        qop[c] = *reinterpret_cast<const uint4 *>(ring_p + r8 * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(r8)));
+        if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
+    }
+    const int vrow = 4 * grp + (col >> 2);  // this lane's V^T read row
+    for (int j = 0; j < ntiles; ++j) {
+        const int st = j % NSTG;
+        wait_vmem_steps<DPT, NSTG - 1>(min(NSTG - 1, ntiles - 1 - j));
+        const uint8_t *kst = ring_p + QB + st * 2 * TB, *vst = kst + TB;
+        uint4 kop[KR];
+        uint2 vop[D / 16];
+#pragma unroll
+        for (int c = 0; c < KR; ++c)
+            kop[c] = *reinterpret_cast<const uint4 *>(kst + col * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(col)));
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b)
+            vop[b] = lds_read_tr16(reinterpret_cast<const uint16_t *>(
+                vst + vrow * (D * 2) + 16 * ((2 * b + ((col & 3) >> 1)) ^ mfma_dswz(vrow)) + 8 * (col & 1)));
+        wait_lds();  // the stage is in registers: refill it
+        if (j + NSTG < ntiles) dma_tile(j + NSTG, st);
+        const int t0 = ws + j * T;
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < KR; ++c) s = mfma16(kop[c], qop[c], s);
+        float sc[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int key = t0 + 4 * grp + v;
+            const bool vis = key < we && key <= hi && key >= lo;
+            sc[v] = vis ? s[v] * a.scale_log2 : -INFINITY;
+        }
+        if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int key = t0 + 4 * grp + v;
+                sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
+        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+        lazy_rescale<D / 16>(tmax, m, l, o);
+        float p[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
+            l += p[v];
+        }
+        // P = P_hi + P_lo in bf16, as in the register-staged tiles
+        const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
+        const uint2 ph = make_uint2(h01, h23);
+        const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
+                                    pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) o[b] = mfma16k16(vop[b], pl, mfma16k16(vop[b], ph, o[b]));
+    }
+    wait_vmem<0>();  // every DMA of the wave has landed before the LDS is reused
+    }
     if (bad) a.err[0] = 1;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));
     // Workgroup merge: every wave puts its partial in LDS (over the tiles);

@@ -243,21 +243,31 @@ constexpr int kMaxWgPerHead = 64;
 
 // Which bf16 decodes run on the MFMA kernel (kvrt_config.decode_kernel).
 // AUTO (bf16): 16 query rows per kv head (GQA group 8 with Q = 2), 8 rows at
-// head_dim 512, and 8 rows at head_dim <= 256 over at least
-// kMfmaDecodeMinKeys8 visible keys — the shapes where the VALU kernel's dot
-// products and P.V products make it compute-bound. Short 8-row decodes (a
+// head_dim 512, 8 rows at head_dim <= 256 over at least kMfmaDecodeMinKeys8
+// visible keys, and 1-4 rows over as many keys where the tiles stream through
+// the LDS DMA ring (mfma_decode_dma) — the shapes where the VALU kernel's
+// dot products and P.V products make it compute-bound. Short 8-row decodes (a
 // 512-key sliding window) stay on the VALU kernel: latency-bound either way,
 // and lighter on a concurrent stream. `keys` is the launch's key count
 // rounded up to the split bucket, so the choice, like the split count, stays
 // fixed within a bucket.
 constexpr int64_t kMfmaDecodeMinKeys8 = 2048;
-bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t keys) {
+bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t keys, int layout) {
     if (mode == KVRT_DECODE_VALU) return false;
     // int8 (PAGED): AUTO keeps the VALU kernel; its page-window lookups and
     // 16 keys per pass in 4 waves per SIMD beat the MFMA kernel's one 16-key
     // tile in flight per wave at this row size (config 5: 32.6 vs 44.5 us)
     if (dtype == KVRT_INT8) return mode == KVRT_DECODE_MFMA;
-    if (rows_tile_ < kMfmaDecodeMinRows) return false;
+    if (rows_tile_ < kMfmaDecodeMinRows) {
+        // 1-4 rows (the talker's 2) ride an 8-row tile: AUTO takes it where
+        // the tiles stream through the LDS DMA ring, over as many keys as the
+        // 8-row rule (talker launch 19.2 -> 17.8 us, step 0.565 -> 0.542 ms);
+        // KVRT_MFMA_SMALL_ROWS=0 keeps them on the VALU kernel
+        static const char *env = std::getenv("KVRT_MFMA_SMALL_ROWS");
+        static const bool small = !env || std::atoi(env) != 0;
+        return mode == KVRT_DECODE_MFMA ||
+               (small && mfma_decode_dma(head_dim, rows_tile_, dtype, layout) && keys >= kMfmaDecodeMinKeys8);
+    }
     return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512 || keys >= kMfmaDecodeMinKeys8;
 }
 
@@ -703,7 +713,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int64_t bucket_keys = (max_keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket;
     const PrefixMask *pmask = talker ? nullptr : launch_masks(c, n, slots);
     // the MFMA kernel's PAGED D 512 variant has no registers for a mask
-    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys) &&
+    const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys, s.layout) &&
                       !(pmask && s.layout == KVRT_LAYOUT_PAGED && D >= 512);
     const int n_split = choose_splits(target_wgs(c->cfg, mfma ? KVRT_BF16 : s.dtype), n, hkv, max_keys,
                                       mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
@@ -746,6 +756,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     std::stable_sort(ord.begin(), ord.end(), [&](int x, int y) { return item_keys[x] > item_keys[y]; });
     for (int i = 0; i < n; ++i) a.order[i] = (uint8_t)ord[i];
     c->counters.launches += a.cnt ? 1 : 2;
+    c->counters.mfma_decodes += mfma ? 1 : 0;
     if (talker) {
         TalkerArgs t{};
         static_cast<DecodeArgs &>(t) = a;
@@ -933,7 +944,7 @@ int tensor_call_setup(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_ten
     const int R = rows_tile(rows);
     const int64_t keys = window > 0 ? std::min<int64_t>(lmax, window + qn - 1) : lmax;
     tc.mfma = use_mfma_decode(KVRT_DECODE_AUTO, KVRT_BF16, R, (int)D,
-                              (keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket);
+                              (keys + kSplitKeyBucket - 1) / kSplitKeyBucket * kSplitKeyBucket, KVRT_LAYOUT_CONTIG);
     a.n_split = choose_splits(target, (int)n, (int)hkv, keys,
                               tc.mfma ? kMfmaDecodeKeys : keys_per_iteration((int)D, R, KVRT_BF16, KVRT_LAYOUT_CONTIG));
     a.n_parts = (tc.mfma || decode_wg_merge((int)D, R)) ? a.n_split / kWaves : a.n_split;

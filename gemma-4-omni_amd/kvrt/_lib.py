@@ -115,6 +115,7 @@ class KvrtCounters(ctypes.Structure):
         ("truncated_rows", c_uint64),
         ("pages_in_use", c_uint64),
         ("pages_evicted", c_uint64),
+        ("mfma_decodes", c_uint64),
     ]
 
 

@@ -181,6 +181,7 @@ typedef struct kvrt_counters {
     uint64_t truncated_rows;
     uint64_t pages_in_use;
     uint64_t pages_evicted;
+    uint64_t mfma_decodes;      /* decode launches on the MFMA kernel (the rest on VALU) */
 } kvrt_counters;
 
 typedef struct kvrt_ctx kvrt_ctx;

@@ -76,7 +76,7 @@ int main(void) {
   F(kvrt_counters, launches); F(kvrt_counters, appended_rows); F(kvrt_counters, appended_bytes);
   F(kvrt_counters, attended_keys); F(kvrt_counters, attended_bytes); F(kvrt_counters, gathered_bytes);
   F(kvrt_counters, truncations); F(kvrt_counters, truncated_rows); F(kvrt_counters, pages_in_use);
-  F(kvrt_counters, pages_evicted);
+  F(kvrt_counters, pages_evicted); F(kvrt_counters, mfma_decodes);
   F(kvrt_talker_mask, prefix_start); F(kvrt_talker_mask, audio_start); F(kvrt_talker_mask, prefix_position);
   F(kvrt_talker_mask, audio_position); F(kvrt_talker_mask, prefix_attention_mode);
   F(kvrt_talker_mask, visible_prefix_count); F(kvrt_talker_mask, prefix_log_gate);

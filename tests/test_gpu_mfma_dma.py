@@ -1,0 +1,65 @@
+"""GPU parity of the MFMA decode's LDS DMA ring (bf16 CONTIG / RING, D 128,
+1, 2, 4 or 8 query rows per KV head over >= 2048 keys, the shapes AUTO sends
+to it) against the oracle at max-abs 1e-2, beside the same launches forced
+onto the VALU kernel: wave ranges of many tiles, of one or two tiles and
+empty ones (decode_wgs 8 / 64 / 512), partial last tiles, fused appends and a
+canonical prefix mask on one slot."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from tests.helpers import randn_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+ATOL = 1e-2
+
+
+@pytest.mark.parametrize("wgs", [8, 64, 512])
+@pytest.mark.parametrize("layout", ["contig", "ring"])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_mfma_dma_decode_parity(group, layout, wgs):
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(100 * group + wgs + len(layout))
+    hkv, d = 2, 128
+    window = 2304 if layout == "ring" else 0
+    ring = dict(ring_rows=window) if layout == "ring" else {}
+    spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window, **ring)
+    rts = {kern: KVRuntime([spec], 3, 4200, max_q=1, decode_wgs=wgs, decode_kernel=kern, device="cuda")
+           for kern in ("auto", "valu")}
+    orc = O.OracleCache([O.OracleLayer(hkv, d, window)], 3)
+    lens = [2100, 4097, 3001]
+    for s, n in enumerate(lens):
+        k, v = randn_bf16(gen, (1, hkv, n, d)), randn_bf16(gen, (1, hkv, n, d))
+        for rt in rts.values():
+            rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    mask = O.canonical_prefix_mask(34)
+    for rt in rts.values():
+        rt.set_prefix_attention(1, torch.from_numpy(mask).cuda())
+    orc.set_prefix_attention(1, mask)
+    slots = [0, 1, 2]
+    before = {name: rt.counters()["mfma_decodes"] for name, rt in rts.items()}
+    worst = {name: 0.0 for name in rts}
+    for _ in range(3):
+        q = randn_bf16(gen, (3, hkv * group, 1, d), 1.0 / math.sqrt(d))
+        k, v = randn_bf16(gen, (3, hkv, 1, d)), randn_bf16(gen, (3, hkv, 1, d))
+        outs = {name: rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), slots, 1.0) for name, rt in rts.items()}
+        torch.cuda.synchronize()
+        for i, s in enumerate(slots):
+            orc.append(s, 0, to_np(k[i]), to_np(v[i]))
+            ref = orc.attend(s, 0, to_np(q[i]), 1.0)
+            for name, out in outs.items():
+                worst[name] = max(worst[name], float(np.abs(to_np(out[i]) - ref).max()))
+    assert max(worst.values()) <= ATOL, worst
+    # AUTO ran every launch on the MFMA kernel, the forced VALU runtime none
+    assert rts["auto"].counters()["mfma_decodes"] - before["auto"] == 3
+    assert rts["valu"].counters()["mfma_decodes"] - before["valu"] == 0
+    for rt in rts.values():
+        assert rt.health() == 0
+        assert [rt.seq_length(s, 0) for s in slots] == [n + 3 for n in lens]

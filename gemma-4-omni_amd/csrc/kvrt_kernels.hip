@@ -1247,207 +1247,207 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         }
     };
     if constexpr (!DMA) {
-    // Software pipeline over the wave's tiles: tile t + 1's K is loaded into
-    // the A-operand registers as soon as tile t's S MFMAs have read them, and
-    // its V as soon as tile t's V is in LDS, so both are in flight during tile
-    // t's softmax and P.V.
-    // (PAGED at D 512 keeps one tile in flight: the page lookups of a second
-    // tile do not fit the registers.)
-    constexpr bool PIPE = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
-    uint4 ka[KR], vt[VR];
-    float ksl = 0.f, vsl = 0.f;  // int8: scales of key t0 + col
-    if (PIPE && ws < we) {
-        load_k(ws, ka, ksl, vsl);
-        load_v(ws, vt);
-    }
-    // The loop runs the tiles that have a successor with unconditional loads
-    // of the next tile (a conditional load would make the compiler's wait
-    // counts assume it may be missing, and wait on the next tile's first load
-    // before storing this tile's V); the last tile is peeled.
-    auto tile = [&](int t0, auto more_c) __attribute__((always_inline)) {
-        constexpr bool more = PIPE && decltype(more_c)::value;
-        if constexpr (!PIPE) {
-            load_k(t0, ka, ksl, vsl);
-            load_v(t0, vt);
+        // Software pipeline over the wave's tiles: tile t + 1's K is loaded into
+        // the A-operand registers as soon as tile t's S MFMAs have read them, and
+        // its V as soon as tile t's V is in LDS, so both are in flight during tile
+        // t's softmax and P.V.
+        // (PAGED at D 512 keeps one tile in flight: the page lookups of a second
+        // tile do not fit the registers.)
+        constexpr bool PIPE = !(LAYOUT == KVRT_LAYOUT_PAGED && D >= 512);
+        uint4 ka[KR], vt[VR];
+        float ksl = 0.f, vsl = 0.f;  // int8: scales of key t0 + col
+        if (PIPE && ws < we) {
+            load_k(ws, ka, ksl, vsl);
+            load_v(ws, vt);
         }
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        float ksv[4], vsv[4];  // int8: K and V scales of this lane's keys t0 + 4grp + v
-        if constexpr (I8) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                ksv[v] = __shfl(ksl, 4 * grp + v);
-                vsv[v] = __shfl(vsl, 4 * grp + v);
+        // The loop runs the tiles that have a successor with unconditional loads
+        // of the next tile (a conditional load would make the compiler's wait
+        // counts assume it may be missing, and wait on the next tile's first load
+        // before storing this tile's V); the last tile is peeled.
+        auto tile = [&](int t0, auto more_c) __attribute__((always_inline)) {
+            constexpr bool more = PIPE && decltype(more_c)::value;
+            if constexpr (!PIPE) {
+                load_k(t0, ka, ksl, vsl);
+                load_v(t0, vt);
             }
-#pragma unroll
-            for (int c2 = 0; c2 < KR; ++c2) {
-                const uint2 a0 = i8x4_to_bf16(ka[c2].x), a1 = i8x4_to_bf16(ka[c2].y);
-                const uint2 a2 = i8x4_to_bf16(ka[c2].z), a3 = i8x4_to_bf16(ka[c2].w);
-                s = mfma16(make_uint4(a0.x, a0.y, a1.x, a1.y), qop[2 * c2], s);
-                s = mfma16(make_uint4(a2.x, a2.y, a3.x, a3.y), qop[2 * c2 + 1], s);
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < KR; ++c) s = mfma16(ka[c], qop[c], s);
-        }
-        if constexpr (more) load_k(t0 + T, ka, ksl, vsl);
-#pragma unroll
-        for (int i = 0; i < VR; ++i) {
-            const int u = lane + 64 * i;
+            f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            float ksv[4], vsv[4];  // int8: K and V scales of this lane's keys t0 + 4grp + v
             if constexpr (I8) {
-                const uint2 b0 = i8x4_to_bf16(vt[i].x), b1 = i8x4_to_bf16(vt[i].y);
-                const uint2 b2 = i8x4_to_bf16(vt[i].z), b3 = i8x4_to_bf16(vt[i].w);
-                uint4 *dst = reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 16 * (u % VU));
-                dst[0] = make_uint4(b0.x, b0.y, b1.x, b1.y);
-                dst[1] = make_uint4(b2.x, b2.y, b3.x, b3.y);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    ksv[v] = __shfl(ksl, 4 * grp + v);
+                    vsv[v] = __shfl(vsl, 4 * grp + v);
+                }
+#pragma unroll
+                for (int c2 = 0; c2 < KR; ++c2) {
+                    const uint2 a0 = i8x4_to_bf16(ka[c2].x), a1 = i8x4_to_bf16(ka[c2].y);
+                    const uint2 a2 = i8x4_to_bf16(ka[c2].z), a3 = i8x4_to_bf16(ka[c2].w);
+                    s = mfma16(make_uint4(a0.x, a0.y, a1.x, a1.y), qop[2 * c2], s);
+                    s = mfma16(make_uint4(a2.x, a2.y, a3.x, a3.y), qop[2 * c2 + 1], s);
+                }
             } else {
-                *reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 8 * (u % VU)) = vt[i];
-            }
-        }
-        if constexpr (more) load_v(t0 + T, vt);
-        // this lane: keys t0 + 4grp + v of row col
-        float sc[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int key = t0 + 4 * grp + v;
-            const bool vis = key < we && key <= hi && key >= lo;
-            sc[v] = vis ? (I8 ? s[v] * ksv[v] : s[v]) * a.scale_log2 : -INFINITY;
-        }
-        if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+                for (int c = 0; c < KR; ++c) s = mfma16(ka[c], qop[c], s);
+            }
+            if constexpr (more) load_k(t0 + T, ka, ksl, vsl);
+#pragma unroll
+            for (int i = 0; i < VR; ++i) {
+                const int u = lane + 64 * i;
+                if constexpr (I8) {
+                    const uint2 b0 = i8x4_to_bf16(vt[i].x), b1 = i8x4_to_bf16(vt[i].y);
+                    const uint2 b2 = i8x4_to_bf16(vt[i].z), b3 = i8x4_to_bf16(vt[i].w);
+                    uint4 *dst = reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 16 * (u % VU));
+                    dst[0] = make_uint4(b0.x, b0.y, b1.x, b1.y);
+                    dst[1] = make_uint4(b2.x, b2.y, b3.x, b3.y);
+                } else {
+                    *reinterpret_cast<uint4 *>(sv + (u / VU) * KP + 8 * (u % VU)) = vt[i];
+                }
+            }
+            if constexpr (more) load_v(t0 + T, vt);
+            // this lane: keys t0 + 4grp + v of row col
+            float sc[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int key = t0 + 4 * grp + v;
-                sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+                const bool vis = key < we && key <= hi && key >= lo;
+                sc[v] = vis ? (I8 ? s[v] * ksv[v] : s[v]) * a.scale_log2 : -INFINITY;
             }
-        }
-        float tmax = -INFINITY;
+            if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
-        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
-        lazy_rescale<D / 16>(tmax, m, l, o);
-        float p[4];
+                for (int v = 0; v < 4; ++v) {
+                    const int key = t0 + 4 * grp + v;
+                    sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+                }
+            }
+            float tmax = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
-            l += p[v];
-            if constexpr (I8) p[v] *= vsv[v];  // dequantise V through P
-        }
-        // P = P_hi + P_lo in bf16 (as in the prefill kernel)
-        const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
-        const uint2 ph = make_uint2(h01, h23);
-        const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
-                                    pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
+            for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
+            tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+            lazy_rescale<D / 16>(tmax, m, l, o);
+            float p[4];
 #pragma unroll
-        for (int b = 0; b < D / 16; ++b) {
-            const uint2 va = lds_read_tr16(sv_lane + 16 * b);
-            o[b] = mfma16k16(va, pl, mfma16k16(va, ph, o[b]));
-        }
-    };
-    int t0 = ws;
-    for (; t0 + T < we; t0 += T) tile(t0, std::true_type{});
-    if (t0 < we) tile(t0, std::false_type{});
+            for (int v = 0; v < 4; ++v) {
+                p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
+                l += p[v];
+                if constexpr (I8) p[v] *= vsv[v];  // dequantise V through P
+            }
+            // P = P_hi + P_lo in bf16 (as in the prefill kernel)
+            const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
+            const uint2 ph = make_uint2(h01, h23);
+            const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
+                                        pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b) {
+                const uint2 va = lds_read_tr16(sv_lane + 16 * b);
+                o[b] = mfma16k16(va, pl, mfma16k16(va, ph, o[b]));
+            }
+        };
+        int t0 = ws;
+        for (; t0 + T < we; t0 += T) tile(t0, std::true_type{});
+        if (t0 < we) tile(t0, std::false_type{});
     } else {
-    // LDS DMA ring: each wave streams its q rows and then its 16-key K and V
-    // tiles into its own LDS with global_load_lds_dwordx4 (16 B per lane,
-    // 1 KiB = RPI rows per instruction; lane l fetches the logical chunk that
-    // lands at chunk l % CPR of its row, see mfma_dswz), NSTG stages deep, so
-    // that NSTG - 1 tiles stay in flight while one is computed and no
-    // register holds them. The DMAs are invisible to the compiler's wait
-    // counts: every wait is an explicit vmcnt on the wave's own DMAs, which
-    // complete in issue order (q, tile 0, tile 1, ...). Rows past the wave's
-    // range read row ws and are masked; fused rows come from k_new / v_new.
-    constexpr int CPR = D / 8;     // 16-byte chunks per row
-    constexpr int RPI = 64 / CPR;  // rows per DMA instruction
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const uint32_t ring = lds_addr(lds_raw) + wave_u * (kRingBytes / kWaves);
-    const uint8_t *ring_p = lds_raw + wave_u * (kRingBytes / kWaves);
-    const int ntiles = __builtin_amdgcn_readfirstlane(we > ws ? (we - ws + T - 1) / T : 0);
-    auto dma_tile = [&](int j, int st) __attribute__((always_inline)) {
-        const uint32_t kd = __builtin_amdgcn_readfirstlane(ring + QB + st * 2 * TB);
+        // LDS DMA ring: each wave streams its q rows and then its 16-key K and V
+        // tiles into its own LDS with global_load_lds_dwordx4 (16 B per lane,
+        // 1 KiB = RPI rows per instruction; lane l fetches the logical chunk that
+        // lands at chunk l % CPR of its row, see mfma_dswz), NSTG stages deep, so
+        // that NSTG - 1 tiles stay in flight while one is computed and no
+        // register holds them. The DMAs are invisible to the compiler's wait
+        // counts: every wait is an explicit vmcnt on the wave's own DMAs, which
+        // complete in issue order (q, tile 0, tile 1, ...). Rows past the wave's
+        // range read row ws and are masked; fused rows come from k_new / v_new.
+        constexpr int CPR = D / 8;     // 16-byte chunks per row
+        constexpr int RPI = 64 / CPR;  // rows per DMA instruction
+        const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t ring = lds_addr(lds_raw) + wave_u * (kRingBytes / kWaves);
+        const uint8_t *ring_p = lds_raw + wave_u * (kRingBytes / kWaves);
+        const int ntiles = __builtin_amdgcn_readfirstlane(we > ws ? (we - ws + T - 1) / T : 0);
+        auto dma_tile = [&](int j, int st) __attribute__((always_inline)) {
+            const uint32_t kd = __builtin_amdgcn_readfirstlane(ring + QB + st * 2 * TB);
 #pragma unroll
-        for (int i = 0; i < TB / 1024; ++i) {
-            const int row = RPI * i + lane / CPR;
-            const int lc = (lane % CPR) ^ mfma_dswz(row);
-            const uint16_t *kp, *vp;
-            key_rows(ws + j * T + row, kp, vp);
-            dma_load16(kp + 8 * lc, kd + i * 1024);
-            dma_load16(vp + 8 * lc, kd + TB + i * 1024);
+            for (int i = 0; i < TB / 1024; ++i) {
+                const int row = RPI * i + lane / CPR;
+                const int lc = (lane % CPR) ^ mfma_dswz(row);
+                const uint16_t *kp, *vp;
+                key_rows(ws + j * T + row, kp, vp);
+                dma_load16(kp + 8 * lc, kd + i * 1024);
+                dma_load16(vp + 8 * lc, kd + TB + i * 1024);
+            }
+        };
+        {
+            // q rows of the tile (rows past the real ones read row 0 and are
+            // zeroed below), swizzled like the K tiles
+#pragma unroll
+            for (int i = 0; i < QB / 1024; ++i) {
+                const int row = RPI * i + lane / CPR;
+                const int lc = (lane % CPR) ^ mfma_dswz(row);
+                const int rq = row < rows ? row : 0;
+                const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + rq / Qn) * Qn + rq % Qn) * D;
+                dma_load16(qp + 8 * lc, __builtin_amdgcn_readfirstlane(ring + i * 1024));
+            }
         }
-    };
-    {
-        // q rows of the tile (rows past the real ones read row 0 and are
-        // zeroed below), swizzled like the K tiles
+        const int pro = min(NSTG, ntiles);
+        for (int j = 0; j < pro; ++j) dma_tile(j, j);
+        wait_vmem_steps<DPT, NSTG>(pro);  // q has landed
 #pragma unroll
-        for (int i = 0; i < QB / 1024; ++i) {
-            const int row = RPI * i + lane / CPR;
-            const int lc = (lane % CPR) ^ mfma_dswz(row);
-            const int rq = row < rows ? row : 0;
-            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + rq / Qn) * Qn + rq % Qn) * D;
-            dma_load16(qp + 8 * lc, __builtin_amdgcn_readfirstlane(ring + i * 1024));
+        for (int c = 0; c < D / 32; ++c) {
+            const int r8 = col & 7;  // columns >= R read row col - 8 and are zeroed
+            qop[c] = *reinterpret_cast<const uint4 *>(ring_p + r8 * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(r8)));
+            if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
         }
-    }
-    const int pro = min(NSTG, ntiles);
-    for (int j = 0; j < pro; ++j) dma_tile(j, j);
-    wait_vmem_steps<DPT, NSTG>(pro);  // q has landed
+        const int vrow = 4 * grp + (col >> 2);  // this lane's V^T read row
+        for (int j = 0; j < ntiles; ++j) {
+            const int st = j % NSTG;
+            wait_vmem_steps<DPT, NSTG - 1>(min(NSTG - 1, ntiles - 1 - j));
+            const uint8_t *kst = ring_p + QB + st * 2 * TB, *vst = kst + TB;
+            uint4 kop[KR];
+            uint2 vop[D / 16];
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-        const int r8 = col & 7;  // columns >= R read row col - 8 and are zeroed
-        qop[c] = *reinterpret_cast<const uint4 *>(ring_p + r8 * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(r8)));
-        if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
-    }
-    const int vrow = 4 * grp + (col >> 2);  // this lane's V^T read row
-    for (int j = 0; j < ntiles; ++j) {
-        const int st = j % NSTG;
-        wait_vmem_steps<DPT, NSTG - 1>(min(NSTG - 1, ntiles - 1 - j));
-        const uint8_t *kst = ring_p + QB + st * 2 * TB, *vst = kst + TB;
-        uint4 kop[KR];
-        uint2 vop[D / 16];
+            for (int c = 0; c < KR; ++c)
+                kop[c] = *reinterpret_cast<const uint4 *>(kst + col * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(col)));
 #pragma unroll
-        for (int c = 0; c < KR; ++c)
-            kop[c] = *reinterpret_cast<const uint4 *>(kst + col * (D * 2) + 16 * ((4 * c + grp) ^ mfma_dswz(col)));
+            for (int b = 0; b < D / 16; ++b)
+                vop[b] = lds_read_tr16(reinterpret_cast<const uint16_t *>(
+                    vst + vrow * (D * 2) + 16 * ((2 * b + ((col & 3) >> 1)) ^ mfma_dswz(vrow)) + 8 * (col & 1)));
+            wait_lds();  // the stage is in registers: refill it
+            if (j + NSTG < ntiles) dma_tile(j + NSTG, st);
+            const int t0 = ws + j * T;
+            f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < D / 16; ++b)
-            vop[b] = lds_read_tr16(reinterpret_cast<const uint16_t *>(
-                vst + vrow * (D * 2) + 16 * ((2 * b + ((col & 3) >> 1)) ^ mfma_dswz(vrow)) + 8 * (col & 1)));
-        wait_lds();  // the stage is in registers: refill it
-        if (j + NSTG < ntiles) dma_tile(j + NSTG, st);
-        const int t0 = ws + j * T;
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < KR; ++c) s = mfma16(kop[c], qop[c], s);
-        float sc[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int key = t0 + 4 * grp + v;
-            const bool vis = key < we && key <= hi && key >= lo;
-            sc[v] = vis ? s[v] * a.scale_log2 : -INFINITY;
-        }
-        if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+            for (int c = 0; c < KR; ++c) s = mfma16(kop[c], qop[c], s);
+            float sc[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int key = t0 + 4 * grp + v;
-                sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+                const bool vis = key < we && key <= hi && key >= lo;
+                sc[v] = vis ? s[v] * a.scale_log2 : -INFINITY;
             }
+            if (PMASK && t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int key = t0 + 4 * grp + v;
+                    sc[v] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[v];
+                }
+            }
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
+            tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+            lazy_rescale<D / 16>(tmax, m, l, o);
+            float p[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
+                l += p[v];
+            }
+            // P = P_hi + P_lo in bf16, as in the register-staged tiles
+            const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
+            const uint2 ph = make_uint2(h01, h23);
+            const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
+                                        pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b) o[b] = mfma16k16(vop[b], pl, mfma16k16(vop[b], ph, o[b]));
         }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[v]);
-        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
-        lazy_rescale<D / 16>(tmax, m, l, o);
-        float p[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            p[v] = __builtin_amdgcn_exp2f(sc[v] - m);
-            l += p[v];
-        }
-        // P = P_hi + P_lo in bf16, as in the register-staged tiles
-        const uint32_t h01 = pack_bf16x2(p[0], p[1]), h23 = pack_bf16x2(p[2], p[3]);
-        const uint2 ph = make_uint2(h01, h23);
-        const uint2 pl = make_uint2(pack_bf16x2(p[0] - bf16_lo(h01), p[1] - bf16_hi(h01)),
-                                    pack_bf16x2(p[2] - bf16_lo(h23), p[3] - bf16_hi(h23)));
-#pragma unroll
-        for (int b = 0; b < D / 16; ++b) o[b] = mfma16k16(vop[b], pl, mfma16k16(vop[b], ph, o[b]));
-    }
-    wait_vmem<0>();  // every DMA of the wave has landed before the LDS is reused
+        wait_vmem<0>();  // every DMA of the wave has landed before the LDS is reused
     }
     if (bad) a.err[0] = 1;
     l = pair<OpSum, 32>(pair<OpSum, 16>(l));

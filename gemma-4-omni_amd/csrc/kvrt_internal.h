@@ -212,16 +212,13 @@ constexpr bool decode_wg_merge(int head_dim, int rows_tile) { return rows_tile *
 constexpr int kMfmaDecodeMinRows = 8;
 constexpr int kMfmaDecodeKeys = 16;  // keys per MFMA decode tile
 // The MFMA decode's LDS DMA ring (K and V tiles streamed into LDS, two
-// stages per wave at D 128): bf16 CONTIG / RING tiles of 8 rows at the head
-// dims switched on here. D 256 stays on the register-staged tiles: its
-// 147 KB ring (2 stages of 16 KB per wave) measured faster alone but kept
-// the talker's workgroups off the thinker's CUs, and the two-stream step
-// slower (0.564 vs 0.542 ms).
+// stages per wave at D 128, one at D 256): bf16 CONTIG / RING tiles of 8
+// rows at the head dims switched on here.
 #ifndef KVRT_MFMA_DMA_D128
 #define KVRT_MFMA_DMA_D128 1
 #endif
 #ifndef KVRT_MFMA_DMA_D256
-#define KVRT_MFMA_DMA_D256 0
+#define KVRT_MFMA_DMA_D256 1
 #endif
 constexpr bool mfma_decode_dma(int head_dim, int rows_tile, int dtype, int layout) {
     return dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && rows_tile <= 8 &&

@@ -1042,14 +1042,18 @@ __device__ __forceinline__ uint2 i8x4_to_bf16(uint32_t w) {
                       pack_bf16x2((float)(int8_t)(w >> 16), (float)(int8_t)(w >> 24)));
 }
 
-// Stages per wave of the MFMA decode's LDS DMA ring (mfma_decode_dma): two
-// at D 128 (72 KB per workgroup; 3 and 4 stages, 104 and 136 KB, lengthened
-// the two-stream step: 0.555 and 0.584 vs 0.542 ms), two at D 256.
+// Stages per wave of the MFMA decode's LDS DMA ring (mfma_decode_dma). A
+// wave copies a stage into registers and refills it before computing, so
+// with S stages S tiles are in flight during a tile's MFMAs. Two at D 128
+// (72 KB per workgroup; 1, 3 and 4 stages: 0.598, 0.555 and 0.584 vs 0.542
+// ms per two-stream step), one at D 256 (80 KB; two, 147 KB, ran the
+// thinker's global layer faster alone but kept the talker's workgroups off
+// its CUs: step 0.564 vs 0.542 ms).
 #ifndef KVRT_MFMA_DMA_STAGES_128
 #define KVRT_MFMA_DMA_STAGES_128 2
 #endif
 #ifndef KVRT_MFMA_DMA_STAGES_256
-#define KVRT_MFMA_DMA_STAGES_256 2
+#define KVRT_MFMA_DMA_STAGES_256 1
 #endif
 // Chunk swizzle of the MFMA decode's DMA tiles: the logical 16-byte chunk c
 // of tile row r sits at chunk c ^ mfma_dswz(r), a permutation of the low 4

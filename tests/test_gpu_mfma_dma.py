@@ -1,5 +1,5 @@
-"""GPU parity of the MFMA decode's LDS DMA ring (bf16 CONTIG / RING, D 128,
-1, 2, 4 or 8 query rows per KV head over >= 2048 keys, the shapes AUTO sends
+"""GPU parity of the MFMA decode's LDS DMA ring (bf16 CONTIG / RING, D 128 and
+256, 1, 2, 4 or 8 query rows per KV head over >= 2048 keys, the shapes AUTO sends
 to it) against the oracle at max-abs 1e-2, beside the same launches forced
 onto the VALU kernel: wave ranges of many tiles, of one or two tiles and
 empty ones (decode_wgs 8 / 64 / 512), partial last tiles, fused appends and a
@@ -22,11 +22,12 @@ ATOL = 1e-2
 @pytest.mark.parametrize("wgs", [8, 64, 512])
 @pytest.mark.parametrize("layout", ["contig", "ring"])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
-def test_mfma_dma_decode_parity(group, layout, wgs):
+@pytest.mark.parametrize("d", [128, 256])
+def test_mfma_dma_decode_parity(d, group, layout, wgs):
     from kvrt import KVRuntime, LayerSpec
 
-    gen = torch.Generator().manual_seed(100 * group + wgs + len(layout))
-    hkv, d = 2, 128
+    gen = torch.Generator().manual_seed(100 * group + wgs + len(layout) + d)
+    hkv = 2
     window = 2304 if layout == "ring" else 0
     ring = dict(ring_rows=window) if layout == "ring" else {}
     spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window, **ring)

@@ -64,3 +64,26 @@ def test_mfma_dma_decode_parity(d, group, layout, wgs):
     for rt in rts.values():
         assert rt.health() == 0
         assert [rt.seq_length(s, 0) for s in slots] == [n + 3 for n in lens]
+
+
+@pytest.mark.parametrize("lmax", [2304, 1024])
+def test_tensor_path_clamps_a_length_beyond_the_view(lmax):
+    """attend_tensors over caller-owned K/V [3, 8, Lmax, 128] with 16 q heads
+    (2 rows per KV head: the MFMA DMA decode at Lmax 2304, the VALU kernel at
+    1024): the item whose length exceeds Lmax attends over the Lmax rows it
+    has (its query at position Lmax - 1) and raises the tensor path's device
+    flag; the other items match the oracle."""
+    from kvrt.runtime import attend_tensors, tensors_status
+
+    gen = torch.Generator().manual_seed(lmax)
+    n, hkv, hq, d = 3, 8, 16, 128
+    k, v = randn_bf16(gen, (n, hkv, lmax, d)), randn_bf16(gen, (n, hkv, lmax, d))
+    q = randn_bf16(gen, (n, hq, 1, d), 1.0 / math.sqrt(d))
+    lens = [lmax - 4, lmax + 100, lmax // 2 + 3]
+    out = attend_tensors(q.cuda(), k.cuda(), v.cuda(), torch.tensor(lens, dtype=torch.int32).cuda(), 1.0)
+    assert tensors_status() == -6
+    for i, ln in enumerate(lens):
+        seen = min(ln, lmax)
+        ref = O.attend(to_np(q[i]), to_np(k[i, :, :seen]), to_np(v[i, :, :seen]), np.array([seen - 1]), 1.0)
+        assert float(np.abs(to_np(out[i]) - ref).max()) <= ATOL, (lmax, i)
+    assert tensors_status() == 0  # the flag was cleared

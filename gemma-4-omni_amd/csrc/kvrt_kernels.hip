@@ -1353,9 +1353,10 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         // LDS DMA ring: each wave streams its q rows and then its 16-key K and V
         // tiles into its own LDS with global_load_lds_dwordx4 (16 B per lane,
         // 1 KiB = RPI rows per instruction; lane l fetches the logical chunk that
-        // lands at chunk l % CPR of its row, see mfma_dswz), NSTG stages deep, so
-        // that NSTG - 1 tiles stay in flight while one is computed and no
-        // register holds them. The DMAs are invisible to the compiler's wait
+        // lands at chunk l % CPR of its row, see mfma_dswz), NSTG stages deep. A
+        // tile's stage is copied into its operand registers and refilled with
+        // the tile NSTG ahead before the tile's MFMAs, so NSTG tiles are in
+        // flight while one is computed. The DMAs are invisible to the compiler's wait
         // counts: every wait is an explicit vmcnt on the wave's own DMAs, which
         // complete in issue order (q, tile 0, tile 1, ...). Rows past the wave's
         // range read row ws and are masked; fused rows come from k_new / v_new.

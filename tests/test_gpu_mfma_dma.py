@@ -87,3 +87,39 @@ def test_tensor_path_clamps_a_length_beyond_the_view(lmax):
         ref = O.attend(to_np(q[i]), to_np(k[i, :, :seen]), to_np(v[i, :, :seen]), np.array([seen - 1]), 1.0)
         assert float(np.abs(to_np(out[i]) - ref).max()) <= ATOL, (lmax, i)
     assert tensors_status() == 0  # the flag was cleared
+
+
+@pytest.mark.parametrize("merge", ["separate", "last_wg"])
+@pytest.mark.parametrize("kernel", ["auto", "valu", "mfma"])
+@pytest.mark.parametrize("d,hkv,hq", [(128, 8, 16), (256, 1, 8)])
+def test_ragged_batch_matches_the_oracle(d, hkv, hq, kernel, merge):
+    """A ragged batch (4038 / 925 / 1269 / 130 / 2600 positions) in one
+    launch: the split count follows the longest item, so the short items'
+    waves hold a few keys or none, and every item's partials still merge to
+    the oracle's attention, with the merge kernel or in the decode's last
+    workgroup, over fused append steps."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(d + hkv + len(kernel) + len(merge))
+    lens = [4038, 925, 1269, 130, 2600]
+    n = len(lens)
+    rt = KVRuntime([LayerSpec(kv_heads=hkv, head_dim=d)], n, 4200, max_q=1, decode_kernel=kernel,
+                   decode_merge=merge, device="cuda")
+    orc = O.OracleCache([O.OracleLayer(hkv, d)], n)
+    for s, ln in enumerate(lens):
+        k, v = randn_bf16(gen, (1, hkv, ln, d)), randn_bf16(gen, (1, hkv, ln, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    slots = list(range(n))
+    worst = 0.0
+    for _ in range(4):
+        q = randn_bf16(gen, (n, hq, 1, d), 1.0 / math.sqrt(d))
+        k, v = randn_bf16(gen, (n, hkv, 1, d)), randn_bf16(gen, (n, hkv, 1, d))
+        out = rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), slots, 1.0)
+        torch.cuda.synchronize()
+        for i, s in enumerate(slots):
+            orc.append(s, 0, to_np(k[i]), to_np(v[i]))
+            worst = max(worst, float(np.abs(to_np(out[i]) - orc.attend(s, 0, to_np(q[i]), 1.0)).max()))
+    assert worst <= ATOL, worst
+    assert rt.health() == 0
+    assert [rt.seq_length(s, 0) for s in slots] == [ln + 4 for ln in lens]

@@ -265,8 +265,9 @@ bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t 
         // KVRT_MFMA_SMALL_ROWS=0 keeps them on the VALU kernel
         static const char *env = std::getenv("KVRT_MFMA_SMALL_ROWS");
         static const bool small = !env || std::atoi(env) != 0;
+        static const int64_t min_keys_small = env_int("KVRT_MFMA_SMALL_MIN_KEYS", (int)kMfmaDecodeMinKeys8);
         return mode == KVRT_DECODE_MFMA ||
-               (small && mfma_decode_dma(head_dim, rows_tile_, dtype, layout) && keys >= kMfmaDecodeMinKeys8);
+               (small && mfma_decode_dma(head_dim, rows_tile_, dtype, layout) && keys >= min_keys_small);
     }
     return mode == KVRT_DECODE_MFMA || rows_tile_ >= 16 || head_dim >= 512 || keys >= kMfmaDecodeMinKeys8;
 }

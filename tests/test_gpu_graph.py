@@ -27,8 +27,11 @@ def _pair(specs, n_slots, capacity, gen, prefill, merge="auto"):
     return a, b
 
 
+@pytest.mark.parametrize("prefill", [1100, 2500])
 @pytest.mark.parametrize("merge", ["auto", "separate", "last_wg"])
-def test_graph_replays_match_eager_bitwise(merge):
+def test_graph_replays_match_eager_bitwise(merge, prefill):
+    """At 1100 positions the talker- and thinker-global-shaped layers run on
+    the VALU decode, at 2500 on the MFMA decode's LDS DMA ring."""
     from kvrt import LayerSpec
 
     gen = torch.Generator().manual_seed(21)
@@ -40,7 +43,7 @@ def test_graph_replays_match_eager_bitwise(merge):
     hq = [16, 8, 8]
     n = 3
     steps = 6
-    a, b = _pair(specs, n, 1500, gen, prefill=1100, merge=merge)
+    a, b = _pair(specs, n, prefill + 400, gen, prefill=prefill, merge=merge)
     inputs = [[(randn_bf16(gen, (n, hq[l], 1, s.head_dim), 0.5).cuda(),
                 randn_bf16(gen, (n, s.kv_heads, 1, s.head_dim), 0.5).cuda(),
                 randn_bf16(gen, (n, s.kv_heads, 1, s.head_dim), 0.5).cuda()) for l, s in enumerate(specs)]
@@ -66,7 +69,7 @@ def test_graph_replays_match_eager_bitwise(merge):
     with torch.cuda.graph(g):
         step()
     b.sync_lengths()
-    assert b.seq_length(0, 0) == 1101
+    assert b.seq_length(0, 0) == prefill + 1
     for t in range(1, steps):
         for l in range(len(specs)):
             for dst, src in zip(static_in[l], inputs[t][l]):
@@ -80,12 +83,14 @@ def test_graph_replays_match_eager_bitwise(merge):
     b.sync_lengths()
     for l in range(len(specs)):
         for s in slots:
-            assert b.seq_length(s, l) == a.seq_length(s, l) == 1100 + steps
+            assert b.seq_length(s, l) == a.seq_length(s, l) == prefill + steps
         ka, va, _ = a.gather(l, slots)
         kb, vb, _ = b.gather(l, slots)
         np.testing.assert_array_equal(bits(ka), bits(kb))
         np.testing.assert_array_equal(bits(va), bits(vb))
     assert a.health() == 0 and b.health() == 0
+    mfma = b.counters()["mfma_decodes"]
+    assert (mfma > 0) == (prefill >= 2048), mfma
 
 
 def test_graph_replays_of_a_key_split_prefill_match_eager():

@@ -3,7 +3,8 @@
 to it) against the oracle at max-abs 1e-2, beside the same launches forced
 onto the VALU kernel: wave ranges of many tiles, of one or two tiles and
 empty ones (decode_wgs 8 / 64 / 512), partial last tiles, fused appends and a
-canonical prefix mask on one slot."""
+canonical prefix mask on one slot. The forced "mfma" kernel choice is also
+checked on short caches and on the PAGED layout, which AUTO leaves to VALU."""
 from __future__ import annotations
 
 import math
@@ -123,3 +124,37 @@ def test_ragged_batch_matches_the_oracle(d, hkv, hq, kernel, merge):
     assert worst <= ATOL, worst
     assert rt.health() == 0
     assert [rt.seq_length(s, 0) for s in slots] == [ln + 4 for ln in lens]
+
+
+@pytest.mark.parametrize("layout", ["contig", "paged"])
+def test_forced_mfma_small_rows_short_and_paged(layout):
+    """decode_kernel="mfma" sends 2-row decodes to the MFMA kernel at any key
+    count and layout: CONTIG at a few hundred keys (the DMA ring), PAGED
+    (register-staged 8-row tiles over a shuffled page pool)."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(7 + len(layout))
+    hkv, hq, d = 8, 16, 128
+    lens = [300, 45, 1000]
+    kw = dict(block_size=16, pool_pages=3 * (1100 // 16 + 4), pool_seed=3) if layout == "paged" else {}
+    rt = KVRuntime([LayerSpec(kv_heads=hkv, head_dim=d, layout=layout)], 3, 1100, max_q=1, decode_kernel="mfma",
+                   device="cuda", **kw)
+    orc = O.OracleCache([O.OracleLayer(hkv, d)], 3)
+    for s, ln in enumerate(lens):
+        k, v = randn_bf16(gen, (1, hkv, ln, d)), randn_bf16(gen, (1, hkv, ln, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    slots = [0, 1, 2]
+    before = rt.counters()["mfma_decodes"]
+    worst = 0.0
+    for _ in range(3):
+        q = randn_bf16(gen, (3, hq, 1, d), 1.0 / math.sqrt(d))
+        k, v = randn_bf16(gen, (3, hkv, 1, d)), randn_bf16(gen, (3, hkv, 1, d))
+        out = rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), slots, 1.0)
+        torch.cuda.synchronize()
+        for i, s in enumerate(slots):
+            orc.append(s, 0, to_np(k[i]), to_np(v[i]))
+            worst = max(worst, float(np.abs(to_np(out[i]) - orc.attend(s, 0, to_np(q[i]), 1.0)).max()))
+    assert worst <= ATOL, worst
+    assert rt.counters()["mfma_decodes"] - before == 3
+    assert rt.health() == 0

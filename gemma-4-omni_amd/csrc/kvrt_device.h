@@ -113,4 +113,57 @@ __device__ __forceinline__ float strided_reduce(float x) {
 template <int S> __device__ __forceinline__ float strided_sum(float x) { return strided_reduce<OpSum, S>(x); }
 template <int S> __device__ __forceinline__ float strided_max(float x) { return strided_reduce<OpMax, S>(x); }
 
+// Agent-scope (cross-XCD) coherent accesses. On gfx950 a relaxed agent-scope
+// store is written through the XCD's L2 (global_store ... sc1) and a relaxed
+// agent-scope load reads past it (global_load ... sc1), so data exchanged
+// only through them needs no L2 write-back or invalidate between workgroups,
+// only the completion wait of the stores. The single-launch decode merge
+// rests on exactly this lowering; the build compiles these helpers alone
+// (kvrt_coherence_probe.hip) and refuses a compiler whose lowering differs.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(float2 *p, float2 v) {
+    const uint64_t b = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// N consecutive floats, as 8-byte stores where N is even (dst 8-byte aligned).
+template <int N>
+__device__ __forceinline__ void store_agent_n(float *dst, const float (&v)[N]) {
+    if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int e = 0; e < N; e += 2) store_agent(reinterpret_cast<float2 *>(dst + e), make_float2(v[e], v[e + 1]));
+    } else {
+#pragma unroll
+        for (int e = 0; e < N; ++e) store_agent(dst + e, v[e]);
+    }
+}
+// 16 bytes as two 8-byte agent-scope stores: written through the XCD's L2
+// instead of left dirty in it. The fused appends' rows use it: no later
+// kernel of the step needs them in this L2, and a step of launches that
+// leave fewer dirty lines measured shorter (two-model step 601.6 -> 593.3 us).
+// Callers load every source first: loads after an atomic store are not moved
+// above it, so a load-store-load-store order costs a round trip per row.
+__device__ __forceinline__ void store_agent16(void *p, const uint4 &x) {
+    uint64_t *d = static_cast<uint64_t *>(p);
+    __hip_atomic_store(d, (uint64_t)x.x | ((uint64_t)x.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(d + 1, (uint64_t)x.z | ((uint64_t)x.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent(const float2 *p) {
+    const uint64_t b = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float2 *>(p)), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
+}
+// Arrival counters of the single-launch merge: an L2 atomic add returning the
+// count before it, and the reset by the last arrival.
+__device__ __forceinline__ uint32_t arrive_agent(uint32_t *c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void clear_agent(uint32_t *c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace kvrt

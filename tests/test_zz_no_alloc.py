@@ -65,6 +65,7 @@ def test_noalloc_entry_point_matches_the_allocating_one_over_successive_calls():
         (4, 8, 1, 2, 512, 4000, [4000, 3100, 2500, 3999], 0, 34),
         (4, 16, 8, 2, 128, 900, [900, 640, 77, 512], 0, 0),        # talker-shaped
         (2, 8, 1, 1, 256, 300, [300, 129], 128, 120),               # thinker sliding, masked
+        (4, 16, 8, 1, 128, 2304, [2304, 2100, 1500, 2201], 0, 0),  # talker, MFMA decode's DMA ring
     ]
     scale = 1.0
     for i, (n, hq, hkv, qn, d, lmax, lens, window, plen) in enumerate(cases):

@@ -736,8 +736,8 @@ def run_configs(args) -> int:
             dlen.add_(2)
             for layer in range(16):
                 q, k, v = ins[i % pool][layer]
-                rt.append(layer, k, v, slots)
-                kp, vp, _ = rt.gather(layer, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm]))
+                # the append and the gather in one launch (kvrt_append_gather_async)
+                kp, vp, _ = rt.append_gather(layer, k, v, slots, out=(kbuf[:, :, :lm], vbuf[:, :, :lm], mbuf[:, :lm]))
                 attend_tensors(q, kp, vp, dlen, 1 / math.sqrt(128), out=outs[layer])
 
         gpu_s = _gpu_timed(c3, steps)
@@ -756,8 +756,7 @@ def run_configs(args) -> int:
             dlen.add_(2)
             for layer in range(16):
                 q, k, v = ins[0][layer]
-                rt.append(layer, k, v, slots)
-                kp, vp, _ = rt.gather(layer, slots, out=(kbuf[:, :, :lt], vbuf[:, :, :lt], mbuf[:, :lt]))
+                kp, vp, _ = rt.append_gather(layer, k, v, slots, out=(kbuf[:, :, :lt], vbuf[:, :, :lt], mbuf[:, :lt]))
                 attend_tensors(q, kp, vp, dlen, 1 / math.sqrt(128), out=outs[layer])
 
         g3_s = graph_time(rt, c3g, steps)

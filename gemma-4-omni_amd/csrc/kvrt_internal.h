@@ -171,6 +171,14 @@ struct GatherArgs {
     int32_t window;         // ring default start rule
     int32_t has_start;
     int32_t *err;
+    // fused append (bf16 CONTIG / RING; else null): k_new, v_new [n, kv_heads,
+    // qn, D] contiguous land at each item's device length before the gather
+    // reads, and the last workgroup of an item (arrival count in cnt) advances
+    // that length by qn
+    const uint16_t *k_new;
+    const uint16_t *v_new;
+    uint32_t *cnt;
+    int32_t qn;
     int32_t start[kMaxItems];
     int32_t slots[kMaxItems];
 };
@@ -203,7 +211,17 @@ struct DecodeArgs {
 // kv head) at item * kv_heads + kvh, then one per item at kCntItemBase + item.
 // Every launch leaves them at zero.
 constexpr int kCntItemBase = kMaxItems * 64;
-constexpr int kCntWords = kCntItemBase + kMaxItems;
+// The fused append + gather counts its workgroups' arrivals per (item, kv
+// head), then per item, each counter on a 128-byte line of its own: up to
+// hundreds of workgroups arrive per item, and atomics on one line serialise
+// (all items' counters on one line made the launch ~7 us longer).
+constexpr int kCntLineWords = 32;
+constexpr int kCntGatherBase = kCntItemBase + kMaxItems + kCntLineWords;  // line aligned below
+constexpr int kCntGatherHead(int item, int h) {
+    return (kCntGatherBase / kCntLineWords + item * 64 + h) * kCntLineWords;
+}
+constexpr int kCntGatherItem(int item) { return kCntGatherHead(kMaxItems, 0) + item * kCntLineWords; }
+constexpr int kCntWords = kCntGatherItem(kMaxItems);
 
 // The split-K decode merges its 4 waves' partials in LDS (one partial per
 // workgroup) when R * D floats per wave fit.

@@ -203,6 +203,14 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // valid length are written as zeros; head 0's workgroups also write the mask
 // entries of their rows. (A flat grid-stride loop over 16-B chunks spent two
 // 64-bit divisions per chunk on the row and head.)
+// Fused append (a.k_new set; bf16 CONTIG / RING): the item's device length L0
+// is the append position; rows L0 .. L0 + qn - 1 of the gathered range come
+// from k_new / v_new, workgroup x = 0 of each (item, head) also stores them
+// into the cache (no workgroup of the launch reads those cache rows; RING rows
+// overwritten hold positions before every gathered start, which ring_rows >=
+// window + max_q - 1 guarantees), and the last workgroup of the item to
+// arrive (counted per (item, head), then per item) advances its length by
+// qn, after every workgroup has read L0.
 constexpr int kGatherUnroll = 4;
 template <int D>
 constexpr int gather_rows() { return 256 / (D / 8) * kGatherUnroll; }
@@ -211,10 +219,33 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     constexpr int LPR = D / 8;
     constexpr int RPP = 256 / LPR;  // rows per pass of the workgroup
     constexpr int U = kGatherUnroll;
+    constexpr bool FUSE = KDT == KVRT_BF16 && LAYOUT != KVRT_LAYOUT_PAGED;
     const int item = blockIdx.z;
     const int h = blockIdx.y;
     const int slot = a.slots[item];
-    const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    const int L0 = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    const bool fused = FUSE && a.k_new != nullptr;
+    const int Qn = fused ? a.qn : 0;
+    const int L = L0 + Qn;
+    // appended row r of this (item, head), 16 B at column chunk sg
+    auto new_row = [&](const uint16_t *src, int r, int sg) __attribute__((always_inline)) {
+        return *reinterpret_cast<const uint4 *>(src + (((int64_t)item * gridDim.y + h) * Qn + r) * D + sg * 8);
+    };
+    if (fused && blockIdx.x == 0) {
+        for (int c = threadIdx.x; c < Qn * (D / 8); c += blockDim.x) {
+            const int r = c / (D / 8), sg = c % (D / 8);
+            const int pos = L0 + r;
+            const int64_t dst = (LAYOUT == KVRT_LAYOUT_CONTIG && pos >= a.kv.rows)
+                                    ? -1 : row_offset<LAYOUT>(a.kv, slot, h, pos, D);
+            if (dst < 0) {
+                a.err[0] = 1;
+                continue;
+            }
+            const uint4 kx = new_row(a.k_new, r, sg), vx = new_row(a.v_new, r, sg);
+            store_agent16(static_cast<uint16_t *>(a.kv.k) + dst + sg * 8, kx);
+            store_agent16(static_cast<uint16_t *>(a.kv.v) + dst + sg * 8, vx);
+        }
+    }
     int start;
     if (a.has_start) start = a.start[item];
     else if (LAYOUT == KVRT_LAYOUT_RING && a.window > 0) start = max(0, L - (a.window - 1));
@@ -230,7 +261,10 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) kf[u][i] = vf[u][i] = 0.f;
         const int j = j0 + u * RPP;
-        if (j < valid && j < a.lmax) {
+        if (fused && j < valid && j < a.lmax && start + j >= L0) {
+            kx[u] = new_row(a.k_new, start + j - L0, seg);
+            vx[u] = new_row(a.v_new, start + j - L0, seg);
+        } else if (j < valid && j < a.lmax) {
             int64_t src = row_offset<LAYOUT>(a.kv, slot, h, start + j, D);
             if (LAYOUT == KVRT_LAYOUT_CONTIG && start + j >= a.kv.rows) src = -1;
             if (src < 0) {
@@ -285,6 +319,20 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
             if (a.mask_dtype == KVRT_BOOL) static_cast<uint8_t *>(a.mask)[mo] = ok ? 1 : 0;
             else if (a.mask_dtype == KVRT_FP32) static_cast<float *>(a.mask)[mo] = ok ? 0.f : -3.4028234663852886e38f;
             else static_cast<uint16_t *>(a.mask)[mo] = ok ? (uint16_t)0 : (uint16_t)0xff7f;  // bf16 finfo.min
+        }
+    }
+    if (fused) {
+        __syncthreads();  // every thread of the workgroup has used L0
+        if (threadIdx.x == 0) {
+            uint32_t *hc = a.cnt + kCntGatherHead(item, h);
+            if (arrive_agent(hc) == gridDim.x - 1) {  // the last of the (item, head)
+                clear_agent(hc);
+                uint32_t *ic = a.cnt + kCntGatherItem(item);
+                if (arrive_agent(ic) == gridDim.y - 1) {  // the last head of the item
+                    clear_agent(ic);
+                    a.len.lens[(int64_t)slot * a.len.stride + a.len.offset] = L;
+                }
+            }
         }
     }
 }
@@ -2305,6 +2353,8 @@ hipError_t launch_gather(const GatherArgs &a, int head_dim, int dtype, hipStream
     const int gx = (a.lmax + rows - 1) / rows;
     if (gx < 1 || a.kv.kv_heads < 1 || a.n_items < 1) return hipSuccess;
     dim3 grid(gx, a.kv.kv_heads, a.n_items), block(256);
+    if (a.k_new && (dtype != KVRT_BF16 || a.kv.layout == KVRT_LAYOUT_PAGED || !a.v_new || !a.cnt || a.qn < 1))
+        return hipErrorInvalidValue;  // the fused append: bf16 CONTIG / RING only
     if (dtype == KVRT_INT8) {
         if (a.kv.layout != KVRT_LAYOUT_PAGED) return hipErrorInvalidValue;
         KVRT_DISPATCH_D(head_dim, hipLaunchKernelGGL((gather_kernel<HD, KVRT_INT8, KVRT_LAYOUT_PAGED>), grid, block, 0, s, a));

@@ -1395,12 +1395,26 @@ int kvrt_slot_info_get(kvrt_ctx *c, int32_t slot, kvrt_slot_info *out) {
     return KVRT_OK;
 }
 
-int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,
-                      const kvrt_tensor *out_k, const kvrt_tensor *out_v, const kvrt_tensor *mask) {
-    int rc = begin(c);
-    if (rc) return rc;
-    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+// Gather, and with k / v the append of their rows fused into the same launch
+// (bf16 CONTIG / RING layers that own their rows, at most max_q rows; the
+// caller has validated the context, layer and slots).
+static int gather_impl(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,
+                       const kvrt_tensor *out_k, const kvrt_tensor *out_v, const kvrt_tensor *mask,
+                       const kvrt_tensor *k, const kvrt_tensor *v) {
     const kvrt_layer_spec &s = c->layers[layer].spec;
+    int qn = 0;
+    if (k) {
+        const int D = s.head_dim, hkv = s.kv_heads;
+        if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4) || !is_contiguous(k) || !is_contiguous(v))
+            return KVRT_EINVAL;
+        for (int i = 0; i < 4; ++i)
+            if (k->dims[i] != v->dims[i]) return KVRT_EINVAL;
+        if (k->dims[0] != n || k->dims[1] != hkv || k->dims[3] != D || k->dims[2] < 1 || k->dims[2] > c->cfg.max_q)
+            return KVRT_EINVAL;
+        qn = (int)k->dims[2];
+        for (int i = 0; i < n; ++i)
+            if ((int64_t)c->len_at(slots[i], layer) + qn > c->cfg.capacity) return KVRT_ESTATE;
+    }
     const int out_dtype = s.dtype == KVRT_INT8 ? KVRT_FP32 : KVRT_BF16;
     if (!tensor_ok(out_k, out_dtype, 4) || !tensor_ok(out_v, out_dtype, 4)) return KVRT_EINVAL;
     for (int i = 0; i < 4; ++i)
@@ -1416,7 +1430,7 @@ int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slot
     }
     GatherArgs a{};
     for (int i = 0; i < n; ++i) {
-        const int L = c->len_at(slots[i], layer);
+        const int L = c->len_at(slots[i], layer) + qn;
         int st;
         if (start_pos) st = start_pos[i];
         else if (s.layout == KVRT_LAYOUT_RING) st = std::max(0, L - (s.window - 1));
@@ -1447,10 +1461,47 @@ int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slot
     a.lmax = (int)lmax;
     a.window = s.window;
     a.err = c->d_err;
+    if (k) {
+        a.k_new = static_cast<const uint16_t *>(k->data);
+        a.v_new = static_cast<const uint16_t *>(v->data);
+        a.cnt = c->d_cnt;
+        a.qn = qn;
+    }
     c->counters.launches++;
     if (launch_gather(a, s.head_dim, s.dtype, c->stream) != hipSuccess) return poison(c);
     c->counters.gathered_bytes += (uint64_t)n * s.kv_heads * lmax * s.head_dim * 2 * elem_size(out_dtype);
+    for (int i = 0; k && i < n; ++i) {
+        c->len_ref(slots[i], layer) += qn;
+        c->counters.appended_rows += (uint64_t)qn * s.kv_heads;
+        c->counters.appended_bytes += (uint64_t)qn * s.kv_heads * s.head_dim * 2 * 2;
+    }
     return KVRT_OK;
+}
+
+int kvrt_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const int32_t *start_pos,
+                      const kvrt_tensor *out_k, const kvrt_tensor *out_v, const kvrt_tensor *mask) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots)) return KVRT_EINVAL;
+    return gather_impl(c, layer, n, slots, start_pos, out_k, out_v, mask, nullptr, nullptr);
+}
+
+int kvrt_append_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slots, const kvrt_tensor *k,
+                             const kvrt_tensor *v, const int32_t *start_pos, const kvrt_tensor *out_k,
+                             const kvrt_tensor *out_v, const kvrt_tensor *mask) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !k || !v) return KVRT_EINVAL;
+    const kvrt_layer_spec &s = c->layers[layer].spec;
+    const bool fusable = c->layers[layer].owner == layer && s.dtype == KVRT_BF16 && s.layout != KVRT_LAYOUT_PAGED &&
+                         k->ndim == 4 && k->dims[2] >= 1 && k->dims[2] <= c->cfg.max_q && is_contiguous(k) &&
+                         is_contiguous(v);
+    if (fusable) return gather_impl(c, layer, n, slots, start_pos, out_k, out_v, mask, k, v);
+    // shared layers (no rows of their own), PAGED and int8 layers, longer
+    // appends: the append launch, then the gather
+    rc = append_impl(c, layer, n, slots, k, v);
+    if (rc != KVRT_OK) return rc;
+    return gather_impl(c, layer, n, slots, start_pos, out_k, out_v, mask, nullptr, nullptr);
 }
 
 int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation) {

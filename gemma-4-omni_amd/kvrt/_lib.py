@@ -164,6 +164,7 @@ SIGNATURES = [
     ("kvrt_set_prefix_attention_async", c_int32, [c_void_p, c_int32, _T]),
     ("kvrt_slot_info_get", c_int32, [c_void_p, c_int32, POINTER(KvrtSlotInfo)]),
     ("kvrt_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T, _T]),
+    ("kvrt_append_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _I32P, _T, _T, _T]),
     ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),
     ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),

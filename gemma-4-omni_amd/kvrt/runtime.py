@@ -577,6 +577,31 @@ class KVRuntime:
                "kvrt_gather_async")
         return out_k, out_v, mask
 
+    def append_gather(self, layer: int, k: torch.Tensor, v: torch.Tensor, slots: Sequence[int],
+                      out: tuple, start_pos: Sequence[int] | None = None) -> tuple:
+        """``append(layer, k, v, slots)`` then ``gather(layer, slots, out=out,
+        start_pos=start_pos)`` in one launch where the layer allows it (bf16
+        CONTIG / RING, Q <= max_q, contiguous k / v). ``out`` is (K, V) or
+        (K, V, mask) as for ``gather``; returns it."""
+        require_cuda(k, "k")
+        require_cuda(v, "v")
+        out_k, out_v = out[0], out[1]
+        require_cuda(out_k, "out_k")
+        require_cuda(out_v, "out_v")
+        mask = out[2] if len(out) > 2 else None
+        if mask is not None:
+            require_cuda(mask, "out mask")
+        self._bind()
+        arr, n = self._slots(slots)
+        sp = None if start_pos is None else (ctypes.c_int32 * n)(*[int(x) for x in start_pos])
+        kd, vd = tensor_desc(k), tensor_desc(v)
+        okd, ovd = tensor_desc(out_k), tensor_desc(out_v)
+        md = None if mask is None else ctypes.byref(tensor_desc(mask))
+        _check(self.lib.kvrt_append_gather_async(self._ctx, layer, n, arr, ctypes.byref(kd), ctypes.byref(vd), sp,
+                                                 ctypes.byref(okd), ctypes.byref(ovd), md),
+               "kvrt_append_gather_async")
+        return out_k, out_v, mask
+
     def truncate(self, slot: int, new_len: int, layer: int = -1, generation: int = L.KVRT_ANY_GENERATION) -> None:
         """Rollback to new_len positions: a length edit, no KV bytes move.
 

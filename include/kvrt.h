@@ -337,6 +337,22 @@ int kvrt_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *sl
                       const int32_t *start_pos, const kvrt_tensor *out_k,
                       const kvrt_tensor *out_v, const kvrt_tensor *mask);
 
+/* Append k, v ([n, kv_heads, Q, D] bf16) to n slots of one layer, then gather
+ * them: the same cache rows, lengths, out_k / out_v / mask and start_pos
+ * rules as kvrt_append_async followed by kvrt_gather_async. For bf16
+ * CONTIG / RING layers that own their rows, with Q <= max_q and contiguous
+ * k / v, both happen in one launch: the new rows are taken from k / v for
+ * the batch, written to the cache, and the device lengths advanced by the
+ * launch's last workgroup per slot, so a captured graph replays it at
+ * advancing lengths. Other layers take the two launches.
+ * Replaces the listener step's DynamicLayer.update (torch.cat,
+ * duplex_kernel/kv_cache.py:95-97) followed by _StaticPaddingWorkspace.padded
+ * / padded_mask (duplex_kernel/shape_stable_listener.py:28-69). */
+int kvrt_append_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
+                             const kvrt_tensor *k, const kvrt_tensor *v, const int32_t *start_pos,
+                             const kvrt_tensor *out_k, const kvrt_tensor *out_v,
+                             const kvrt_tensor *mask);
+
 /* Turn-local rollback: set the length of (slot, layer) to new_len
  * (layer = -1: every layer). Moves no KV bytes. Fails with KVRT_ESTATE when
  * the slot's generation is not expected_generation (KVRT_ANY_GENERATION

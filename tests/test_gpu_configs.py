@@ -102,7 +102,8 @@ def test_config3_listener_microbatch_gather_500_steps(n_streams):
     D 128; each step appends one listener frame (Q = 2 rows, the reference's
     GEMMA4_STREAM_Q_LEN) per stream, gathers the padded [N, 8, Lmax, 128] batch
     with its mask and attends over it (8 q heads); 500 steps, seed 2. Gather
-    bit-exact and attention of every layer at steps 0, 100, ..., 499."""
+    bit-exact and attention of every layer at steps 0, 100, ..., 499. Odd
+    layers take the fused append + gather call, even ones the two calls."""
     from kvrt import KVRuntime, LayerSpec, attend_tensors
 
     gen = torch.Generator().manual_seed(2)
@@ -122,8 +123,15 @@ def test_config3_listener_microbatch_gather_500_steps(n_streams):
     for step in range(500):
         for layer in range(n_layers):
             q, k, v = (randn_bf16(gen, (n_streams, 8, 2, 128), 0.5) for _ in range(3))
-            rt.append(layer, k.cuda(), v.cuda(), slots)
-            kpad, vpad, mask = rt.gather(layer, slots)
+            if layer % 2 == 0:
+                rt.append(layer, k.cuda(), v.cuda(), slots)
+                kpad, vpad, mask = rt.gather(layer, slots)
+            else:  # the fused append + gather (one launch)
+                lm = max(rt.seq_length(s, layer) for s in slots) + 2
+                kpad = torch.empty((n_streams, 8, lm, 128), dtype=torch.bfloat16, device="cuda")
+                vpad = torch.empty_like(kpad)
+                mask = torch.empty((n_streams, lm), dtype=torch.bool, device="cuda")
+                rt.append_gather(layer, k.cuda(), v.cuda(), slots, out=(kpad, vpad, mask))
             out = attend_tensors(q.cuda(), kpad, vpad, mask.sum(1).to(torch.int32), scale)
             for s in slots:
                 orc.append(s, layer, to_np(k[s]), to_np(v[s]))

@@ -870,9 +870,12 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
 // Workspace of the context-free tensor attention, one per (device, stream):
 // calls on one stream share it in stream order, calls on different streams
 // never do. Layout: the error flag (kTensorWsHead floats), the prefix masks
-// of the call's items (kMaxItems records), then the split-K partials.
+// of the call's items (kMaxItems records), the arrival counters of
+// single-launch decodes (zero between launches), then the split-K partials.
 constexpr size_t kTensorWsHead = 64;
 constexpr size_t kTensorWsMasks = kMaxItems * sizeof(PrefixMask) / sizeof(float);
+constexpr size_t kTensorWsCnt = (kCntItemBase + kMaxItems + 63) / 64 * 64;
+constexpr size_t kTensorWsParts = kTensorWsHead + kTensorWsMasks + kTensorWsCnt;
 
 struct TensorWorkspace {
     float *ptr = nullptr;
@@ -894,6 +897,7 @@ struct TensorCall {
     PrefixPackArgs pk{};
     bool masked = false;
     bool mfma = false;
+    bool single = false;  // the decode may merge its own partials (bit-identical to the merge kernel)
     int D = 0, rows = 0;
     size_t acc_elems = 0;
     size_t bytes = 0;
@@ -956,7 +960,11 @@ int tensor_call_setup(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_ten
     tc.D = (int)D;
     tc.rows = rows;
     tc.acc_elems = (size_t)n * hkv * a.n_split * Rw * D;
-    tc.bytes = (kTensorWsHead + kTensorWsMasks + tc.acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * Rw * 8;
+    tc.bytes = (kTensorWsParts + tc.acc_elems + 64) * 4 + (size_t)n * hkv * a.n_split * Rw * 8;
+    // At most 16 partials per (item, kv head): the last workgroup's merge
+    // rounds exactly as the merge kernel's, so the result does not depend on
+    // which of the two ran.
+    tc.single = a.n_parts <= 16 && single_launch_decode(KVRT_MERGE_AUTO, tc.mfma, (int)D, R, rows, a.n_parts);
     return KVRT_OK;
 }
 
@@ -980,10 +988,11 @@ int scratch_pointer(int dev, float **out) {
 
 // Enqueue a set-up call on workspace ws (at least tc.bytes, laid out as the
 // per-stream workspaces: error flag, masks, partials).
-int tensor_call_launch(TensorCall &tc, float *ws, hipStream_t st) {
+int tensor_call_launch(TensorCall &tc, float *ws, hipStream_t st, bool single) {
     DecodeArgs &a = tc.a;
     a.err = reinterpret_cast<int32_t *>(ws);
-    a.part_acc = ws + kTensorWsHead + kTensorWsMasks;
+    a.cnt = single && tc.single ? reinterpret_cast<uint32_t *>(ws + kTensorWsHead + kTensorWsMasks) : nullptr;
+    a.part_acc = ws + kTensorWsParts;
     a.part_ml = reinterpret_cast<float2 *>(a.part_acc + ((tc.acc_elems + 63) / 64) * 64);
     if (tc.masked) {
         tc.pk.dst = reinterpret_cast<PrefixMask *>(ws + kTensorWsHead);
@@ -1970,12 +1979,13 @@ int kvrt_attend_tensors_async(const kvrt_tensor *q, const kvrt_tensor *k, const 
         float *fresh = nullptr;
         const size_t want = std::max(tc.bytes, (size_t)1 << 20);
         if (hipMalloc(&fresh, want) != hipSuccess) return KVRT_EDEVICE;
-        if (launch_zero(fresh, kTensorWsHead * 4, st) != hipSuccess) return KVRT_EDEVICE;
+        // the error flag and the arrival counters start at zero
+        if (launch_zero(fresh, kTensorWsParts * 4, st) != hipSuccess) return KVRT_EDEVICE;
         if (ws.ptr) g_tensor_retired.push_back(ws.ptr);
         ws.ptr = fresh;
         ws.bytes = want;
     }
-    return tensor_call_launch(tc, ws.ptr, st);
+    return tensor_call_launch(tc, ws.ptr, st, true);
 }
 
 int kvrt_attend_tensors_noalloc_async(const kvrt_tensor *q, const kvrt_tensor *k, const kvrt_tensor *v,
@@ -1999,7 +2009,8 @@ int kvrt_attend_tensors_noalloc_async(const kvrt_tensor *q, const kvrt_tensor *k
     float *ws = nullptr;
     rc = scratch_pointer(dev, &ws);
     if (rc != KVRT_OK) return rc;
-    return tensor_call_launch(tc, ws, static_cast<hipStream_t>(stream));
+    // the merge kernel after the decode: the scratch holds no arrival counters
+    return tensor_call_launch(tc, ws, static_cast<hipStream_t>(stream), false);
 }
 
 int kvrt_tensors_status(void *stream) {

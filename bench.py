@@ -444,6 +444,24 @@ def run_kernels(args) -> int:
         sum(lens) * 8 * 128 * 2 * 2 + 4 * lmax * 8 * 128 * 2 * 2 + 4 * lmax, f"N=4, L={lens} -> [4,8,{lmax},128] + mask")
     rt.close()
 
+    # the same gather with the frame's Q 2 append in the launch (kvrt_append_gather_async); the
+    # lengths grow by 2 per call, so the batch is sized for the last call and the bytes are
+    # those of the median call
+    lmax_f = max(lens) + 2 * (w + r) + 2
+    rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)], 4, lmax_f + 8, max_q=2, device="cuda")
+    for s, n in enumerate(lens):
+        rt.import_(s, 0, bf((1, 8, n, 128)), bf((1, 8, n, 128)))
+    okf = torch.empty((4, 8, lmax_f, 128), dtype=torch.bfloat16, device="cuda")
+    ovf = torch.empty_like(okf)
+    mkf = torch.empty((4, lmax_f), dtype=torch.bool, device="cuda")
+    kf, vf = bf((4, 8, 2, 128)), bf((4, 8, 2, 128))
+    mid = [n + 2 * (w + r // 2) for n in lens]
+    add("append_gather_listener_n4", "gather_kernel<128,bf16,contig> + fused Q 2 append",
+        _event_median(lambda: rt.append_gather(0, kf, vf, [0, 1, 2, 3], out=(okf, ovf, mkf)), w, r),
+        sum(mid) * 8 * 128 * 2 * 2 + 4 * lmax_f * 8 * 128 * 2 * 2 + 4 * lmax_f + 2 * 4 * 8 * 2 * 128 * 2 * 2,
+        f"N=4, L~{mid} + 2 -> [4,8,{lmax_f},128] + mask, append read + written")
+    rt.close()
+
     # decode attention (fused append + attend where the layout allows)
     def decode_case(name, kernel, hq, hkv, d, n, L, qn=1, window=0, layout="contig", fused=True, dtype="bf16",
                     lens=None, wgs=0, **kw):

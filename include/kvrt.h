@@ -344,7 +344,9 @@ int kvrt_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *sl
  * k / v, both happen in one launch: the new rows are taken from k / v for
  * the batch, written to the cache, and the device lengths advanced by the
  * launch's last workgroup per slot, so a captured graph replays it at
- * advancing lengths. Other layers take the two launches.
+ * advancing lengths; a refused call there changes nothing. Other layers
+ * take the two launches, with the two calls' effect: an append that
+ * succeeds stays done if the gather is then refused.
  * Replaces the listener step's DynamicLayer.update (torch.cat,
  * duplex_kernel/kv_cache.py:95-97) followed by _StaticPaddingWorkspace.padded
  * / padded_mask (duplex_kernel/shape_stable_listener.py:28-69). */

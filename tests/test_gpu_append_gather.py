@@ -162,3 +162,37 @@ def test_fused_append_gather_refusals_change_nothing():
     np.testing.assert_array_equal(bits(ka), bits(kb))
     np.testing.assert_array_equal(bits(va), bits(vb))
     assert fused.health() == 0
+
+
+def test_fused_append_gather_at_the_item_and_head_limits():
+    """64 slots x 64 kv heads in one call (every per-(item, head) and
+    per-item arrival counter in use), three steps: bit for bit the two calls,
+    lengths advanced on every slot."""
+    from kvrt import LayerSpec
+
+    spec = LayerSpec(kv_heads=64, head_dim=64)
+    gen = torch.Generator().manual_seed(64)
+    n, hkv, d = 64, 64, 64
+    two, fused = _pair(spec, n, 64)
+    lens = [int(x) for x in torch.randint(0, 40, (n,), generator=gen)]
+    slots = list(range(n))[::-1]
+    for s, ln in zip(slots, lens):
+        if ln:
+            k, v = randn_bf16(gen, (1, hkv, ln, d)).cuda(), randn_bf16(gen, (1, hkv, ln, d)).cuda()
+            two.import_(s, 0, k, v)
+            fused.import_(s, 0, k, v)
+    for step in range(3):
+        k, v = randn_bf16(gen, (n, hkv, 2, d)).cuda(), randn_bf16(gen, (n, hkv, 2, d)).cuda()
+        lm = max(lens) + 2 * (step + 1)
+        two.append(0, k, v, slots)
+        ka, va, ma = two.gather(0, slots, lmax=lm)
+        kb = torch.empty((n, hkv, lm, d), dtype=torch.bfloat16, device="cuda")
+        vb, mb = torch.empty_like(kb), torch.empty((n, lm), dtype=torch.bool, device="cuda")
+        fused.append_gather(0, k, v, slots, out=(kb, vb, mb))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(ka), bits(kb), err_msg=f"step {step}")
+        np.testing.assert_array_equal(bits(va), bits(vb), err_msg=f"step {step}")
+        np.testing.assert_array_equal(ma.cpu().numpy(), mb.cpu().numpy())
+    fused.sync_lengths()
+    assert [fused.seq_length(s, 0) for s in slots] == [ln + 6 for ln in lens]
+    assert fused.health() == 0 and two.health() == 0

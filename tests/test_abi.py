@@ -184,6 +184,8 @@ def test_null_context_calls_fail_with_einval():
     slots = (ctypes.c_int32 * 1)(0)
     assert lib.kvrt_truncate(None, 0, 0, 0, 0) == L.KVRT_EINVAL
     assert lib.kvrt_append_async(None, 0, 1, slots, None, None) == L.KVRT_EINVAL
+    assert lib.kvrt_gather_async(None, 0, 1, slots, None, None, None, None) == L.KVRT_EINVAL
+    assert lib.kvrt_append_gather_async(None, 0, 1, slots, None, None, None, None, None, None) == L.KVRT_EINVAL
     assert lib.kvrt_health(None) == L.KVRT_EINVAL
     assert lib.kvrt_destroy(None) == L.KVRT_EINVAL
     assert lib.kvrt_attend_tensors_async(None, None, None, None, None, None, 1.0, 0, None) == L.KVRT_EINVAL

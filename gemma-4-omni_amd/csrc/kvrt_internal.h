@@ -285,11 +285,17 @@ struct PrefillArgs {
     int32_t slots[kMaxItems];
 };
 
+// Edits lens[idx[i]] = val[i]. With check set (a rollback), all of them or
+// none: only when every lens[idx[i]] still holds expect[i], the value the
+// host validated against; otherwise err[0] is raised and nothing changes.
 struct SetLenArgs {
     int32_t *lens;
     int32_t n;
+    int32_t check;
+    int32_t *err;
     int32_t idx[kPtUpdates];
     int32_t val[kPtUpdates];
+    int32_t expect[kPtUpdates];
 };
 
 // Static description of one layer, kept in device memory by the context

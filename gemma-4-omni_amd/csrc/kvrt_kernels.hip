@@ -2114,8 +2114,22 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int D
 // ---------------------------------------------------------------------------
 // small control kernels
 // ---------------------------------------------------------------------------
-__global__ void set_i32_kernel(SetLenArgs a) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// One workgroup of kPtUpdates threads, thread i edits entry i.
+__global__ __launch_bounds__(kPtUpdates) void set_i32_kernel(SetLenArgs a) {
+    const int i = threadIdx.x;
+    if (a.check) {
+        // a rollback validated against host lengths that the device no longer
+        // holds (a captured graph advanced it since): refuse it whole
+        __shared__ int stale;
+        if (i == 0) stale = 0;
+        __syncthreads();
+        if (i < a.n && a.lens[a.idx[i]] != a.expect[i]) stale = 1;
+        __syncthreads();
+        if (stale) {
+            if (i == 0) a.err[0] = 2;
+            return;
+        }
+    }
     if (i < a.n) a.lens[a.idx[i]] = a.val[i];
 }
 

@@ -80,6 +80,7 @@ struct kvrt_ctx {
     std::vector<Layer> layers;
     hipStream_t stream = nullptr;
     bool dirty = false;             // work enqueued since the bound stream was last synchronised
+    bool lens_stale = false;        // work captured into a graph since the host lengths were read back
     int device = 0;
     bool poisoned = false;
     bool inject = false;
@@ -118,8 +119,9 @@ int device_ok(kvrt_ctx *c, hipError_t e) {
     return KVRT_OK;
 }
 
-// Preamble of every mutating call. The context counts as having work in
-// flight on its bound stream from here until a synchronising call.
+// Preamble of every mutating call. A call refused by its argument checks
+// enqueues nothing and leaves the context as it was (enq below marks work in
+// flight).
 int begin(kvrt_ctx *c) {
     if (!c) return KVRT_EINVAL;
     if (c->poisoned) return KVRT_EPOISONED;
@@ -127,13 +129,28 @@ int begin(kvrt_ctx *c) {
         c->inject = false;
         return poison(c);
     }
-    c->dirty = true;
     // Switch devices only when needed: hipSetDevice is refused inside a
     // stream capture, and calls of one context are captured into graphs.
     int cur = -1;
     if (hipGetDevice(&cur) != hipSuccess) return poison(c);
     if (cur != c->device && hipSetDevice(c->device) != hipSuccess) return poison(c);
     return KVRT_OK;
+}
+
+// The bound stream, for an enqueue: the context counts as having work in
+// flight on it from here until a synchronising call. Work enqueued while the
+// stream is capturing only runs when the graph is replayed, which advances
+// the device lengths behind the host's back: the host lengths stay
+// unverified until kvrt_sync_lengths reads them back.
+hipStream_t enq(kvrt_ctx *c) {
+    c->dirty = true;
+    if (!c->lens_stale) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        const hipError_t e = hipStreamIsCapturing(c->stream, &st);
+        if (e != hipSuccess) (void)hipGetLastError();  // the launch that follows reports its own status
+        if (e != hipSuccess || st != hipStreamCaptureStatusNone) c->lens_stale = true;
+    }
+    return c->stream;
 }
 
 KVView make_view(kvrt_ctx *c, int layer) {
@@ -430,22 +447,29 @@ int map_items(kvrt_ctx *c, int n, const int32_t *slots, const std::vector<int> &
 int enqueue_pages(kvrt_ctx *c, const std::vector<int32_t> &idx, const std::vector<int32_t> &val) {
     if (idx.empty()) return KVRT_OK;
     c->counters.launches += (idx.size() + kPtUpdates - 1) / kPtUpdates;
-    if (launch_set_pages(c->d_pt, (int)idx.size(), idx.data(), val.data(), c->stream) != hipSuccess)
+    if (launch_set_pages(c->d_pt, (int)idx.size(), idx.data(), val.data(), enq(c)) != hipSuccess)
         return poison(c);
     return KVRT_OK;
 }
 
-int set_device_lens(kvrt_ctx *c, const std::vector<int32_t> &idx) {
+// Mirror host lengths len[idx[i]] to the device. With expect (a rollback),
+// the device edits only if it still holds expect[i] at every index (else it
+// raises the context's error flag), so a rollback validated against stale
+// host lengths never lands.
+int set_device_lens(kvrt_ctx *c, const std::vector<int32_t> &idx, const std::vector<int32_t> *expect = nullptr) {
     for (size_t off = 0; off < idx.size(); off += kPtUpdates) {
         SetLenArgs a{};
         a.lens = c->d_len;
         a.n = (int)std::min<size_t>(kPtUpdates, idx.size() - off);
+        a.check = expect != nullptr;
+        a.err = c->d_err;
         for (int i = 0; i < a.n; ++i) {
             a.idx[i] = idx[off + i];
             a.val[i] = c->len[idx[off + i]];
+            if (expect) a.expect[i] = (*expect)[off + i];
         }
         c->counters.launches++;
-        if (launch_set_lens(a, c->stream) != hipSuccess) return poison(c);
+        if (launch_set_lens(a, enq(c)) != hipSuccess) return poison(c);
     }
     return KVRT_OK;
 }
@@ -465,7 +489,7 @@ int set_prefix_len_device(kvrt_ctx *c, int slot, int len) {
     a.idx[0] = slot * (int)(sizeof(PrefixMask) / sizeof(int32_t));
     a.val[0] = len;
     c->counters.launches++;
-    if (launch_set_lens(a, c->stream) != hipSuccess) return poison(c);
+    if (launch_set_lens(a, enq(c)) != hipSuccess) return poison(c);
     c->slot[slot].prefix_len = len;
     return KVRT_OK;
 }
@@ -762,7 +786,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         TalkerArgs t{};
         static_cast<DecodeArgs &>(t) = a;
         for (int i = 0; i < n; ++i) t.talk[i] = titems[i];
-        if (launch_decode_talker(t, D, rows, c->stream) != hipSuccess) return poison(c);
+        if (launch_decode_talker(t, D, rows, enq(c)) != hipSuccess) return poison(c);
         for (int i = 0; i < n; ++i) {
             const uint64_t keys = (uint64_t)titems[i].audio_pos + 1;
             c->counters.attended_keys += keys * hkv;
@@ -770,7 +794,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         }
         return KVRT_OK;
     }
-    if ((mfma ? launch_decode_mfma(a, D, s.dtype, rows, c->stream) : launch_decode(a, D, s.dtype, rows, c->stream)) !=
+    if ((mfma ? launch_decode_mfma(a, D, s.dtype, rows, enq(c)) : launch_decode(a, D, s.dtype, rows, enq(c))) !=
         hipSuccess)
         return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
@@ -857,7 +881,7 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         grid_x = (int)std::max<int64_t>(1, std::min<int64_t>(4096, (chunks + 255) / 256));
     }
     c->counters.launches++;
-    if (launch_append(a, D, s.dtype, grid_x, c->stream) != hipSuccess) return poison(c);
+    if (launch_append(a, D, s.dtype, grid_x, enq(c)) != hipSuccess) return poison(c);
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
     for (int i = 0; i < n; ++i) {
         c->len_ref(slots[i], layer) += (int)qn;
@@ -1016,7 +1040,8 @@ uint32_t kvrt_abi_version(void) { return KVRT_ABI_VERSION; }
 uint64_t kvrt_capabilities(void) {
     return KVRT_CAP_CONTIG | KVRT_CAP_RING | KVRT_CAP_PAGED | KVRT_CAP_INT8 | KVRT_CAP_FUSED_APPEND_ATTEND |
            KVRT_CAP_GATHER | KVRT_CAP_DEVICE_LENGTHS | KVRT_CAP_TENSOR_ATTEND | KVRT_CAP_PREFILL_MFMA |
-           KVRT_CAP_TALKER_MASK | KVRT_CAP_PREFIX_ATTENTION | KVRT_CAP_SLOT_GENERATION | KVRT_CAP_STREAM_CONFINED;
+           KVRT_CAP_TALKER_MASK | KVRT_CAP_PREFIX_ATTENTION | KVRT_CAP_SLOT_GENERATION | KVRT_CAP_STREAM_CONFINED |
+           KVRT_CAP_ROLLBACK_POSITION;
 }
 
 const char *kvrt_strerror(int code) {
@@ -1222,6 +1247,10 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
     const int64_t S = k->dims[2];
     if (k->dims[0] != 1 || k->dims[1] != s.kv_heads || k->dims[3] != s.head_dim) return KVRT_EINVAL;
     if (S < 0 || S > c->cfg.capacity || first_pos < 0 || first_pos > S) return KVRT_EINVAL;
+    // an import starts a session: never over one that is live (rows on this
+    // layer, or a prefix mask), import_cache_async's `primed` refusal; the
+    // host must vouch for the lengths it checks
+    if (c->len_at(slot, layer) != 0 || c->slot[slot].prefix_len != 0 || c->lens_stale) return KVRT_ESTATE;
     int keep_from = first_pos;
     std::vector<int32_t> pidx, pval;
     if (s.layout == KVRT_LAYOUT_RING) {
@@ -1253,7 +1282,7 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
         const int64_t chunks = (int64_t)s.kv_heads * S * (s.head_dim / 8);
         int gx = (int)std::min<int64_t>(4096, (chunks + 255) / 256);
         c->counters.launches++;
-        if (launch_append(a, s.head_dim, s.dtype, std::max(1, gx), c->stream) != hipSuccess) return poison(c);
+        if (launch_append(a, s.head_dim, s.dtype, std::max(1, gx), enq(c)) != hipSuccess) return poison(c);
     } else {
         std::vector<int32_t> idx{(int32_t)((size_t)slot * c->cfg.n_layers + layer)};
         c->len_ref(slot, layer) = 0;
@@ -1263,6 +1292,8 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
     c->len_ref(slot, layer) = (int)S;
     c->counters.appended_rows += (uint64_t)S * s.kv_heads;
     c->counters.appended_bytes += (uint64_t)S * s.kv_heads * s.head_dim * 2 * (s.dtype == KVRT_INT8 ? 1 : 2);
+    // new contents: holders of the slot's previous generation are stale
+    renew_generation(c, slot);
     return KVRT_OK;
 }
 
@@ -1316,7 +1347,7 @@ int kvrt_write_positions_async(kvrt_ctx *c, int32_t layer, int32_t n, const int3
     a.import_mode = 2;
     a.err = c->d_err;
     c->counters.launches++;
-    if (launch_append(a, D, s.dtype, 1, c->stream) != hipSuccess) return poison(c);
+    if (launch_append(a, D, s.dtype, 1, enq(c)) != hipSuccess) return poison(c);
     for (int i = 0; i < n; ++i) {
         int &L = c->len_ref(slots[i], layer);
         L = std::max(L, a.pos_end[i]);
@@ -1339,7 +1370,7 @@ int kvrt_reset_slot_async(kvrt_ctx *c, int32_t slot) {
             const uint64_t bytes = (uint64_t)vw.slot_stride * 2;
             for (void *base : {vw.k, vw.v}) {
                 c->counters.launches++;
-                if (launch_zero(static_cast<uint8_t *>(base) + (uint64_t)slot * bytes, bytes, c->stream) != hipSuccess)
+                if (launch_zero(static_cast<uint8_t *>(base) + (uint64_t)slot * bytes, bytes, enq(c)) != hipSuccess)
                     return poison(c);
             }
         }
@@ -1382,7 +1413,7 @@ int kvrt_set_prefix_attention_async(kvrt_ctx *c, int32_t slot, const kvrt_tensor
     a.dst = c->d_prefix;
     a.index[0] = slot;
     c->counters.launches++;
-    if (launch_prefix_pack(a, c->stream) != hipSuccess) return poison(c);
+    if (launch_prefix_pack(a, enq(c)) != hipSuccess) return poison(c);
     c->slot[slot].prefix_len = a.plen;
     return KVRT_OK;
 }
@@ -1454,7 +1485,11 @@ static int gather_impl(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slo
         a.start[i] = st;
         a.slots[i] = slots[i];
     }
-    a.has_start = 1;
+    // RING without start_pos: the kernel derives max(0, L - (W - 1)) from
+    // the device length, so a captured call replays with the window moving
+    // along (the host value above only validates this call); CONTIG starts
+    // at 0 either way; PAGED starts at the host's first live page
+    a.has_start = start_pos != nullptr || s.layout == KVRT_LAYOUT_PAGED;
     a.kv = make_view(c, layer);
     a.len = make_len(c, layer);
     a.out_k = out_k->data;
@@ -1477,7 +1512,7 @@ static int gather_impl(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slo
         a.qn = qn;
     }
     c->counters.launches++;
-    if (launch_gather(a, s.head_dim, s.dtype, c->stream) != hipSuccess) return poison(c);
+    if (launch_gather(a, s.head_dim, s.dtype, enq(c)) != hipSuccess) return poison(c);
     c->counters.gathered_bytes += (uint64_t)n * s.kv_heads * lmax * s.head_dim * 2 * elem_size(out_dtype);
     for (int i = 0; k && i < n; ++i) {
         c->len_ref(slots[i], layer) += qn;
@@ -1513,12 +1548,17 @@ int kvrt_append_gather_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_
     return gather_impl(c, layer, n, slots, start_pos, out_k, out_v, mask, nullptr, nullptr);
 }
 
-int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation) {
+int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation,
+                  int32_t expected_len) {
     int rc = begin(c);
     if (rc) return rc;
-    if (!valid_slot(c, slot) || layer < -1 || layer >= c->cfg.n_layers || new_len < 0) return KVRT_EINVAL;
-    // identity and the rewind floor: the prefix-attention mask's positions stay
-    if (!generation_ok(c, slot, expected_generation) || new_len < c->slot[slot].prefix_len) return KVRT_ESTATE;
+    if (!valid_slot(c, slot) || layer < -1 || layer >= c->cfg.n_layers || new_len < 0 || expected_len < -1)
+        return KVRT_EINVAL;
+    // identity and the rewind floor: the prefix-attention mask's positions
+    // stay; lengths the host cannot vouch for (captured work since the last
+    // read-back) refuse the rollback
+    if (!generation_ok(c, slot, expected_generation) || new_len < c->slot[slot].prefix_len || c->lens_stale)
+        return KVRT_ESTATE;
     std::vector<int> targets;
     for (int l = 0; l < c->cfg.n_layers; ++l) {
         if (layer >= 0 && l != layer) continue;
@@ -1529,17 +1569,20 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
     for (int l : targets) {
         const kvrt_layer_spec &s = c->layers[l].spec;
         const int L = c->len_at(slot, l);
-        if (new_len > L) return KVRT_ESTATE;
+        // the caller's position must be the slot's (rewind_session_async's
+        // current_position == valid_kv_len)
+        if (new_len > L || (expected_len >= 0 && L != expected_len)) return KVRT_ESTATE;
         if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && new_len - s.window + 1 < L - s.ring_rows)
             return KVRT_ESTATE;
         if (s.layout == KVRT_LAYOUT_PAGED && new_len < c->first_live[slot] * c->cfg.block_size && new_len < L)
             return KVRT_ESTATE;
     }
-    std::vector<int32_t> idx;
+    std::vector<int32_t> idx, before;
     for (int l : targets) {
         int &L = c->len_ref(slot, l);
         if (L == new_len) continue;
         c->counters.truncated_rows += (uint64_t)(L - new_len);
+        before.push_back(L);
         L = new_len;
         idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
     }
@@ -1561,7 +1604,7 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
         if (keep == 0) c->first_live[slot] = 0;
     }
     c->counters.truncations++;
-    return set_device_lens(c, idx);
+    return set_device_lens(c, idx, &before);
 }
 
 int kvrt_evict(kvrt_ctx *c, int32_t slot, int32_t keep_from) {
@@ -1665,7 +1708,7 @@ int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int
     auto flush = [&]() -> int {
         if (a.n_entries == 0) return KVRT_OK;
         dst->counters.launches++;
-        if (launch_slot_copy(a, max_units, dst->stream) != hipSuccess) return poison(dst);
+        if (launch_slot_copy(a, max_units, enq(dst)) != hipSuccess) return poison(dst);
         a.n_entries = 0;
         max_units = 0;
         return KVRT_OK;
@@ -1699,7 +1742,7 @@ int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int
     m.d0 = m.d1 = m.rows = 1;
     m.row_bytes = sizeof(PrefixMask);
     dst->counters.launches++;
-    if (launch_copy_rows(m, dst->stream) != hipSuccess) return poison(dst);
+    if (launch_copy_rows(m, enq(dst)) != hipSuccess) return poison(dst);
     dst->slot[dst_slot].prefix_len = src_plen;
     renew_generation(dst, dst_slot);
     return KVRT_OK;
@@ -1794,7 +1837,7 @@ int kvrt_rollover_async(kvrt_ctx *c, int32_t slot, int32_t prefix_len, int32_t r
         bytes += (uint64_t)retained_rows * s.kv_heads * s.head_dim * 2 * 2;
         if (a.n_entries == kMaxMoveLayers) {
             c->counters.launches++;
-            if (launch_slot_rebase(a, max_heads, c->stream) != hipSuccess) return poison(c);
+            if (launch_slot_rebase(a, max_heads, enq(c)) != hipSuccess) return poison(c);
             a.n_entries = 0;
         }
         c->len_ref(slot, l) = prefix_len + retained_rows;
@@ -1802,7 +1845,7 @@ int kvrt_rollover_async(kvrt_ctx *c, int32_t slot, int32_t prefix_len, int32_t r
     }
     if (a.n_entries) {
         c->counters.launches++;
-        if (launch_slot_rebase(a, max_heads, c->stream) != hipSuccess) return poison(c);
+        if (launch_slot_rebase(a, max_heads, enq(c)) != hipSuccess) return poison(c);
     }
     c->counters.truncations++;
     c->counters.truncated_rows += (uint64_t)(L - prefix_len - retained_rows) * idx.size();
@@ -1952,7 +1995,7 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     a.scale_log2 = scale * 1.4426950408889634f;
     for (int i = 0; i < n; ++i) a.slots[i] = slots[i];
     c->counters.launches += a.n_ksplit > 1 ? 2 : 1;
-    if (launch_prefill(a, D, c->stream) != hipSuccess) return poison(c);
+    if (launch_prefill(a, D, enq(c)) != hipSuccess) return poison(c);
     c->counters.attended_keys += tile_keys * hkv;
     c->counters.attended_bytes += tile_keys * hkv * (uint64_t)D * 2 * 2;
     return KVRT_OK;
@@ -2077,6 +2120,7 @@ int kvrt_sync_lengths(kvrt_ctx *c) {
         if (dev[i] < 0 || dev[i] > c->cfg.capacity) return KVRT_EFAULT;
     }
     c->len = dev;
+    c->lens_stale = false;
     return KVRT_OK;
 }
 

@@ -10,7 +10,7 @@ from ctypes import POINTER, c_float, c_int32, c_int64, c_uint32, c_uint64, c_voi
 
 from ._build import LIB_PATH
 
-KVRT_ABI_VERSION = 2
+KVRT_ABI_VERSION = 3
 KVRT_MAX_RANK = 4
 KVRT_MAX_ROLLOVER_ROWS = 128
 KVRT_MAX_ITEMS = 64
@@ -50,6 +50,7 @@ CAP_TALKER_MASK = 1 << 9
 CAP_PREFIX_ATTENTION = 1 << 10
 CAP_SLOT_GENERATION = 1 << 11
 CAP_STREAM_CONFINED = 1 << 12
+CAP_ROLLBACK_POSITION = 1 << 13
 
 
 class KvrtTensor(ctypes.Structure):
@@ -165,7 +166,7 @@ SIGNATURES = [
     ("kvrt_slot_info_get", c_int32, [c_void_p, c_int32, POINTER(KvrtSlotInfo)]),
     ("kvrt_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T, _T]),
     ("kvrt_append_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _I32P, _T, _T, _T]),
-    ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
+    ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64, c_int32]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),
     ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
     ("kvrt_copy_session_async", c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_uint64]),

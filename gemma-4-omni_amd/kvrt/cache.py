@@ -98,6 +98,10 @@ class KVRTCache:
         self._owns_slot = slot is None
         self.slot = runtime.acquire_slot() if slot is None else int(slot)
         self.layers = [KVRTCacheLayer(self, i) for i in range(len(runtime.layers))]
+        # the slot's generation when this cache took it (or last changed its
+        # contents): rollbacks through this cache are refused once the slot
+        # holds another session
+        self.generation = runtime.slot_generation(self.slot)
         # Gemma shared-KV sources, as the reference keeps them on its
         # DynamicCache (shape_stable_listener.py:222-226, :234-238).
         self.shared_layers: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
@@ -185,16 +189,21 @@ class KVRTCache:
             new_len = max(0, length + tokens)
         else:
             return
-        self.runtime.truncate(self.slot, new_len, layer=layer)
+        self.runtime.truncate(self.slot, new_len, layer=layer, generation=self.generation, expected_len=length)
 
     def truncate(self, keep_len: int) -> None:
         """Rollback every layer to ``keep_len`` positions (no KV byte moves)."""
-        self.runtime.truncate(self.slot, int(keep_len))
+        self.runtime.truncate(self.slot, int(keep_len), generation=self.generation)
 
     def reset(self) -> None:
         """Zero the slot's rows and lengths (``_SlotKVCache.reset``)."""
-        self.runtime.reset_slot(self.slot)
+        self.generation = self.runtime.reset_slot(self.slot)
         self.shared_layers.clear()
+
+    def adopt(self) -> None:
+        """Take the slot's current generation after its contents were replaced
+        through the runtime (an import or a copy into it)."""
+        self.generation = self.runtime.slot_generation(self.slot)
 
     def __len__(self) -> int:
         return len(self.layers)
@@ -213,7 +222,7 @@ class KVRTCache:
         if len(lengths) != 1:
             raise ValueError("KVRTCache deepcopy needs every layer at one length")
         clone = KVRTCache(self.runtime)
-        self.runtime.copy_prefix(self.slot, clone.slot, lengths.pop())
+        clone.generation = self.runtime.copy_prefix(self.slot, clone.slot, lengths.pop(), generation=self.generation)
         memo[id(self)] = clone
         return clone
 

@@ -372,7 +372,11 @@ class KVRuntime:
 
     # ---- KV operations -----------------------------------------------------
     def import_(self, slot: int, layer: int, k: torch.Tensor, v: torch.Tensor, first_pos: int = 0) -> None:
-        """Import an HF layer view [1, kv_heads, S, D] bf16 as positions 0..S-1."""
+        """Import an HF layer view [1, kv_heads, S, D] bf16 as positions 0..S-1.
+
+        The layer must be empty and the slot unmasked (a fresh, reset or
+        released slot), else ``KVRTError`` code -2; the slot's generation is
+        renewed (import_cache_async refuses a primed slot, impl.inc:2595)."""
         require_cuda(k, "k")
         require_cuda(v, "v")
         self._bind()
@@ -446,14 +450,14 @@ class KVRuntime:
         shared layers' entries are ignored) and set its prefix mask. Returns
         the slot's generation. Mirrors gemma4_listener_batch_import_cache_async
         (gemma4_listener_microbatch_impl.inc:2590-2640)."""
-        gen = self.reset_slot(slot)
+        self.reset_slot(slot)
         for i, kv in enumerate(layers):
             if self._owner(i) != i:
                 continue
             self.import_(slot, i, kv[0], kv[1])
         if prefix_attention is not None:
             self.set_prefix_attention(slot, prefix_attention)
-        return gen
+        return self.slot_generation(slot)
 
     # Query rows per kv head (g * Q) above which attention runs on the MFMA
     # prefill kernel instead of the split-K decode kernel.
@@ -602,14 +606,21 @@ class KVRuntime:
                "kvrt_append_gather_async")
         return out_k, out_v, mask
 
-    def truncate(self, slot: int, new_len: int, layer: int = -1, generation: int = L.KVRT_ANY_GENERATION) -> None:
+    def truncate(self, slot: int, new_len: int, layer: int = -1, generation: int = L.KVRT_ANY_GENERATION,
+                 expected_len: int = -1) -> None:
         """Rollback to new_len positions: a length edit, no KV bytes move.
 
         Refused (``KVRTError`` code -2, nothing changes) below the slot's prefix
-        mask or, with a nonzero ``generation``, when the slot has been
-        replaced since (rewind_session_async's identity check, impl.inc:3588-3618)."""
+        mask; with a nonzero ``generation``, when the slot has been replaced
+        since; with ``expected_len`` >= 0, when a layer's length is not that
+        position; and after a graph capture until :meth:`sync_lengths`
+        (rewind_session_async's identity and position checks,
+        impl.inc:3588-3618). A rollback the host accepted against lengths that
+        graph replays have since advanced is dropped on the device and
+        reported by :meth:`health` (code -6)."""
         self._bind()
-        _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len), int(generation)), "kvrt_truncate")
+        _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len), int(generation), int(expected_len)),
+               "kvrt_truncate")
 
     def evict(self, slot: int, keep_from: int) -> None:
         self._own()

@@ -84,6 +84,7 @@ def import_dynamic_cache(cache: Any, target: KVRTCache) -> int:
     for i, (k, v) in enumerate(layers):
         if rt._owner(i) == i:
             rt.import_(target.slot, i, k, v)
+    target.adopt()
     return seq
 
 

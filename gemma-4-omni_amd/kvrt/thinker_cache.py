@@ -124,7 +124,7 @@ def _copy_kvrt(source: KVRTCache, target: KVRTCache, n: int) -> CachePrefixCopyR
             raise CachePrefixCopyError(f"layer {i} length differs from the source cache length")
         if target.get_seq_length(i) != 0:
             raise CachePrefixCopyError(f"target layer {i} is not empty")
-    rt.copy_prefix(source.slot, target.slot, n)
+    target.generation = rt.copy_prefix(source.slot, target.slot, n, generation=source.generation)
     copied = sum(2 * rt.layers[i].kv_heads * n * rt.layers[i].head_dim * 2 for i in owned)
     if _cache_length(target) != n:
         raise CachePrefixCopyError("target length does not match the copied prefix")

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define KVRT_ABI_VERSION 2u
+#define KVRT_ABI_VERSION 3u
 #define KVRT_MAX_RANK 4
 #define KVRT_MAX_ITEMS 64      /* slots per batched call                 */
 #define KVRT_MAX_POSITIONS 128 /* rows per kvrt_write_positions_async call */
@@ -78,6 +78,7 @@ extern "C" {
 #define KVRT_CAP_PREFIX_ATTENTION (1ull << 10)
 #define KVRT_CAP_SLOT_GENERATION (1ull << 11)
 #define KVRT_CAP_STREAM_CONFINED (1ull << 12)
+#define KVRT_CAP_ROLLBACK_POSITION (1ull << 13) /* truncate checks expected_len; import refuses live slots */
 
 /* ---- enums ------------------------------------------------------------- */
 enum kvrt_layout {
@@ -244,6 +245,15 @@ int kvrt_layer_storage(kvrt_ctx *ctx, int32_t layer, kvrt_storage *out);
  * to S. RING keeps the last ring_rows rows; PAGED allocates pages (pages
  * wholly below first_pos are not stored: first_pos = 0 stores all); INT8
  * quantises on import.
+ * An import starts a session: it fails with KVRT_ESTATE, changing nothing,
+ * when the (slot, layer) holds rows, when the slot has a prefix-attention
+ * mask, or while the host lengths are unverified (work of this context was
+ * captured into a graph since the last kvrt_sync_lengths). Reset, release
+ * (truncate to 0 with the mask cleared) or a fresh slot take one. A
+ * successful import renews the slot's generation: holders of the previous
+ * one are refused by truncate, copy and rollover (as
+ * gemma4_listener_batch_import_cache_async refuses a primed slot and takes
+ * the row's identity, gemma4_listener_microbatch_impl.inc:2595, :2629-2637).
  * Replaces gemma4_cache_import_async (gemma4_listener_cache.cu:278-301),
  * qwen_talker import_cache_prefix (qwen_talker_kernels.cu:276-294,
  * qwen_talker.cu:1060-1110) and the Python copy at
@@ -329,8 +339,10 @@ int kvrt_slot_info_get(kvrt_ctx *ctx, int32_t slot, kvrt_slot_info *out);
  * dequantised for INT8 layers); row j of item i holds position
  * start_i + j for j < L_i - start_i, zeros after. mask [n, Lmax] (KVRT_BOOL:
  * 1 valid / 0 pad, or KVRT_FP32 / KVRT_BF16: 0 valid / finfo.min pad) may be
- * NULL. start_pos may be NULL (contig/paged: 0, ring: max(0, L-(W-1)) which
- * is the HF DynamicSlidingWindowLayer retained range).
+ * NULL. start_pos may be NULL (contig: 0, paged: the first live page, ring:
+ * max(0, L-(W-1)) which is the HF DynamicSlidingWindowLayer retained range;
+ * for contig and ring the kernel takes L from the device length, so a
+ * captured call replays with the window moving along).
  * Replaces _StaticPaddingWorkspace.padded / padded_mask
  * (duplex_kernel/shape_stable_listener.py:28-69). */
 int kvrt_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int32_t *slots,
@@ -358,18 +370,28 @@ int kvrt_append_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
 /* Turn-local rollback: set the length of (slot, layer) to new_len
  * (layer = -1: every layer). Moves no KV bytes. Fails with KVRT_ESTATE when
  * the slot's generation is not expected_generation (KVRT_ANY_GENERATION
- * skips the check), when new_len exceeds the current length or lies below
- * the slot's prefix-attention mask (the rewind floor), or when a RING layer
- * would need rows already overwritten (L > ring_rows and new_len - window + 1
- * < L - ring_rows, i.e. a rollback deeper than ring_rows - window + 1
- * positions). Nothing changes when it fails.
+ * skips the check), when expected_len >= 0 and a targeted layer's length is
+ * not expected_len (the caller's position is not the slot's; -1 skips the
+ * check), when new_len exceeds the current length or lies below the slot's
+ * prefix-attention mask (the rewind floor), while the host lengths are
+ * unverified (work of this context was captured into a graph since the
+ * last kvrt_sync_lengths), or when a RING layer would need rows already
+ * overwritten (L > ring_rows and new_len - window + 1 < L - ring_rows, i.e.
+ * a rollback deeper than ring_rows - window + 1 positions). Nothing changes
+ * when it fails. The device applies the edit only where it still holds the
+ * lengths the host validated against; where a graph replay has advanced
+ * them since (replays after a kvrt_sync_lengths), the edit is dropped whole
+ * and kvrt_health reports KVRT_EFAULT (kvrt_sync_lengths then reloads the
+ * device's lengths).
  * Replaces TurnKVState.truncate_to_prefix / _slice_kv
  * (duplex_kernel/kv_cache.py:99-104, :205-216), gemma4_cache_truncate_async
  * (gemma4_listener_cache.cu:409-421) and the identity-checked
  * gemma4_listener_batch_rewind_session_async
- * (gemma4_listener_microbatch_impl.inc:3588-3618: stale identity or a target
- * below prefix_len -> -2). */
-int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation);
+ * (gemma4_listener_microbatch_impl.inc:3588-3618: a stale identity, a
+ * sequence position that is not the slot's, current_position !=
+ * valid_kv_len, or a target below prefix_len -> -2). */
+int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation,
+                  int32_t expected_len);
 
 /* PAGED: release every page of slot wholly below position keep_from (all
  * layers share one page table per slot). Positions below keep_from must not
@@ -570,7 +592,8 @@ int kvrt_copy_rows_async(const kvrt_tensor *src, const kvrt_tensor *dst, int64_t
 int kvrt_session_state(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t *length);
 /* Synchronise the bound stream and reload the host lengths from the device
  * mirror. Needed after replaying a captured HIP graph of append / fused
- * calls: replays advance the device lengths only. The split count and
+ * calls: replays advance the device lengths only. After work of the context
+ * was captured, import and truncate are refused until this call. The split count and
  * workspace of a captured call are fixed at capture; lengths must stay within
  * capacity and, for PAGED layers, within mapped pages. No counterpart in the
  * reference (its graphs use a device cursor, qwen_talker_kernels.cu:349-374). */

@@ -46,11 +46,11 @@ def test_every_declared_function_is_exported_and_bound():
 
 def test_version_capabilities_and_error_strings():
     L, lib = _lib()
-    assert lib.kvrt_abi_version() == L.KVRT_ABI_VERSION == 2
+    assert lib.kvrt_abi_version() == L.KVRT_ABI_VERSION == 3
     caps = lib.kvrt_capabilities()
     for bit in (L.CAP_CONTIG, L.CAP_RING, L.CAP_PAGED, L.CAP_INT8, L.CAP_FUSED_APPEND_ATTEND, L.CAP_GATHER,
                 L.CAP_DEVICE_LENGTHS, L.CAP_TENSOR_ATTEND, L.CAP_PREFILL_MFMA, L.CAP_TALKER_MASK,
-                L.CAP_PREFIX_ATTENTION, L.CAP_SLOT_GENERATION, L.CAP_STREAM_CONFINED):
+                L.CAP_PREFIX_ATTENTION, L.CAP_SLOT_GENERATION, L.CAP_STREAM_CONFINED, L.CAP_ROLLBACK_POSITION):
         assert caps & bit
     assert L.strerror(0) == "ok"
     for code in range(-1, -7, -1):
@@ -182,7 +182,7 @@ def test_create_rejects_invalid_configs_before_touching_the_device(bad):
 def test_null_context_calls_fail_with_einval():
     L, lib = _lib()
     slots = (ctypes.c_int32 * 1)(0)
-    assert lib.kvrt_truncate(None, 0, 0, 0, 0) == L.KVRT_EINVAL
+    assert lib.kvrt_truncate(None, 0, 0, 0, 0, -1) == L.KVRT_EINVAL
     assert lib.kvrt_append_async(None, 0, 1, slots, None, None) == L.KVRT_EINVAL
     assert lib.kvrt_gather_async(None, 0, 1, slots, None, None, None, None) == L.KVRT_EINVAL
     assert lib.kvrt_append_gather_async(None, 0, 1, slots, None, None, None, None, None, None) == L.KVRT_EINVAL

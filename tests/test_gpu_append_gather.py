@@ -84,13 +84,17 @@ def test_fused_append_gather_equals_append_then_gather(layout, qn):
     np.testing.assert_array_equal(bits(va), bits(vb))
 
 
-def test_fused_append_gather_graph_replays_at_advancing_lengths():
-    """One captured fused call (4 slots, Q 2, CONTIG D 128) replayed 8 times
-    with fresh rows copied in: every replay's batch equals the two eager calls
-    of a second runtime bit for bit, and the device lengths advance by 2."""
-    spec, _ = _specs()["contig"]
+@pytest.mark.parametrize("layout", ["contig", "ring"])
+def test_fused_append_gather_graph_replays_at_advancing_lengths(layout):
+    """One captured fused call (4 slots, Q 2; CONTIG 8 x D 128, or RING
+    window 64 / 65 rows, 1 x D 256) replayed 8 times with fresh rows copied
+    in: every replay's batch and mask equal the two eager calls of a second
+    runtime bit for bit (on RING the window start moves with the device
+    length), and the device lengths advance by 2."""
+    spec, _ = _specs()[layout]
     gen = torch.Generator().manual_seed(11)
-    n, hkv, d, qn, lmax = 4, 8, 128, 2, 700
+    n, hkv, d, qn = 4, spec.kv_heads, spec.head_dim, 2
+    lmax = 700 if layout == "contig" else 64
     two, fused = _pair(spec, n, 720)
     lens = [454, 610, 334, 542]
     slots = list(range(n))

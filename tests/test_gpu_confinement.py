@@ -89,12 +89,14 @@ def test_stale_generations_are_refused_and_change_nothing():
 
     gen = torch.Generator().manual_seed(3)
     rt = _rt()
-    g1 = rt.reset_slot(0)
+    g0 = rt.reset_slot(0)
     _fill(rt, 0, 300, gen)
+    g1 = rt.slot_generation(0)  # the imports renewed it
     rt.synchronize()
-    g2 = rt.reset_slot(0)  # a new session in slot 0: holders of g1 are stale
+    rt.reset_slot(0)  # a new session in slot 0: holders of g1 are stale
     _fill(rt, 0, 300, gen)
-    assert g1 != g2 and g2 == rt.slot_generation(0) and g1 != 0
+    g2 = rt.slot_generation(0)
+    assert len({g0, g1, g2}) == 3 and 0 not in (g0, g1, g2)
     k0, v0, _ = rt.gather(0, [0])
     torch.cuda.synchronize()
     before = rt.counters()

@@ -111,16 +111,22 @@ def test_append_fills_capacity_then_refuses_without_changes():
 
 
 def test_empty_import_leaves_an_empty_layer():
-    """An import replaces the layer's positions with its S rows, so S = 0 (an
-    empty torch tensor, whose data pointer is null) empties the layer; the
-    next fused step then sees only its own key."""
-    from kvrt import KVRuntime, LayerSpec
+    """An import fills an empty layer with its S rows, so S = 0 (an empty
+    torch tensor, whose data pointer is null) leaves it empty; an import over
+    a layer that holds rows is refused (code -2, nothing changes) until the
+    slot is emptied. The next fused step then sees only its own key."""
+    from kvrt import KVRTError, KVRuntime, LayerSpec
 
     gen = torch.Generator().manual_seed(1)
     rt = KVRuntime([LayerSpec(kv_heads=2, head_dim=64)], 2, 32, max_q=1, device="cuda")
     k = randn_bf16(gen, (1, 2, 5, 64)).cuda()
     rt.import_(1, 0, k, k)
     e = torch.empty((1, 2, 0, 64), dtype=torch.bfloat16, device="cuda")
+    before = rt.counters()
+    with pytest.raises(KVRTError) as err:
+        rt.import_(1, 0, e, e)
+    assert err.value.code == -2 and rt.counters() == before and rt.seq_length(1, 0) == 5
+    rt.truncate(1, 0)
     rt.import_(1, 0, e, e)
     rt.import_(0, 0, e, e)
     torch.cuda.synchronize()

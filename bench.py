@@ -485,14 +485,18 @@ def run_kernels(args) -> int:
         o = torch.empty_like(q)
         slots = list(range(n))
         sc = 1.0 / math.sqrt(d)
-        if fused:
+        if fused == "two":  # the append kernel, then the decode
+            def fn():
+                rt.append(0, kn, vn, slots)
+                rt.attend(0, q, slots, sc, out=o)
+        elif fused:
             fn = lambda: rt.append_attend(0, q, kn, vn, slots, sc, out=o)  # noqa: E731
         else:
             fn = lambda: rt.attend(0, q, slots, sc, out=o)  # noqa: E731
         c0 = rt.counters()
         t = _event_median(fn, w, r)
         c1 = rt.counters()
-        if c1["launches"] - c0["launches"] > w + r:  # the decode did not merge its own partials
+        if c1["launches"] - c0["launches"] > (2 if fused == "two" else 1) * (w + r):  # a separate merge
             kernel += " + merge_kernel"
         if kernel.startswith("decode_kernel") and c1["mfma_decodes"] - c0["mfma_decodes"] == w + r:
             raise RuntimeError(f"kernel case {name}: expected the VALU decode, AUTO chose the MFMA kernel")
@@ -523,6 +527,14 @@ def run_kernels(args) -> int:
     decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> (attend only)", 16, 8, 128, 16, 0,
                 window=4096, layout="paged", fused=False, dtype="int8", lens=lens5, block_size=16,
                 pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
+    # config 5's per-layer call: the append quantised inside the decode launch, and the
+    # same step as the append kernel followed by the decode
+    decode_case("decode_int8_paged_fused", "decode_kernel<128,2,int8,paged> (quantise-on-append in the launch)",
+                16, 8, 128, 16, 0, window=4096, layout="paged", fused=True, dtype="int8", lens=lens5,
+                block_size=16, pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
+    decode_case("decode_int8_paged_two_launch", "append_kernel<128,int8,paged> + decode_kernel<128,2,int8,paged>",
+                16, 8, 128, 16, 0, window=4096, layout="paged", fused="two", dtype="int8", lens=lens5,
+                block_size=16, pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
 
     # slot lifecycle: clone a 4096-position talker session (28 layers, one launch)
     rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)] * 28, 2, 4096 + 64, max_q=1, device="cuda")
@@ -898,9 +910,9 @@ def run_configs(args) -> int:
     steps, n, wnd, bs = 64, 16, 4096, 16
     lg = torch.Generator().manual_seed(4)
     lens = [int(x) for x in torch.randint(256, 8193, (n,), generator=lg)]
-    pages = n * (wnd // bs + 8)
+    pages = n * (wnd // bs + 16)  # the window's pages, plus the graph replays' reservation
     spec = LayerSpec(kv_heads=8, head_dim=128, layout="paged", dtype="int8", window=wnd)
-    rt = KVRuntime([spec] * 28, n, 8192 + steps + 16, max_q=1, block_size=bs, pool_pages=pages, pool_seed=4,
+    rt = KVRuntime([spec] * 28, n, 8192 + 2 * steps + 32, max_q=1, block_size=bs, pool_pages=pages, pool_seed=4,
                    device="cuda")
     for layer in range(28):
         for s, ln in enumerate(lens):
@@ -921,6 +933,25 @@ def run_configs(args) -> int:
             rt.evict(s, max(0, rt.seq_length(s, 0) + 1 - wnd))
 
     gpu_s = _gpu_timed(c5, steps)
+
+    # graph: the pages of the replays are reserved up front (kvrt_reserve_async), so the captured
+    # step's fused appends cross page boundaries without a page-table edit; eviction runs between
+    # replays on the host (after reading the device lengths back)
+    def c5g(i):
+        for layer in range(28):
+            q, k, v = ins[0][layer]
+            rt.append_attend(layer, q, k, v, slots, 1 / math.sqrt(128), out=outs[layer])
+
+    def between5(i):
+        if i > 0 and i % 16 == 0:
+            rt.sync_lengths()
+            for s in slots:
+                rt.evict(s, max(0, rt.seq_length(s, 0) + 1 - wnd))
+
+    rt.synchronize()
+    for s in slots:
+        rt.reserve(s, steps + 2)  # graph_time's eager step plus the replays
+    g_s = graph_time(rt, c5g, steps, between5)
     vis = sum(min(ln + steps // 2, wnd) for ln in lens)
     row5 = 8 * (128 + 4)  # int8 row + fp32 scale per head
     b5 = 28 * (2 * row5 * vis + n * (2 * 8 * 128 * 2 + 2 * row5) + 2 * n * 16 * 128 * 2)
@@ -959,7 +990,9 @@ def run_configs(args) -> int:
         cpu = _cpu_timed(c5c, steps, budget)
     report("5", f"paged int8: 16 sessions (L0 U[256, 8192]), 16-token pages over a shuffled shared pool, "
            "8 kv heads / 16 q heads, D 128, 28 layers, window 4096; per step append (quantise), decode "
-           "(dequantise in-kernel), evict pages older than the window; 64 steps", n, gpu_s, b5, cpu)
+           "(dequantise in-kernel), evict pages older than the window; 64 steps", n, gpu_s, b5, cpu, g_s,
+           graph_timing="one captured step replayed (pages reserved ahead, eviction between replays), host "
+                        "clock around all replays")
     rt.close()
 
     best = max(results, key=lambda x: x["gpu"]["frac"])

@@ -204,6 +204,14 @@ struct DecodeArgs {
     const PrefixMask *pmask;  // non-null: prefix-attention masks, indexed by slot
     uint8_t order[kMaxItems];  // PAGED: item of grid z-index i, the most visible keys first
     float scale_log2;       // softmax scale * log2(e)
+    // PAGED fused appends: page-table edits page_table[upd_idx[i]] = upd_val[i]
+    // that map the new rows' pages (a slot's rows crossing into a new block).
+    // The launch's first workgroup writes them into the table; no workgroup of
+    // the launch reads those entries (the new rows come from k_new / v_new),
+    // and the workgroups storing the new rows take their page from here.
+    int32_t n_upd;
+    int32_t upd_idx[kMaxItems];
+    int32_t upd_val[kMaxItems];
     int32_t slots[kMaxItems];
 };
 

@@ -99,6 +99,76 @@ __device__ __forceinline__ int64_t paged_offset(const KVView &v, int slot, int h
     return (((int64_t)page * v.kv_heads + head) * v.rows + (pos & (v.rows - 1))) * (int64_t)D;
 }
 
+// Symmetric int8 quantisation of one (token, head) row whose D values are
+// spread over G consecutive lanes, NV per lane: scale = amax / 127,
+// q = clamp(rne(x / scale), -127, 127), zeros when amax == 0. q packs this
+// lane's NV values, 4 per word; returns the scale. Every lane of the G must
+// call it together (the amax is reduced across them). The append kernel and
+// the fused int8 decode both quantise through here, so a row appended either
+// way holds the same bytes.
+template <int NV, int G>
+__device__ __forceinline__ float quantize_row(const float (&x)[NV], uint32_t (&q)[NV / 4]) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = group_max<G>(amax);
+    const float sc = amax / 127.0f;
+#pragma unroll
+    for (int w = 0; w < NV / 4; ++w) q[w] = 0u;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int qi = amax > 0.f ? (int)fminf(fmaxf(rintf(x[i] / sc), -127.f), 127.f) : 0;
+        q[i >> 2] |= ((uint32_t)(qi & 0xff)) << (8 * (i & 3));
+    }
+    return sc;
+}
+
+// quantize_row of 16 bf16 values (two 16-B words), G lanes per row.
+template <int G>
+__device__ __forceinline__ float quantize16_bf16(const uint4 (&src)[2], uint4 &q) {
+    float f[16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 x = src[h];
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[8 * h + 2 * i] = bf16_lo(w[i]);
+            f[8 * h + 2 * i + 1] = bf16_hi(w[i]);
+        }
+    }
+    uint32_t qw[4];
+    const float sc = quantize_row<16, G>(f, qw);
+    q = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+    return sc;
+}
+
+// Element offset of the new row (slot, head, pos) of a fused append: a PAGED
+// row's page comes from the launch's page-table edits where one maps it (the
+// table entry is written by the same launch), else from the table.
+template <int LAYOUT>
+__device__ __forceinline__ int64_t new_row_offset(const DecodeArgs &a, int slot, int head, int pos, int D) {
+    if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+        const int lp = pos >> a.kv.block_shift;
+        if (pos < 0 || lp >= a.kv.pt_stride) return -1;
+        const int idx = slot * a.kv.pt_stride + lp;
+        int page = -2;
+        for (int i = 0; i < a.n_upd; ++i) page = a.upd_idx[i] == idx ? a.upd_val[i] : page;
+        if (page == -2) return row_offset<LAYOUT>(a.kv, slot, head, pos, D);
+        if (page < 0 || page >= a.kv.pool_pages) return -1;
+        return (((int64_t)page * a.kv.kv_heads + head) * a.kv.rows + (pos & (a.kv.rows - 1))) * (int64_t)D;
+    } else {
+        return row_offset<LAYOUT>(a.kv, slot, head, pos, D);
+    }
+}
+
+// The launch's page-table edits (DecodeArgs::n_upd), written by its first
+// workgroup.
+__device__ __forceinline__ void apply_page_edits(const DecodeArgs &a) {
+    if (a.n_upd > 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+        for (int i = threadIdx.x; i < a.n_upd; i += blockDim.x) a.kv.page_table[a.upd_idx[i]] = a.upd_val[i];
+}
+
 // ---------------------------------------------------------------------------
 // append / import
 // ---------------------------------------------------------------------------
@@ -147,12 +217,10 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
             *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.k) + dst + seg * 8) = kx;
             *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kv.v) + dst + seg * 8) = vx;
         } else {
-            // Symmetric int8 per (token, head): scale = amax / 127,
-            // q = clamp(rne(x / scale), -127, 127); amax == 0 stores zeros.
+            // symmetric int8 per (token, head), D/8 lanes per row
             const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
             const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
             float kf[8], vf[8];
-            float ka = 0.f, va = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 kf[2 * i] = bf16_lo(kw[i]);
@@ -160,24 +228,9 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
                 vf[2 * i] = bf16_lo(vw[i]);
                 vf[2 * i + 1] = bf16_hi(vw[i]);
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                ka = fmaxf(ka, fabsf(kf[i]));
-                va = fmaxf(va, fabsf(vf[i]));
-            }
-            ka = group_max<LPR>(ka);
-            va = group_max<LPR>(va);
-            const float ksc = ka / 127.0f;
-            const float vsc = va / 127.0f;
-            uint32_t kq[2] = {0u, 0u}, vq[2] = {0u, 0u};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                int qk = 0, qv = 0;
-                if (ka > 0.f) qk = (int)fminf(fmaxf(rintf(kf[i] / ksc), -127.f), 127.f);
-                if (va > 0.f) qv = (int)fminf(fmaxf(rintf(vf[i] / vsc), -127.f), 127.f);
-                kq[i >> 2] |= ((uint32_t)(qk & 0xff)) << (8 * (i & 3));
-                vq[i >> 2] |= ((uint32_t)(qv & 0xff)) << (8 * (i & 3));
-            }
+            uint32_t kq[2], vq[2];
+            const float ksc = quantize_row<8, LPR>(kf, kq);
+            const float vsc = quantize_row<8, LPR>(vf, vq);
             *reinterpret_cast<uint2 *>(static_cast<int8_t *>(a.kv.k) + dst + seg * 8) = make_uint2(kq[0], kq[1]);
             *reinterpret_cast<uint2 *>(static_cast<int8_t *>(a.kv.v) + dst + seg * 8) = make_uint2(vq[0], vq[1]);
             if (seg == 0) {
@@ -578,13 +631,14 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
+    const int64_t new_base = (((int64_t)item * hkv + kvh) * a.qn) * D + seg * VEC;
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     int plen = 0;          // prefix-attention mask (listener slots); the talker has its own masks
     uint32_t pw = ~0u;
     if constexpr (!TALK) load_prefix(a.pmask, slot, lane, plen, pw);
     const int Qn = a.qn;
     const int rows = a.group * Qn;
-    const bool fused = (KDT == KVRT_BF16) && a.k_new != nullptr;
+    const bool fused = a.k_new != nullptr;  // bf16: rows copied; int8: quantised in-kernel
     int kend = fused ? len + Qn : len;
     if constexpr (TALK) kend = min(kend, a.talk[item].audio_pos + 1);
     if (LAYOUT == KVRT_LAYOUT_CONTIG && kend > a.kv.rows) {
@@ -601,6 +655,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int ws = kstart + split * chunk;
     const int we = min(kend, ws + chunk);
 
+    if constexpr (!TALK) apply_page_edits(a);
     if constexpr (KDT == KVRT_BF16) {
         // Fused append: workgroup 0 of every (item, kv head) stores the new
         // rows. No workgroup of this launch reads those cache rows (they are
@@ -612,7 +667,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 const int pos = len + r;
                 bool ok = true;
                 if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) ok = pos < a.kv.rows;
-                const int64_t dst = ok ? row_offset<LAYOUT>(a.kv, slot, kvh, pos, D) : -1;
+                const int64_t dst = ok ? new_row_offset<LAYOUT>(a, slot, kvh, pos, D) : -1;
                 if (dst < 0) {
                     a.err[0] = 1;
                     continue;
@@ -622,6 +677,76 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                 const uint4 vx = *reinterpret_cast<const uint4 *>(a.v_new + src);
                 store_agent16(static_cast<uint16_t *>(a.kv.k) + dst + sg * 8, kx);
                 store_agent16(static_cast<uint16_t *>(a.kv.v) + dst + sg * 8, vx);
+            }
+        }
+    }
+
+    // Fused int8 append. Workgroup 0 of every (item, kv head) quantises the
+    // new rows (exactly as the append kernel does: LPR lanes of 16 values per
+    // row) and stores them with their scales; no workgroup of the launch reads
+    // those cache rows. A wave whose key range reaches them quantises them
+    // again into LDS before its main loop, where registers are free, for the
+    // pass that reaches them. Two waves of a workgroup may both fill the LDS
+    // copy: they write the same bytes, and each reads its own writes. (The
+    // rows are loaded here rather than next to the length load: holding them
+    // from there raised the kernel to 132 VGPRs, 3 waves per SIMD, and config
+    // 5 from 0.83 to 0.94 ms per step; one loop for both copies took 130.)
+    constexpr int NQ = KDT == KVRT_INT8 ? kMaxInt8Rows : 1;
+    __shared__ uint4 nrow_k[NQ * LPR], nrow_v[NQ * LPR];
+    __shared__ float nrow_s[2 * NQ];
+    if constexpr (KDT == KVRT_INT8) {
+        if (fused && blockIdx.x == 0) {
+            for (int c0 = 0; c0 < Qn * LPR; c0 += blockDim.x) {
+                const int c = c0 + threadIdx.x;
+                const bool live = c < Qn * LPR;
+                const int r = live ? c / LPR : 0, sg = c % LPR;
+                const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 16;
+                uint4 kx2[2], vx2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + src + 8 * h);
+                    vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + src + 8 * h);
+                }
+                uint4 kq, vq;
+                const float ksc = quantize16_bf16<LPR>(kx2, kq);
+                const float vsc = quantize16_bf16<LPR>(vx2, vq);
+                if (live) {
+                    const int64_t dst = new_row_offset<LAYOUT>(a, slot, kvh, len + r, D);
+                    if (dst < 0) {
+                        a.err[0] = 1;
+                    } else {
+                        *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.k) + dst + sg * 16) = kq;
+                        *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.v) + dst + sg * 16) = vq;
+                        if (sg == 0) {
+                            a.kv.ks[dst / D] = ksc;
+                            a.kv.vs[dst / D] = vsc;
+                        }
+                    }
+                }
+            }
+        }
+        if (fused && we > len) {
+            for (int r0 = 0; r0 < Qn; r0 += KPW) {
+                const int r = r0 + sub;
+                const bool live = r < Qn;
+                const int64_t on = new_base + (int64_t)(live ? r : 0) * D;
+                uint4 kx2[2], vx2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + on + 8 * h);
+                    vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + on + 8 * h);
+                }
+                uint4 kq, vq;
+                const float ks = quantize16_bf16<LPR>(kx2, kq);
+                const float vs = quantize16_bf16<LPR>(vx2, vq);
+                if (live) {
+                    nrow_k[r * LPR + seg] = kq;
+                    nrow_v[r * LPR + seg] = vq;
+                    if (seg == 0) {
+                        nrow_s[r] = ks;
+                        nrow_s[NQ + r] = vs;
+                    }
+                }
             }
         }
     }
@@ -691,7 +816,6 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         for (int e = 0; e < VEC; ++e) acc[r][e] = 0.f;
     }
 
-    const int64_t new_base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * VEC;
     bool bad = false;  // a visible key on an unmapped page (PAGED)
     const int npass = we > ws ? (we - ws + KPW * U - 1) / (KPW * U) : 0;
     // PAGED: the page-table entries of the wave's first 64 pages, one per
@@ -788,8 +912,11 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
             else o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
             bool ok = kk < we;
             if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
-                bad |= ok && o < 0;
-                ok = ok && o >= 0;
+                // a fused append's new rows come from k_new / v_new; their
+                // page may be mapped by this very launch
+                const bool nw = fused && kc >= len;
+                bad |= ok && !nw && o < 0;
+                ok = ok && (nw || o >= 0);
                 o = o < 0 ? 0 : o;
             }
             key[u] = ok ? kk : 0x7fffffff;
@@ -816,6 +943,25 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         // would otherwise sink the last ones under register pressure and
         // expose a second memory round trip per pass)
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (KDT == KVRT_INT8) {
+            // Fused int8 append: the pass that reaches the new rows (one per
+            // (item, kv head); wave-uniform) takes them, quantised, from LDS,
+            // so the launch attends over the rows an append followed by a
+            // decode would read.
+            if (fused && base + KPW * U > len) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int kk = base + u * KPW + sub;
+                    if (kk < we && kk >= len) {
+                        const int r = kk - len;
+                        kx[u] = nrow_k[r * LPR + seg];
+                        vx[u] = nrow_v[r * LPR + seg];
+                        ksc[u] = nrow_s[r];
+                        vsc[u] = nrow_s[NQ + r];
+                    }
+                }
+            }
+        }
         }
         if (base < plen) {
             // keys of this pass below the end of the prefix mask: a masked
@@ -1131,13 +1277,14 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
 
     // Fused append: workgroup 0 of every (item, kv head) stores the new rows;
     // no workgroup of this launch reads them from the cache.
+    apply_page_edits(a);
     if (!I8 && fused && blockIdx.x == 0) {
         for (int c = threadIdx.x; c < Qn * (D / 8); c += blockDim.x) {
             const int r = c / (D / 8), sg = c % (D / 8);
             const int pos = len + r;
             bool ok = true;
             if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) ok = pos < a.kv.rows;
-            const int64_t dst = ok ? row_offset<LAYOUT>(a.kv, slot, kvh, pos, D) : -1;
+            const int64_t dst = ok ? new_row_offset<LAYOUT>(a, slot, kvh, pos, D) : -1;
             if (dst < 0) {
                 a.err[0] = 1;
                 continue;
@@ -1199,7 +1346,9 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         if constexpr (PWIN) off = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
         else off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
         if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
-            bad |= kk < we && off < 0;
+            // a fused append's new rows come from k_new / v_new (their page
+            // may be mapped by this very launch)
+            bad |= kk < we && !(fused && kc >= len) && off < 0;
             off = off < 0 ? 0 : off;
         }
         return off;

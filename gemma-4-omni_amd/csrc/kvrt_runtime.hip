@@ -709,7 +709,10 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         if (rc != KVRT_OK) return rc;
     }
     if (fused) {
-        if (s.dtype != KVRT_BF16) return KVRT_EINVAL;
+        // int8 rows are quantised in-kernel by the VALU decode only (the
+        // caller routes a forced MFMA decode through the append kernel)
+        if (s.dtype == KVRT_INT8 && (s.layout != KVRT_LAYOUT_PAGED || c->cfg.decode_kernel == KVRT_DECODE_MFMA))
+            return KVRT_EINVAL;
         if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4) || !is_contiguous(k) || !is_contiguous(v))
             return KVRT_EINVAL;
         if (k->dims[0] != n || k->dims[1] != hkv || k->dims[2] != qn || k->dims[3] != D) return KVRT_EINVAL;
@@ -751,9 +754,19 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         rc = map_items(c, n, slots, from, (int)qn, pidx, pval);
         if (rc != KVRT_OK) return rc;
     }
-    rc = enqueue_pages(c, pidx, pval);
-    if (rc != KVRT_OK) return rc;
     DecodeArgs a{};
+    if (pidx.size() <= (size_t)kMaxItems) {
+        // the new rows' pages travel in the launch (its first workgroup
+        // writes them into the table): no page-table launch ahead of it
+        a.n_upd = (int)pidx.size();
+        for (size_t i = 0; i < pidx.size(); ++i) {
+            a.upd_idx[i] = pidx[i];
+            a.upd_val[i] = pval[i];
+        }
+    } else {
+        rc = enqueue_pages(c, pidx, pval);
+        if (rc != KVRT_OK) return rc;
+    }
     a.kv = make_view(c, layer);
     a.len = make_len(c, layer);
     a.q = static_cast<const uint16_t *>(q->data);
@@ -1607,6 +1620,21 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
     return set_device_lens(c, idx, &before);
 }
 
+int kvrt_reserve_async(kvrt_ctx *c, int32_t slot, int32_t positions) {
+    int rc = begin(c);
+    if (rc) return rc;
+    if (!c->paged || !valid_slot(c, slot) || positions < 0) return KVRT_EINVAL;
+    if (c->lens_stale) return KVRT_ESTATE;  // the host must vouch for the length it maps from
+    int L = 0;  // pages are per slot: from the longest PAGED layer on
+    for (int l = 0; l < c->cfg.n_layers; ++l)
+        if (c->layers[l].owner == l && c->layers[l].spec.layout == KVRT_LAYOUT_PAGED) L = std::max(L, c->len_at(slot, l));
+    if ((int64_t)L + positions > c->cfg.capacity) return KVRT_ESTATE;
+    std::vector<int32_t> idx, val;
+    rc = map_pages(c, slot, L, L + positions, idx, val);
+    if (rc != KVRT_OK) return rc;
+    return enqueue_pages(c, idx, val);
+}
+
 int kvrt_evict(kvrt_ctx *c, int32_t slot, int32_t keep_from) {
     int rc = begin(c);
     if (rc) return rc;
@@ -1875,12 +1903,14 @@ int kvrt_append_attend_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_
     if (rc) return rc;
     if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !k || !v) return KVRT_EINVAL;
     if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // shared layers append nothing
-    if (c->layers[layer].spec.dtype == KVRT_INT8) {
-        // int8 rows are quantised by the append kernel, then read back.
+    if (c->layers[layer].spec.dtype == KVRT_INT8 && c->cfg.decode_kernel == KVRT_DECODE_MFMA) {
+        // the MFMA decode reads int8 rows only: the append kernel quantises
+        // them first
         rc = append_impl(c, layer, n, slots, k, v);
         if (rc) return rc;
         return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
     }
+    // one launch: the decode stores the new rows (int8: quantised in-kernel)
     return decode_impl(c, layer, n, slots, q, k, v, out, scale);
 }
 

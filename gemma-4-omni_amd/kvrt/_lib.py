@@ -167,6 +167,7 @@ SIGNATURES = [
     ("kvrt_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _I32P, _T, _T, _T]),
     ("kvrt_append_gather_async", c_int32, [c_void_p, c_int32, c_int32, _I32P, _T, _T, _I32P, _T, _T, _T]),
     ("kvrt_truncate", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64, c_int32]),
+    ("kvrt_reserve_async", c_int32, [c_void_p, c_int32, c_int32]),
     ("kvrt_evict", c_int32, [c_void_p, c_int32, c_int32]),
     ("kvrt_copy_prefix_async", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_uint64]),
     ("kvrt_copy_session_async", c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_uint64]),

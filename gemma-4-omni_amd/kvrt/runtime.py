@@ -622,6 +622,12 @@ class KVRuntime:
         _check(self.lib.kvrt_truncate(self._ctx, slot, layer, int(new_len), int(generation), int(expected_len)),
                "kvrt_truncate")
 
+    def reserve(self, slot: int, positions: int) -> None:
+        """PAGED: map the pages of the slot's next ``positions`` positions now, so
+        that a captured graph of fused appends replays across page boundaries."""
+        self._bind()
+        _check(self.lib.kvrt_reserve_async(self._ctx, int(slot), int(positions)), "kvrt_reserve_async")
+
     def evict(self, slot: int, keep_from: int) -> None:
         self._own()
         _check(self.lib.kvrt_evict(self._ctx, slot, int(keep_from)), "kvrt_evict")

@@ -393,6 +393,17 @@ int kvrt_append_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
 int kvrt_truncate(kvrt_ctx *ctx, int32_t slot, int32_t layer, int32_t new_len, uint64_t expected_generation,
                   int32_t expected_len);
 
+/* PAGED: map the pages of the next `positions` positions of slot (after its
+ * longest PAGED layer's length) now, so that appends up to there take no
+ * page-table edit: a captured HIP graph of fused appends then replays across
+ * page boundaries (a replay that outruns the reservation raises the device
+ * flag: kvrt_health reports KVRT_EFAULT). KVRT_ENOMEM when the pool runs out
+ * (nothing mapped), KVRT_ESTATE past capacity or while the host lengths are
+ * unverified (captured work not yet read back). A truncate releases pages
+ * wholly beyond the remaining rows, reserved ones included. No counterpart in
+ * the reference (paged KV is absent there). */
+int kvrt_reserve_async(kvrt_ctx *ctx, int32_t slot, int32_t positions);
+
 /* PAGED: release every page of slot wholly below position keep_from (all
  * layers share one page table per slot). Positions below keep_from must not
  * be attended afterwards (the layer window guarantees it). No counterpart in

@@ -378,12 +378,15 @@ def run_prefill(args) -> int:
     return 0
 
 
-def _event_median(fn, warmup: int, reps: int) -> float:
+def _event_median(fn, warmup: int, reps: int, setup=None) -> float:
     """Median seconds of fn's GPU work: HIP events around each call on the
     current stream, after a GPU sleep so the host enqueues the whole call
-    before the GPU reaches it."""
+    before the GPU reaches it. ``setup`` runs before each call, outside the
+    events."""
     times = []
     for _ in range(warmup + reps):
+        if setup is not None:
+            setup()
         torch.cuda._sleep(1_000_000)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -418,12 +421,10 @@ def run_kernels(args) -> int:
     # import (append_kernel, host position): one talker layer, 4 streams x [8, 8192, 128]
     rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)], 4, 8192 + 64, max_q=1, device="cuda")
     kv = [bf((1, 8, 8192, 128)) for _ in range(2)]
-    def reimport():
-        rt.truncate(0, 0)  # an import lands only on an empty layer: one set_i32_kernel launch first
-        rt.import_(0, 0, kv[0], kv[1])
-
-    add("import_talker_8192", "append_kernel<128,bf16,contig> (import, after set_i32_kernel emptying the layer)",
-        _event_median(reimport, w, r), 4 * 8 * 8192 * 128 * 2, "[1,8,8192,128] x K,V")
+    # an import lands only on an empty layer: the layer is emptied before each timed import
+    add("import_talker_8192", "append_kernel<128,bf16,contig> (import)",
+        _event_median(lambda: rt.import_(0, 0, kv[0], kv[1]), w, r, setup=lambda: rt.truncate(0, 0)),
+        4 * 8 * 8192 * 128 * 2, "[1,8,8192,128] x K,V")
     # per-frame append (device cursor): 4 streams x 1 row x 8 heads
     rt.truncate(0, 0)
     for s in range(4):
@@ -602,8 +603,9 @@ def run_configs(args) -> int:
     attention per layer; config 3 appends, gathers the padded batch and
     attends over it; config 4 rolls back every 25 steps; config 5 evicts),
     issued eagerly from Python through the C ABI and timed with the host
-    clock around all of a config's steps; configs 1, 2 and 4 also replay one
-    captured step as a HIP graph (config 4 rolls back between replays).
+    clock around all of a config's steps; every config also replays one
+    captured step as a HIP graph (config 4 rolls back between replays;
+    config 5 reserves the pages its replays will append into).
     Inputs are seeded N(0, 1) draws made on the device before the timed
     region and cycled through; the CPU side uses draws of the same law.
     Algorithmic bytes per step: visible K/V rows read once, appended rows

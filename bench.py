@@ -499,9 +499,10 @@ def run_kernels(args) -> int:
         c1 = rt.counters()
         if c1["launches"] - c0["launches"] > (2 if fused == "two" else 1) * (w + r):  # a separate merge
             kernel += " + merge_kernel"
-        if kernel.startswith("decode_kernel") and c1["mfma_decodes"] - c0["mfma_decodes"] == w + r:
+        on_mfma = "mfma_kernel" in kernel
+        if not on_mfma and c1["mfma_decodes"] - c0["mfma_decodes"] == w + r:
             raise RuntimeError(f"kernel case {name}: expected the VALU decode, AUTO chose the MFMA kernel")
-        if kernel.startswith("decode_mfma") and c1["mfma_decodes"] - c0["mfma_decodes"] != w + r:
+        if on_mfma and c1["mfma_decodes"] - c0["mfma_decodes"] != w + r:
             raise RuntimeError(f"kernel case {name}: expected the MFMA decode, AUTO chose the VALU kernel")
         if rt.health() != 0:
             raise RuntimeError(f"kvrt health check failed in kernel case {name}")
@@ -525,7 +526,8 @@ def run_kernels(args) -> int:
     decode_case("decode_listener_q2_d512", "decode_mfma_kernel<512,16,contig>", 8, 1, 512, 4, 8192, qn=2)
     g4 = torch.Generator().manual_seed(4)
     lens5 = [int(x) for x in torch.randint(256, 8193, (16,), generator=g4)]
-    decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> (attend only)", 16, 8, 128, 16, 0,
+    decode_case("decode_int8_paged", "decode_kernel<128,2,int8,paged> (attend only)",
+                16, 8, 128, 16, 0,
                 window=4096, layout="paged", fused=False, dtype="int8", lens=lens5, block_size=16,
                 pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
     # config 5's per-layer call: the append quantised inside the decode launch, and the
@@ -536,6 +538,11 @@ def run_kernels(args) -> int:
     decode_case("decode_int8_paged_two_launch", "append_kernel<128,int8,paged> + decode_kernel<128,2,int8,paged>",
                 16, 8, 128, 16, 0, window=4096, layout="paged", fused="two", dtype="int8", lens=lens5,
                 block_size=16, pool_pages=16 * (8192 // 16 + 8), pool_seed=4)
+    # the same call on the int8 MFMA ring kernel (kvrt_config.decode_kernel = MFMA)
+    decode_case("decode_int8_paged_fused_mfma", "decode_i8_mfma_kernel<128> (2 rows in an 8-row tile, LDS DMA ring, "
+                "quantise-on-append in the launch)", 16, 8, 128, 16, 0, window=4096, layout="paged", fused=True,
+                dtype="int8", lens=lens5, block_size=16, pool_pages=16 * (8192 // 16 + 8), pool_seed=4,
+                decode_kernel="mfma")
 
     # slot lifecycle: clone a 4096-position talker session (28 layers, one launch)
     rt = KVRuntime([LayerSpec(kv_heads=8, head_dim=128)] * 28, 2, 4096 + 64, max_q=1, device="cuda")

@@ -61,6 +61,9 @@ constexpr int dma_wave_bytes(int R, int head_dim) {
 // the merge's (m, l) table (an M0-addressed LDS DMA reaches the whole range:
 // probed at byte 96 KiB of a 128 KiB allocation); a wave's fp32 partial
 // (R x D) must fit its own ring.
+// (int8 PAGED decodes measured no faster through such a ring — 28.2 vs
+// 28.0 us at config 5's layer, a 256-byte block of scales per stage, 4
+// workgroups per CU — and load their passes into registers.)
 constexpr bool decode_dma(int R, int dtype, int layout, int head_dim) {
     return KVRT_DECODE_DMA && dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && R <= KVRT_DMA_MAX_ROWS &&
            kWaves * dma_wave_bytes(R, head_dim) <= 160 * 1024 - 1024 &&
@@ -246,6 +249,19 @@ constexpr int kMfmaDecodeKeys = 16;  // keys per MFMA decode tile
 #ifndef KVRT_MFMA_DMA_D256
 #define KVRT_MFMA_DMA_D256 1
 #endif
+// int8 PAGED decodes of up to 8 rows per kv head at head_dim 64 / 128 run on
+// decode_i8_mfma_kernel: 32-key tiles of int8 K, V and scales DMAd into a ring
+// of KVRT_I8_MFMA_STAGES stages per wave (8.25 KiB per stage at D 128).
+#ifndef KVRT_I8_MFMA
+#define KVRT_I8_MFMA 1
+#endif
+#ifndef KVRT_I8_MFMA_STAGES
+#define KVRT_I8_MFMA_STAGES 2
+#endif
+constexpr int kI8MfmaKeys = 32;  // keys per int8 MFMA decode tile
+constexpr bool i8_mfma_dma(int head_dim, int rows_tile) {
+    return KVRT_I8_MFMA && (head_dim == 64 || head_dim == 128) && rows_tile >= 1 && rows_tile <= 8;
+}
 constexpr bool mfma_decode_dma(int head_dim, int rows_tile, int dtype, int layout) {
     return dtype == KVRT_BF16 && layout != KVRT_LAYOUT_PAGED && rows_tile <= 8 &&
            ((head_dim == 128 && KVRT_MFMA_DMA_D128) || (head_dim == 256 && KVRT_MFMA_DMA_D256));

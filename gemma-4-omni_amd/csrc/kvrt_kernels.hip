@@ -28,6 +28,15 @@ constexpr float kNegBig = -1.0e30f;  // running-max start; exp2(kNegBig - m) == 
 // merge weights a partial by its own m.
 constexpr float kRescaleSlack = 8.0f;
 
+// Row number of position pos of a head on a PAGED page, in pool order
+// ((page, head, pos % rows)); -1 if the page is unmapped or out of the pool.
+// 32-bit arithmetic: the host keeps pool_pages below 2^24 and the pool's rows
+// below 2^31, so page * (kv_heads * rows) is a 24-bit product.
+__device__ __forceinline__ int page_row(const KVView &v, int page, int head, int pos) {
+    if (page < 0 || page >= v.pool_pages) return -1;
+    return (int)__umul24((unsigned)page, (unsigned)(v.kv_heads * v.rows)) + head * v.rows + (pos & (v.rows - 1));
+}
+
 // Element offset of the first element of row (slot, head, pos); -1 if the
 // page is unmapped or out of the pool.
 template <int LAYOUT>
@@ -40,8 +49,8 @@ __device__ __forceinline__ int64_t row_offset(const KVView &v, int slot, int hea
         const int lp = pos >> v.block_shift;
         if (pos < 0 || lp >= v.pt_stride) return -1;
         const int page = v.page_table[(int64_t)slot * v.pt_stride + lp];
-        if (page < 0 || page >= v.pool_pages) return -1;
-        return (((int64_t)page * v.kv_heads + head) * v.rows + (pos & (v.rows - 1))) * (int64_t)D;
+        const int row = page_row(v, page, head, pos);
+        return row < 0 ? -1 : (int64_t)row * D;
     }
 }
 
@@ -83,6 +92,19 @@ __device__ __forceinline__ uint32_t prefix_bits8(uint32_t pw, int k0, int plen) 
 }
 
 
+// A wave's window of page-table entries: lane i holds the entry of logical
+// page win0 + i of the slot (-1 past the table).
+__device__ __forceinline__ int load_page_window(const KVView &v, int slot, int win0, int lane) {
+    const int lp = win0 + lane;
+    return lp < v.pt_stride ? v.page_table[(int64_t)slot * v.pt_stride + lp] : -1;
+}
+// Element offset of row pos of a head on a page; -1 if the page is unmapped
+// or out of the pool.
+__device__ __forceinline__ int64_t page_row_offset(const KVView &v, int page, int head, int pos, int D) {
+    const int row = page_row(v, page, head, pos);
+    return row < 0 ? -1 : (int64_t)row * D;
+}
+
 // PAGED row offset with the page taken from a wave's window of page-table
 // entries (lane i holds the entry of logical page win0 + i; pages past the
 // window are looked up directly). Every lane of the wave must call it.
@@ -95,8 +117,7 @@ __device__ __forceinline__ int64_t paged_offset(const KVView &v, int slot, int h
         if (pos < 0 || lp >= v.pt_stride) return -1;
         page = v.page_table[(int64_t)slot * v.pt_stride + lp];
     }
-    if (page < 0 || page >= v.pool_pages) return -1;
-    return (((int64_t)page * v.kv_heads + head) * v.rows + (pos & (v.rows - 1))) * (int64_t)D;
+    return page_row_offset(v, page, head, pos, D);
 }
 
 // Symmetric int8 quantisation of one (token, head) row whose D values are
@@ -155,10 +176,80 @@ __device__ __forceinline__ int64_t new_row_offset(const DecodeArgs &a, int slot,
         int page = -2;
         for (int i = 0; i < a.n_upd; ++i) page = a.upd_idx[i] == idx ? a.upd_val[i] : page;
         if (page == -2) return row_offset<LAYOUT>(a.kv, slot, head, pos, D);
-        if (page < 0 || page >= a.kv.pool_pages) return -1;
-        return (((int64_t)page * a.kv.kv_heads + head) * a.kv.rows + (pos & (a.kv.rows - 1))) * (int64_t)D;
+        return page_row_offset(a.kv, page, head, pos, D);
     } else {
         return row_offset<LAYOUT>(a.kv, slot, head, pos, D);
+    }
+}
+
+// Fused int8 append, store side: the launch's Qn new rows of (item, kv head)
+// quantised exactly as the append kernel does (D/16 lanes of 16 values per
+// row, quantize16_bf16) and stored with their scales, by the calling
+// workgroup's threads together.
+template <int D, int LAYOUT>
+__device__ __forceinline__ void i8_store_new_rows(const DecodeArgs &a, int item, int slot, int kvh, int hkv, int len,
+                                                  int Qn) {
+    constexpr int LPR = D / 16;
+    for (int c0 = 0; c0 < Qn * LPR; c0 += blockDim.x) {
+        const int c = c0 + threadIdx.x;
+        const bool live = c < Qn * LPR;
+        const int r = live ? c / LPR : 0, sg = c % LPR;
+        const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 16;
+        uint4 kx2[2], vx2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + src + 8 * h);
+            vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + src + 8 * h);
+        }
+        uint4 kq, vq;
+        const float ksc = quantize16_bf16<LPR>(kx2, kq);
+        const float vsc = quantize16_bf16<LPR>(vx2, vq);
+        if (live) {
+            const int64_t dst = new_row_offset<LAYOUT>(a, slot, kvh, len + r, D);
+            if (dst < 0) {
+                a.err[0] = 1;
+            } else {
+                *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.k) + dst + sg * 16) = kq;
+                *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.v) + dst + sg * 16) = vq;
+                if (sg == 0) {
+                    a.kv.ks[dst / D] = ksc;
+                    a.kv.vs[dst / D] = vsc;
+                }
+            }
+        }
+    }
+}
+// Fused int8 append, read side: the same rows quantised again into LDS by the
+// calling wave (row r: 16-byte units nrow_k / nrow_v[r * D/16 + unit], scales
+// nrow_s[r] (K) and nrow_s[NQ + r] (V)), for the decode's tile or pass that
+// attends over them.
+template <int D, int NQ>
+__device__ __forceinline__ void i8_new_rows_lds(const DecodeArgs &a, int item, int kvh, int hkv, int Qn, int lane,
+                                                uint4 *nrow_k, uint4 *nrow_v, float *nrow_s) {
+    constexpr int LPR = D / 16, RPW = 64 / LPR;
+    const int sub = lane / LPR, seg = lane % LPR;
+    const int64_t base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * 16;
+    for (int r0 = 0; r0 < Qn; r0 += RPW) {
+        const int r = r0 + sub;
+        const bool live = r < Qn;
+        const int64_t on = base + (int64_t)(live ? r : 0) * D;
+        uint4 kx2[2], vx2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + on + 8 * h);
+            vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + on + 8 * h);
+        }
+        uint4 kq, vq;
+        const float ks = quantize16_bf16<LPR>(kx2, kq);
+        const float vs = quantize16_bf16<LPR>(vx2, vq);
+        if (live) {
+            nrow_k[r * LPR + seg] = kq;
+            nrow_v[r * LPR + seg] = vq;
+            if (seg == 0) {
+                nrow_s[r] = ks;
+                nrow_s[NQ + r] = vs;
+            }
+        }
     }
 }
 
@@ -403,6 +494,10 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 __device__ __forceinline__ void dma_load16(const void *g, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
 }
+// 4 bytes per lane, to LDS byte M0 + 4 * l.
+__device__ __forceinline__ void dma_load4(const void *g, uint32_t lds) {
+    asm volatile("global_load_lds_dword %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
+}
 // The same without the streaming hint, for tiles other workgroups read again.
 __device__ __forceinline__ void dma_load16_cached(const void *g, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
@@ -618,7 +713,8 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     static_assert(!DMA || R * D * 4 <= WAVE_BYTES, "DMA ring holds the wave's partial");
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (an SGPR): the split, key range and pass count follow
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int sub = lane / LPR;
     const int seg = lane % LPR;
     // workgroups start in linear id order, z slowest: PAGED items (pools of
@@ -632,7 +728,8 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
     const int64_t new_base = (((int64_t)item * hkv + kvh) * a.qn) * D + seg * VEC;
-    const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
+    // wave-uniform (an SGPR): the key range, pass count and their tests follow
+    const int len = __builtin_amdgcn_readfirstlane(a.len.lens[(int64_t)slot * a.len.stride + a.len.offset]);
     int plen = 0;          // prefix-attention mask (listener slots); the talker has its own masks
     uint32_t pw = ~0u;
     if constexpr (!TALK) load_prefix(a.pmask, slot, lane, plen, pw);
@@ -695,60 +792,8 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     __shared__ uint4 nrow_k[NQ * LPR], nrow_v[NQ * LPR];
     __shared__ float nrow_s[2 * NQ];
     if constexpr (KDT == KVRT_INT8) {
-        if (fused && blockIdx.x == 0) {
-            for (int c0 = 0; c0 < Qn * LPR; c0 += blockDim.x) {
-                const int c = c0 + threadIdx.x;
-                const bool live = c < Qn * LPR;
-                const int r = live ? c / LPR : 0, sg = c % LPR;
-                const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 16;
-                uint4 kx2[2], vx2[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + src + 8 * h);
-                    vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + src + 8 * h);
-                }
-                uint4 kq, vq;
-                const float ksc = quantize16_bf16<LPR>(kx2, kq);
-                const float vsc = quantize16_bf16<LPR>(vx2, vq);
-                if (live) {
-                    const int64_t dst = new_row_offset<LAYOUT>(a, slot, kvh, len + r, D);
-                    if (dst < 0) {
-                        a.err[0] = 1;
-                    } else {
-                        *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.k) + dst + sg * 16) = kq;
-                        *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.v) + dst + sg * 16) = vq;
-                        if (sg == 0) {
-                            a.kv.ks[dst / D] = ksc;
-                            a.kv.vs[dst / D] = vsc;
-                        }
-                    }
-                }
-            }
-        }
-        if (fused && we > len) {
-            for (int r0 = 0; r0 < Qn; r0 += KPW) {
-                const int r = r0 + sub;
-                const bool live = r < Qn;
-                const int64_t on = new_base + (int64_t)(live ? r : 0) * D;
-                uint4 kx2[2], vx2[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + on + 8 * h);
-                    vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + on + 8 * h);
-                }
-                uint4 kq, vq;
-                const float ks = quantize16_bf16<LPR>(kx2, kq);
-                const float vs = quantize16_bf16<LPR>(vx2, vq);
-                if (live) {
-                    nrow_k[r * LPR + seg] = kq;
-                    nrow_v[r * LPR + seg] = vq;
-                    if (seg == 0) {
-                        nrow_s[r] = ks;
-                        nrow_s[NQ + r] = vs;
-                    }
-                }
-            }
-        }
+        if (fused && blockIdx.x == 0) i8_store_new_rows<D, LAYOUT>(a, item, slot, kvh, hkv, len, Qn);
+        if (fused && we > len) i8_new_rows_lds<D, NQ>(a, item, kvh, hkv, Qn, lane, nrow_k, nrow_v, nrow_s);
     }
 
     // q rows of this kv head, packed bf16 pairs. Row r = j*Q + i of the tile
@@ -824,9 +869,31 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     int pwin = -1, pwin0 = 0;
     if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
         pwin0 = ws >> a.kv.block_shift;
-        const int lp = pwin0 + lane;
-        if (lp < a.kv.pt_stride) pwin = a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp];
+        pwin = load_page_window(a.kv, slot, pwin0, lane);
     }
+    // PAGED: row offset of key kc >= base of the pass at base (-1: unmapped
+    // page). The pass's keys, [base, min(we, base + KPW * U)), are looked up
+    // in the wave's window of 64 page-table entries, which moves (a
+    // wave-uniform branch) when a pass leaves it; a pass over more than 64
+    // pages (tiny pages) looks them up directly. Every lane calls it together.
+    // The lookups of a pass come before its K/V loads: a page-table load
+    // between them would hold every later load of the pass until all earlier
+    // ones had landed (a load's result is awaited by count, and loads
+    // complete in order).
+    auto pass_window = [&](int base) __attribute__((always_inline)) {
+        const int lp_end = (min(we, base + KPW * U) - 1) >> a.kv.block_shift;
+        if (lp_end - pwin0 >= 64) {
+            pwin0 = base >> a.kv.block_shift;
+            pwin = load_page_window(a.kv, slot, pwin0, lane);
+        }
+        return lp_end - pwin0 < 64;  // wave-uniform
+    };
+    auto page_off = [&](int kc, bool inwin) __attribute__((always_inline)) {
+        const int lp = kc >> a.kv.block_shift;
+        int page = __shfl(pwin, (lp - pwin0) & 63);
+        if (!inwin) page = lp < a.kv.pt_stride ? a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp] : -1;
+        return page_row_offset(a.kv, page, kvh, kc, D);
+    };
     __shared__ __align__(16) u32x4_t dma_lds[DMA ? kWaves * WAVE_BYTES / 16 : 1];
     // this wave's LDS: q rows (QI KiB), then STG stages of U x (K, V) KiB
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -880,6 +947,16 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         uint4 kx[U], vx[U];
         float ksc[U], vsc[U];
         int key[U];
+        int64_t po[U];  // PAGED: row offsets of the pass's keys (-1: unmapped page)
+        if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
+            const bool inwin = pass_window(base);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int kk = base + u * KPW + sub;
+                po[u] = page_off(kk < we ? kk : base, inwin);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
         if constexpr (DMA) {
             // stage p: wait for it (the later passes stay in flight), read it,
             // then refill the stage with pass p + STG before computing
@@ -906,9 +983,9 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kk = base + u * KPW + sub;
-            const int kc = kk < we ? kk : ws;  // clamped: always a readable row
+            const int kc = kk < we ? kk : base;  // clamped: always a readable row
             int64_t o;
-            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) o = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
+            if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) o = po[u];
             else o = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
             bool ok = kk < we;
             if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
@@ -943,6 +1020,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         // would otherwise sink the last ones under register pressure and
         // expose a second memory round trip per pass)
         __builtin_amdgcn_sched_barrier(0);
+        }
         if constexpr (KDT == KVRT_INT8) {
             // Fused int8 append: the pass that reaches the new rows (one per
             // (item, kv head); wave-uniform) takes them, quantised, from LDS,
@@ -961,7 +1039,6 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
                     }
                 }
             }
-        }
         }
         if (base < plen) {
             // keys of this pass below the end of the prefix mask: a masked
@@ -1214,6 +1291,64 @@ __device__ __forceinline__ uint2 i8x4_to_bf16(uint32_t w) {
 // chunks x 2 halves per 16 lanes, 32 lanes per pass) then hit distinct
 // banks (rows are 256 or 512 B: every row starts on bank 0).
 __device__ __forceinline__ int mfma_dswz(int r) { return (2 * (r & 7)) ^ ((r >> 3) & 1); }
+
+// The end of an MFMA decode workgroup. o holds its wave's O^T tile (o[b]:
+// dims 16b + 4grp + v of row col), m the row's running max, l this lane's
+// share of the row's sum. Every wave puts its partial in LDS (lds_raw, at
+// least kWaves * R * (D + 4) floats, free of other use from here on); wave w
+// then merges rows w, w + kWaves, ... and writes the workgroup's partial of
+// those rows (one partial per workgroup, as decode_kernel), and with a merge
+// counter the last workgroup of the (item, kv head) merges the partials.
+template <int D, int R>
+__device__ __forceinline__ void mfma_decode_finish(const DecodeArgs &a, uint8_t *lds_raw, float2 *lds_ml,
+                                                   const f32x4_t (&o)[D / 16], float m, float l, int wave, int lane,
+                                                   bool rvalid, int item, int kvh, int hkv, int rows) {
+    // partial rows in LDS are PP floats apart: 16 B of padding per row, so the
+    // 16 rows (query columns) of a half-wave's float4 writes start on distinct
+    // banks (with a pitch of D floats they all hit the same ones)
+    constexpr int PP = D + 4;
+    const int col = lane & 15, grp = lane >> 4;
+    l = pair<OpSum, 32>(pair<OpSum, 16>(l));
+    __syncthreads();  // every wave is done with its tiles
+    float *lds_part = reinterpret_cast<float *>(lds_raw);
+    if (rvalid) {  // columns >= rows (>= R when R = 8) hold no row of this wave
+        float *dst = lds_part + (wave * R + col) * PP + 4 * grp;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b)
+            *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+        if (grp == 0) lds_ml[wave * R + col] = make_float2(m, l);
+    }
+    __syncthreads();
+    constexpr int EPL = D / 64;  // dims per lane
+    const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + blockIdx.x) * R;
+    for (int r = wave; r < R && r < rows; r += kWaves) {
+        float M = kNegBig;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
+        float L = 0.f, acc[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+            const float2 ml = lds_ml[w2 * R + r];
+            const float ww = __builtin_amdgcn_exp2f(ml.x - M);
+            L = fmaf(ml.y, ww, L);
+            const float *src = lds_part + (w2 * R + r) * PP + lane * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[e] = fmaf(src[e], ww, acc[e]);
+        }
+        float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
+        if (a.cnt) {
+            store_agent_n<EPL>(dst, acc);
+            if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[e] = acc[e];
+            if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+        }
+    }
+    if (a.cnt) decode_merge_tail<D, R>(a, item, kvh, hkv, rows);
+}
 
 template <int D, int R, int LAYOUT, int KDT = KVRT_BF16>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
@@ -1610,49 +1745,296 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         wait_vmem<0>();  // every DMA of the wave has landed before the LDS is reused
     }
     if (bad) a.err[0] = 1;
-    l = pair<OpSum, 32>(pair<OpSum, 16>(l));
-    // Workgroup merge: every wave puts its partial in LDS (over the tiles);
-    // wave w then merges rows w, w + kWaves, ... and writes the workgroup's
-    // partial of those rows (one partial per workgroup, as decode_kernel).
-    __syncthreads();  // every wave is done with its V tile
-    float *lds_part = reinterpret_cast<float *>(lds_raw);
-    if (rvalid) {  // columns >= rows (>= R when R = 8) hold no row of this wave
-        float *dst = lds_part + (wave * R + col) * PP + 4 * grp;
+    mfma_decode_finish<D, R>(a, lds_raw, lds_ml, o, m, l, wave, lane, rvalid, item, kvh, hkv, rows);
+}
+
+// gfx950 LDS transpose read of bytes: in each group of 16 lanes, lane s gives
+// the address of 8 consecutive bytes; lane t = 8a + e receives byte e of the
+// chunks of lanes a, a + 2, ..., a + 14 (probed on the device).
+__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t *p) {
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    const v2i_t x = __builtin_amdgcn_ds_read_tr8_b64_v2i32((v2i_t __attribute__((address_space(3))) *)(p));
+    return __builtin_bit_cast(uint2, x);
+}
+// Eight int8 values as eight bf16 (exact).
+__device__ __forceinline__ uint4 i8x8_to_bf16(uint2 w) {
+    const uint2 lo = i8x4_to_bf16(w.x), hi = i8x4_to_bf16(w.y);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Split-K decode of int8 PAGED rows on MFMA (up to 8 query rows per kv head
+// in an 8-row tile, head_dim 64 / 128): grid, key splits, visibility and
+// partial format as decode_mfma_kernel<D, 8>. Each wave streams 32-key tiles
+// of its range into an LDS ring of its own (global_load_lds: NSTG stages,
+// NSTG tiles in flight while one is computed). A DMA instruction moves whole
+// rows (1 KiB: 1024 / D keys), so that every K/V row is fetched by one
+// instruction. In LDS a stage holds the tile's K rows and its V rows (key k
+// at k * D, its 16-byte unit u at unit u ^ swz(k), swizzles chosen so that
+// each operand read below touches every bank at most twice, the minimum for
+// 512 bytes) and 256 B of scales (word k the K scale of key k, word 32 + k
+// its V scale).
+// S^T (16 keys x 16 rows) = K Q^T on v_mfma_f32_16x16x32_bf16, the A operand
+// of block kb being keys kperm(kb, i) = 8 (i / 4) + 4 kb + i % 4, K converted
+// to bf16 from LDS (exact: int8 has 7 significant bits), scores times the K
+// scale; kperm puts lane (col, grp)'s eight scores on keys 8 grp .. 8 grp + 7,
+// the layout of the B operand P^T of O^T (16 dims x 16 rows) += V^T P^T on
+// v_mfma_f32_16x16x32_bf16 over the tile's 32 keys, whose A operand V^T
+// (8 keys of one dim per lane) is one ds_read_b64_tr_b8 per 16 dims. P
+// carries the V scale and is split into two bf16 terms. A fused append's new
+// rows are quantised as in decode_kernel (workgroup 0 stores them, the waves
+// that reach them read them from LDS).
+template <int D>
+__global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
+    constexpr int R = 8;                   // rows per tile and partial
+    constexpr int T = kI8MfmaKeys;         // keys per tile
+    constexpr int NSTG = KVRT_I8_MFMA_STAGES;
+    constexpr int KB = T * D;              // K (or V) bytes of a tile
+    constexpr int SB = 2 * KB + 256;       // stage: K, V, scales
+    constexpr int DPT = 2 * (KB / 1024) + 1;  // DMA instructions per tile
+    constexpr int WB = NSTG * SB;          // ring bytes per wave
+    constexpr int NQ = kMaxInt8Rows;
+    constexpr int LPR = D / 16;
+    constexpr int kPartBytes = kWaves * R * (D + 4) * 4;
+    constexpr int kLdsBytes = kWaves * WB > kPartBytes ? kWaves * WB : kPartBytes;
+    constexpr int CPR = D / 16;   // 16-byte units per row
+    constexpr int RPI = 64 / CPR;  // rows per DMA instruction
+    constexpr int RPB = 256 / D;   // rows per 256 bytes (one pass over the banks)
+    static_assert(T == 32 && (D == 64 || D == 128), "int8 MFMA decode tiles");
+    static_assert(DPT * NSTG < 64, "outstanding DMAs fit vmcnt");
+    static_assert(kLdsBytes + 2 * NQ * D + 8 * NQ + kWaves * (R * 8 + NSTG * 4) <= 80 * 1024,
+                  "two workgroups per CU");
+    __shared__ __align__(16) uint8_t lds_raw[kLdsBytes];
+    __shared__ float2 lds_ml[kWaves * R];
+    __shared__ uint32_t lds_unm[kWaves * NSTG];  // per (wave, stage): bit k = key k on an unmapped page
+    __shared__ __align__(16) uint4 nrow_k[NQ * LPR], nrow_v[NQ * LPR];
+    __shared__ float nrow_s[2 * NQ];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const int item = a.order[blockIdx.z];
+    const int kvh = blockIdx.y, hkv = gridDim.y;
+    const int split = blockIdx.x * kWaves + wave;
+    const int slot = a.slots[item];
+    const int len = __builtin_amdgcn_readfirstlane(a.len.lens[(int64_t)slot * a.len.stride + a.len.offset]);
+    int plen = 0;
+    uint32_t pw = ~0u;
+    load_prefix(a.pmask, slot, lane, plen, pw);
+    const int Qn = a.qn;
+    const int rows = a.group * Qn;
+    const bool fused = a.k_new != nullptr;
+    const int kend = fused ? len + Qn : len;
+    const int p0 = kend - Qn;
+    const int kstart = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int nk = max(0, kend - kstart);
+    int chunk = (nk + a.n_split - 1) / a.n_split;
+    chunk = (chunk + T - 1) / T * T;
+    const int ws = kstart + split * chunk;
+    const int we = min(kend, ws + chunk);
+    const int ntiles = we > ws ? (we - ws + T - 1) / T : 0;
+
+    apply_page_edits(a);
+
+    // Q^T as the B operand: column col is row r = col (q head kvh*g + r/Qn,
+    // query r % Qn), lane (col, grp) dims 32c + 8grp .. + 7 of step c; rows
+    // past the real ones read row 0 and are zeroed
+    const int hq = hkv * a.group;
+    const bool rvalid = col < rows;
+    uint4 qop[D / 32];
+    {
+        const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
+        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D + 8 * grp;
 #pragma unroll
-        for (int b = 0; b < D / 16; ++b)
-            *reinterpret_cast<float4 *>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
-        if (grp == 0) lds_ml[wave * R + col] = make_float2(m, l);
+        for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + 32 * c);
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c)
+            if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
-    constexpr int EPL = D / 64;  // dims per lane
-    const int64_t pbase = (((int64_t)item * hkv + kvh) * a.n_split + blockIdx.x) * R;
-    for (int r = wave; r < R && r < rows; r += kWaves) {
-        float M = kNegBig;
+    const int hi = rvalid ? p0 + col % Qn : -1;
+    const int lo = a.window > 0 ? p0 + col % Qn - a.window + 1 : 0;
+
+    // unit swizzles: K reads take units 2c + g2 of the 16 keys kperm(kb, i),
+    // V^T reads unit b of 32 keys
+    auto swz_k = [](int k) { return 2 * ((k >> 3) & (CPR / 2 - 1)); };
+    auto swz_v = [](int k) { return (k / RPB) & (CPR - 1); };
+    // this lane's key (tile-relative) for the row lookup and the scale DMA;
+    // the K/V DMAs take their rows from the lanes that looked them up
+    const int vkey = lane & 31;
+    const float *sc_src = lane < 32 ? a.kv.ks : a.kv.vs;
+    // the page-table entries of the wave's first 64 pages, one per lane
+    int pwin0 = ws >> a.kv.block_shift;
+    int pwin = load_page_window(a.kv, slot, pwin0, lane);
+    // q, the page window and the scale source are awaited before the first
+    // DMA: the compiler's own wait at a first use inside the loop would count
+    // only its own loads and so drain the ring on every tile
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2 * R + r].x);
-        float L = 0.f, acc[EPL];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-            const float2 ml = lds_ml[w2 * R + r];
-            const float ww = __builtin_amdgcn_exp2f(ml.x - M);
-            L = fmaf(ml.y, ww, L);
-            const float *src = lds_part + (w2 * R + r) * PP + lane * EPL;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[e] = fmaf(src[e], ww, acc[e]);
+    for (int c = 0; c < D / 32; ++c) asm volatile("" ::"v"(qop[c].x), "v"(qop[c].y), "v"(qop[c].z), "v"(qop[c].w));
+    asm volatile("" ::"v"(pwin), "v"(sc_src));
+
+    const uint32_t ring = lds_addr(lds_raw) + wave * WB;
+    const uint8_t *ring_p = lds_raw + wave * WB;
+    bool bad = false;  // a visible key on an unmapped page
+    // DMA of tile j into stage st. A tile spans at most T pages, so the
+    // window, moved to the tile when the tile leaves it, always covers it.
+    // Keys past we read key t0's row and are masked; keys on unmapped pages
+    // read pool row 0 and are masked (fused new rows excepted: those come
+    // from LDS, their page may be mapped by this launch).
+    auto dma_tile = [&](int j, int st) __attribute__((always_inline)) {
+        const int t0 = ws + j * T;
+        if (((min(we, t0 + T) - 1) >> a.kv.block_shift) - pwin0 >= 64) {
+            pwin0 = t0 >> a.kv.block_shift;
+            pwin = load_page_window(a.kv, slot, pwin0, lane);
+            asm volatile("" ::"v"(pwin));  // awaited here, not at a use past the branch
         }
-        float *dst = a.part_acc + (pbase + r) * D + lane * EPL;
-        if (a.cnt) {
-            store_agent_n<EPL>(dst, acc);
-            if (lane == 0) store_agent(a.part_ml + pbase + r, make_float2(M, L));
+        const int vc = t0 + vkey < we ? t0 + vkey : t0;
+        const int vrow = page_row(a.kv, __shfl(pwin, ((vc >> a.kv.block_shift) - pwin0) & 63), kvh, vc);
+        const bool unm = t0 + vkey < we && !(fused && t0 + vkey >= len) && vrow < 0;
+        bad |= unm;
+        const uint32_t bal = (uint32_t)__ballot(unm);
+        if (lane == 0) lds_unm[wave * NSTG + st] = bal;
+        const int rowc = max(vrow, 0);
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(ring + st * SB);
+        const int8_t *kb8 = static_cast<const int8_t *>(a.kv.k);
+        const int8_t *vb8 = static_cast<const int8_t *>(a.kv.v);
+#pragma unroll
+        for (int i = 0; i < KB / 1024; ++i) {
+            // lane l: unit l % CPR of tile row RPI i + l / CPR, whose pool row
+            // the lane of that key looked up
+            const int key = RPI * i + lane / CPR;
+            const int64_t row = (int64_t)__shfl(rowc, key) * D;
+            dma_load16(kb8 + row + 16 * ((lane % CPR) ^ swz_k(key)), dst + i * 1024);
+            dma_load16(vb8 + row + 16 * ((lane % CPR) ^ swz_v(key)), dst + KB + i * 1024);
+        }
+        dma_load4(sc_src + rowc, dst + 2 * KB);
+    };
+
+    float m = kNegBig, l = 0.f;  // running max (uniform per column) and this lane's partial sum
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int pro = min(NSTG, ntiles);
+    for (int j = 0; j < pro; ++j) dma_tile(j, j);
+    // A fused append's new rows, quantised while the first tiles stream in:
+    // workgroup 0 of each (item, kv head) stores them, the waves that reach
+    // them put them in LDS (their loads complete after the DMAs issued
+    // before them, so the wait for them also covers the first tiles, which
+    // the wave computes next)
+    if (fused && blockIdx.x == 0) i8_store_new_rows<D, KVRT_LAYOUT_PAGED>(a, item, slot, kvh, hkv, len, Qn);
+    if (fused && we > len) i8_new_rows_lds<D, NQ>(a, item, kvh, hkv, Qn, lane, nrow_k, nrow_v, nrow_s);
+    // this lane's K operand keys kperm(kb, col) (dims 32c + 8grp .. + 7 of
+    // step c) and V^T source key and half unit
+    const int kq0 = 8 * (col >> 2) + (col & 3), kq1 = kq0 + 4;
+    const int vk = 8 * grp + ((lane & 15) >> 1);
+    auto koff = [&](int k, int c) { return k * D + 16 * ((2 * c + (grp >> 1)) ^ swz_k(k)) + 8 * (grp & 1); };
+    const int voff = vk * D + 8 * (lane & 1);
+    for (int j = 0; j < ntiles; ++j) {
+        const int st = j % NSTG;
+        wait_vmem_steps<DPT, NSTG - 1>(min(NSTG - 1, ntiles - 1 - j));
+        const int t0 = ws + j * T;
+        const uint8_t *kst = ring_p + st * SB, *vst = kst + KB;
+        const float *scs = reinterpret_cast<const float *>(kst + 2 * KB);
+        uint2 kraw[2][D / 32], vraw[D / 16];
+        float ksc[8], vsc[8];
+        // a tile that reaches a fused append's new rows (wave-uniform) takes
+        // them, quantised, from LDS: per-lane addresses of the K units, V^T
+        // sources and scales of those keys point there
+        if (fused && t0 + T > len) {
+            const uint8_t *nk8 = reinterpret_cast<const uint8_t *>(nrow_k);
+            const uint8_t *nv8 = reinterpret_cast<const uint8_t *>(nrow_v);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int kq = kb ? kq1 : kq0;
+                const int key = t0 + kq;
+                const bool nw = key >= len && key < we;
+#pragma unroll
+                for (int c = 0; c < D / 32; ++c)
+                    kraw[kb][c] = *reinterpret_cast<const uint2 *>(
+                        nw ? nk8 + (key - len) * D + 32 * c + 8 * grp : kst + koff(kq, c));
+            }
+            {
+                const int key = t0 + vk;
+                const bool nw = key >= len && key < we;
+#pragma unroll
+                for (int b = 0; b < D / 16; ++b)
+                    vraw[b] = lds_read_tr8(nw ? nv8 + (key - len) * D + 16 * b + 8 * (lane & 1)
+                                              : vst + voff + 16 * (b ^ swz_v(vk)));
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int key = t0 + 8 * grp + jj;
+                const bool nw = key >= len && key < we;
+                ksc[jj] = nw ? nrow_s[key - len] : scs[8 * grp + jj];
+                vsc[jj] = nw ? nrow_s[NQ + key - len] : scs[32 + 8 * grp + jj];
+            }
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) dst[e] = acc[e];
-            if (lane == 0) a.part_ml[pbase + r] = make_float2(M, L);
+            for (int c = 0; c < D / 32; ++c) {
+                kraw[0][c] = *reinterpret_cast<const uint2 *>(kst + koff(kq0, c));
+                kraw[1][c] = *reinterpret_cast<const uint2 *>(kst + koff(kq1, c));
+            }
+#pragma unroll
+            for (int b = 0; b < D / 16; ++b) vraw[b] = lds_read_tr8(vst + voff + 16 * (b ^ swz_v(vk)));
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                ksc[jj] = scs[8 * grp + jj];
+                vsc[jj] = scs[32 + 8 * grp + jj];
+            }
+        }
+        const uint32_t unm = lds_unm[wave * NSTG + st];
+        wait_lds();  // the stage is in registers: refill it
+        if (j + NSTG < ntiles) dma_tile(j + NSTG, st);
+        // S^T for the two 16-key blocks: lane (col, grp) gets keys
+        // 8grp + 4kb + v (v < 4) of row col
+        f32x4_t s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < D / 32; ++c) s[kb] = mfma16(i8x8_to_bf16(kraw[kb][c]), qop[c], s[kb]);
+        }
+        float sc[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int key = t0 + 8 * grp + jj;
+            const bool vis = key < we && key <= hi && key >= lo && !((unm >> (8 * grp + jj)) & 1u);
+            sc[jj] = vis ? s[jj >> 2][jj & 3] * ksc[jj] * a.scale_log2 : -INFINITY;
+        }
+        if (t0 < plen) {  // the tile reaches into the prefix mask (wave-uniform)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int key = t0 + 8 * grp + jj;
+                sc[jj] = key < plen && !prefix_bit(pw, key) ? -INFINITY : sc[jj];
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) tmax = fmaxf(tmax, sc[jj]);
+        tmax = pair<OpMax, 32>(pair<OpMax, 16>(tmax));
+        lazy_rescale<D / 16>(tmax, m, l, o);
+        float p[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            p[jj] = __builtin_amdgcn_exp2f(sc[jj] - m);
+            l += p[jj];
+            p[jj] *= vsc[jj];  // dequantise V through P
+        }
+        // P = P_hi + P_lo in bf16: B operand keys 8grp + jj of row col
+        uint32_t ph[4], pl[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ph[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+            pl[i] = pack_bf16x2(p[2 * i] - bf16_lo(ph[i]), p[2 * i + 1] - bf16_hi(ph[i]));
+        }
+        const uint4 phv = make_uint4(ph[0], ph[1], ph[2], ph[3]), plv = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) {
+            const uint4 va = i8x8_to_bf16(vraw[b]);
+            o[b] = mfma16(va, plv, mfma16(va, phv, o[b]));
         }
     }
-    if (a.cnt) decode_merge_tail<D, R>(a, item, kvh, hkv, rows);
+    wait_vmem<0>();  // every DMA of the wave has landed before the LDS is reused
+    if (bad) a.err[0] = 1;
+    mfma_decode_finish<D, R>(a, lds_raw, lds_ml, o, m, l, wave, lane, rvalid, item, kvh, hkv, rows);
 }
 
 // grid (kv_heads, n_items, chunks), 256 threads: G consecutive threads merge
@@ -2577,6 +2959,16 @@ hipError_t launch_decode_mfma(const DecodeArgs &a, int head_dim, int dtype, int 
         return hipErrorInvalidValue;
     dim3 grid(a.n_split / kWaves, a.kv.kv_heads, a.n_items), block(256);
     const int rt = rows_tile(rows_per_head);
+    if (dtype == KVRT_INT8 && i8_mfma_dma(head_dim, rt)) {
+        auto go8 = [&](auto dc) -> hipError_t {
+            constexpr int HD = decltype(dc)::value;
+            hipLaunchKernelGGL((decode_i8_mfma_kernel<HD>), grid, block, 0, s, a);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess || a.cnt) return e;
+            return launch_merge<HD, 8>(a, s);
+        };
+        return head_dim == 64 ? go8(std::integral_constant<int, 64>{}) : go8(std::integral_constant<int, 128>{});
+    }
     auto go = [&](auto rc) -> hipError_t {
         constexpr int RT = decltype(rc)::value;
         KVRT_DISPATCH_D(head_dim, {

@@ -271,10 +271,17 @@ constexpr int kMaxWgPerHead = 64;
 constexpr int64_t kMfmaDecodeMinKeys8 = 2048;
 bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t keys, int layout) {
     if (mode == KVRT_DECODE_VALU) return false;
-    // int8 (PAGED): AUTO keeps the VALU kernel; its page-window lookups and
-    // 16 keys per pass in 4 waves per SIMD beat the MFMA kernel's one 16-key
-    // tile in flight per wave at this row size (config 5: 32.6 vs 44.5 us)
-    if (dtype == KVRT_INT8) return mode == KVRT_DECODE_MFMA;
+    // int8 (PAGED): AUTO keeps the VALU kernel. A forced MFMA decode runs
+    // the int8 ring kernel at head_dim 64 / 128 (i8_mfma_dma), the register-
+    // staged MFMA tiles elsewhere. At config 5 the ring kernel matches the
+    // VALU kernel per launch (29.0 vs 28.0 us, fused 32.2 vs 31.7) with a
+    // third of its VALU instructions, and runs the step slower (0.838 vs
+    // 0.808 ms); KVRT_I8_MFMA=1 lets AUTO take it.
+    if (dtype == KVRT_INT8) {
+        static const char *env = std::getenv("KVRT_I8_MFMA");
+        static const bool ring = env && std::atoi(env) != 0;
+        return mode == KVRT_DECODE_MFMA || (ring && i8_mfma_dma(head_dim, rows_tile_));
+    }
     if (rows_tile_ < kMfmaDecodeMinRows) {
         // 1-4 rows (the talker's 2) ride an 8-row tile: AUTO takes it where
         // the tiles stream through the LDS DMA ring, over as many keys as the
@@ -558,8 +565,15 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
             return KVRT_EINVAL;
         }
     }
-    if (any_paged && (!is_pow2(cfg->block_size) || cfg->block_size > 1024 || cfg->pool_pages <= 0))
+    if (any_paged && (!is_pow2(cfg->block_size) || cfg->block_size > 1024 || cfg->pool_pages <= 0 ||
+                      cfg->pool_pages >= (1 << 24)))
         return KVRT_EINVAL;
+    for (int i = 0; i < cfg->n_layers; ++i) {
+        // the kernels number a pool's rows in 32 bits
+        const kvrt_layer_spec &s = specs[i];
+        if (s.shared_src < 0 && s.layout == KVRT_LAYOUT_PAGED && (int64_t)cfg->pool_pages * s.kv_heads * cfg->block_size > INT32_MAX)
+            return KVRT_EINVAL;
+    }
 
     kvrt_ctx *c = new (std::nothrow) kvrt_ctx();
     if (!c) return KVRT_EDEVICE;
@@ -709,9 +723,11 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         if (rc != KVRT_OK) return rc;
     }
     if (fused) {
-        // int8 rows are quantised in-kernel by the VALU decode only (the
-        // caller routes a forced MFMA decode through the append kernel)
-        if (s.dtype == KVRT_INT8 && (s.layout != KVRT_LAYOUT_PAGED || c->cfg.decode_kernel == KVRT_DECODE_MFMA))
+        // int8 rows are quantised in-kernel by the VALU decode and the int8
+        // MFMA ring kernel (the caller routes other forced MFMA decodes
+        // through the append kernel)
+        if (s.dtype == KVRT_INT8 && (s.layout != KVRT_LAYOUT_PAGED || (c->cfg.decode_kernel == KVRT_DECODE_MFMA &&
+                                                                      !i8_mfma_dma(D, rows_tile(rows)))))
             return KVRT_EINVAL;
         if (!tensor_ok(k, KVRT_BF16, 4) || !tensor_ok(v, KVRT_BF16, 4) || !is_contiguous(k) || !is_contiguous(v))
             return KVRT_EINVAL;
@@ -743,8 +759,9 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     // the MFMA kernel's PAGED D 512 variant has no registers for a mask
     const bool mfma = !talker && use_mfma_decode(c->cfg.decode_kernel, s.dtype, R, D, bucket_keys, s.layout) &&
                       !(pmask && s.layout == KVRT_LAYOUT_PAGED && D >= 512);
+    const int mfma_keys = s.dtype == KVRT_INT8 && i8_mfma_dma(D, R) ? kI8MfmaKeys : kMfmaDecodeKeys;
     const int n_split = choose_splits(target_wgs(c->cfg, mfma ? KVRT_BF16 : s.dtype), n, hkv, max_keys,
-                                      mfma ? kMfmaDecodeKeys : keys_per_iteration(D, R, s.dtype, s.layout));
+                                      mfma ? mfma_keys : keys_per_iteration(D, R, s.dtype, s.layout));
     const int Rw = mfma ? std::max(R, kMfmaDecodeMinRows) : R;  // rows per partial (MFMA tiles are 8 or 16)
     const size_t acc_elems = (size_t)n * hkv * n_split * Rw * D;
     int rc = ensure_workspace(c, workspace_bytes(n, hkv, n_split, Rw, D));
@@ -1903,12 +1920,18 @@ int kvrt_append_attend_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32_
     if (rc) return rc;
     if (!valid_layer(c, layer) || !distinct_slots(c, n, slots) || !k || !v) return KVRT_EINVAL;
     if (c->layers[layer].owner != layer) return KVRT_EINVAL;  // shared layers append nothing
-    if (c->layers[layer].spec.dtype == KVRT_INT8 && c->cfg.decode_kernel == KVRT_DECODE_MFMA) {
-        // the MFMA decode reads int8 rows only: the append kernel quantises
-        // them first
-        rc = append_impl(c, layer, n, slots, k, v);
-        if (rc) return rc;
-        return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
+    const kvrt_layer_spec &ls = c->layers[layer].spec;
+    if (ls.dtype == KVRT_INT8 && c->cfg.decode_kernel == KVRT_DECODE_MFMA) {
+        // the register-staged MFMA decode reads int8 rows only: the append
+        // kernel quantises them first (the int8 ring kernel quantises them
+        // in its own launch)
+        int64_t rows = 0;
+        if (tensor_ok(q, KVRT_BF16, 4) && q->dims[1] % ls.kv_heads == 0) rows = q->dims[1] / ls.kv_heads * q->dims[2];
+        if (!(rows > 0 && rows <= 16 && i8_mfma_dma(ls.head_dim, rows_tile((int)rows)))) {
+            rc = append_impl(c, layer, n, slots, k, v);
+            if (rc) return rc;
+            return decode_impl(c, layer, n, slots, q, nullptr, nullptr, out, scale);
+        }
     }
     // one launch: the decode stores the new rows (int8: quantised in-kernel)
     return decode_impl(c, layer, n, slots, q, k, v, out, scale);

@@ -124,7 +124,9 @@ typedef struct kvrt_config {
     int32_t n_slots;      /* sessions / streams                               */
     int32_t capacity;     /* max logical tokens per slot                      */
     int32_t block_size;   /* PAGED: tokens per page (power of two, e.g. 16)   */
-    int32_t pool_pages;   /* PAGED: pages in the shared pool                  */
+    int32_t pool_pages;   /* PAGED: pages in the shared pool (< 2^24, and
+                             pool_pages * kv_heads * block_size < 2^31 for
+                             every PAGED layer: rows are numbered in 32 bits) */
     int32_t max_q;        /* max rows per decode append / attend; RING rows >= W + max_q - 1 */
     int32_t pool_seed;    /* PAGED: nonzero = hand out pool pages in an order
                              shuffled with this seed (0 = ascending)          */

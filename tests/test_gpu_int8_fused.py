@@ -18,21 +18,25 @@ from tests.helpers import bits, randn_bf16
 pytestmark = pytest.mark.gpu
 
 
-def _rt(max_q):
+def _rt(max_q, kernel="auto"):
     from kvrt import KVRuntime, LayerSpec
 
     spec = LayerSpec(kv_heads=8, head_dim=128, layout="paged", dtype="int8")
-    return KVRuntime([spec], 4, 640, max_q=max_q, device="cuda", block_size=16, pool_pages=160, pool_seed=4)
+    return KVRuntime([spec], 4, 640, max_q=max_q, device="cuda", block_size=16, pool_pages=160, pool_seed=4,
+                     decode_kernel=kernel)
 
 
 def _raw(t):
     return t.detach().cpu().contiguous().view(torch.uint8).numpy()
 
 
+@pytest.mark.parametrize("kernel", ["auto", "mfma"])
 @pytest.mark.parametrize("qn", [1, 2])
-def test_fused_int8_append_attend_equals_append_then_attend(qn):
+def test_fused_int8_append_attend_equals_append_then_attend(qn, kernel):
+    """AUTO runs the VALU decode; a forced MFMA decode at this shape runs the
+    int8 ring kernel, which quantises the new rows in its own launch too."""
     gen = torch.Generator().manual_seed(60 + qn)
-    fused, two = _rt(qn), _rt(qn)
+    fused, two = _rt(qn, kernel), _rt(qn, kernel)
     slots = [3, 0, 1]
     lens = [37, 130, 79]  # the appends cross block boundaries on different steps
     for s, n in zip(slots, lens):

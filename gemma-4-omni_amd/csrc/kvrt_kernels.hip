@@ -105,21 +105,6 @@ __device__ __forceinline__ int64_t page_row_offset(const KVView &v, int page, in
     return row < 0 ? -1 : (int64_t)row * D;
 }
 
-// PAGED row offset with the page taken from a wave's window of page-table
-// entries (lane i holds the entry of logical page win0 + i; pages past the
-// window are looked up directly). Every lane of the wave must call it.
-__device__ __forceinline__ int64_t paged_offset(const KVView &v, int slot, int head, int pos, int D, int win,
-                                                int win0) {
-    const int lp = pos >> v.block_shift;
-    const int idx = lp - win0;
-    int page = __shfl(win, idx & 63);
-    if (idx < 0 || idx >= 64) {
-        if (pos < 0 || lp >= v.pt_stride) return -1;
-        page = v.page_table[(int64_t)slot * v.pt_stride + lp];
-    }
-    return page_row_offset(v, page, head, pos, D);
-}
-
 // Symmetric int8 quantisation of one (token, head) row whose D values are
 // spread over G consecutive lanes, NV per lane: scale = amax / 127,
 // q = clamp(rne(x / scale), -127, 127), zeros when amax == 0. q packs this
@@ -1470,16 +1455,31 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     int pwin = -1, pwin0 = 0;
     if constexpr (PWIN) {
         pwin0 = ws >> a.kv.block_shift;
-        const int lp = pwin0 + lane;
-        if (lp < a.kv.pt_stride) pwin = a.kv.page_table[(int64_t)slot * a.kv.pt_stride + lp];
+        pwin = load_page_window(a.kv, slot, pwin0, lane);
     }
-    // Row offset of key kk of the wave's range (keys past we read row ws and
-    // are masked).
+    // PWIN: the window moves (a wave-uniform branch, before the tile's
+    // loads) when the tile at t0 leaves it; a tile spans at most T pages, so
+    // the window then covers it, and no page-table load sits between K/V
+    // loads (its wait would hold every later load until all earlier ones
+    // had landed)
+    auto tile_window = [&](int t0) __attribute__((always_inline)) {
+        if constexpr (PWIN) {
+            if (((min(we, t0 + T) - 1) >> a.kv.block_shift) - pwin0 >= 64) {
+                pwin0 = t0 >> a.kv.block_shift;
+                pwin = load_page_window(a.kv, slot, pwin0, lane);
+                asm volatile("" ::"v"(pwin));
+            }
+        }
+    };
+    // Row offset of key kk of the wave's range (keys past we read row ws, or
+    // with PWIN a row of the window, and are masked).
     auto key_off = [&](int kk) __attribute__((always_inline)) {
         const int kc = kk < we ? kk : ws;
         int64_t off;
-        if constexpr (PWIN) off = paged_offset(a.kv, slot, kvh, kc, D, pwin, pwin0);
-        else off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
+        if constexpr (PWIN)
+            off = page_row_offset(a.kv, __shfl(pwin, ((kc >> a.kv.block_shift) - pwin0) & 63), kvh, kc, D);
+        else
+            off = row_offset<LAYOUT>(a.kv, slot, kvh, kc, D);
         if constexpr (LAYOUT == KVRT_LAYOUT_PAGED) {
             // a fused append's new rows come from k_new / v_new (their page
             // may be mapped by this very launch)
@@ -1512,6 +1512,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int KR = I8 ? D / 64 : D / 32, VR = I8 ? D / 64 : D / 32;
     constexpr int VU = I8 ? D / 16 : D / 8;  // 16-byte units per V row
     auto load_k = [&](int t0, uint4 (&ka)[KR], float &ks, float &vs) __attribute__((always_inline)) {
+        tile_window(t0);  // load_k comes first for every tile
         if constexpr (I8) {
             const int64_t off = key_off(t0 + col);
             const int8_t *kp = static_cast<const int8_t *>(a.kv.k) + off;

@@ -168,6 +168,8 @@ def test_layer_storage_bytes_per_layout():
     dict(spec=dict(dtype=1)),                                   # int8 needs PAGED
     dict(spec=dict(layout=1, window=8, ring_rows=8)),          # ring rows < W + max_q - 1
     dict(spec=dict(layout=2), cfg=dict(block_size=12)),        # block size not a power of two
+    dict(spec=dict(layout=2), cfg=dict(block_size=1, pool_pages=1 << 24)),  # pages past 24 bits
+    dict(spec=dict(layout=2, kv_heads=64), cfg=dict(block_size=1024, pool_pages=1 << 15)),  # rows past 31 bits
     dict(spec=dict(shared_src=0)),                              # a layer cannot alias itself
 ])
 def test_create_rejects_invalid_configs_before_touching_the_device(bad):

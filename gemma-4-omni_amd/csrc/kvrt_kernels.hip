@@ -167,50 +167,17 @@ __device__ __forceinline__ int64_t new_row_offset(const DecodeArgs &a, int slot,
     }
 }
 
-// Fused int8 append, store side: the launch's Qn new rows of (item, kv head)
-// quantised exactly as the append kernel does (D/16 lanes of 16 values per
-// row, quantize16_bf16) and stored with their scales, by the calling
-// workgroup's threads together.
-template <int D, int LAYOUT>
-__device__ __forceinline__ void i8_store_new_rows(const DecodeArgs &a, int item, int slot, int kvh, int hkv, int len,
-                                                  int Qn) {
-    constexpr int LPR = D / 16;
-    for (int c0 = 0; c0 < Qn * LPR; c0 += blockDim.x) {
-        const int c = c0 + threadIdx.x;
-        const bool live = c < Qn * LPR;
-        const int r = live ? c / LPR : 0, sg = c % LPR;
-        const int64_t src = (((int64_t)item * hkv + kvh) * Qn + r) * D + sg * 16;
-        uint4 kx2[2], vx2[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            kx2[h] = *reinterpret_cast<const uint4 *>(a.k_new + src + 8 * h);
-            vx2[h] = *reinterpret_cast<const uint4 *>(a.v_new + src + 8 * h);
-        }
-        uint4 kq, vq;
-        const float ksc = quantize16_bf16<LPR>(kx2, kq);
-        const float vsc = quantize16_bf16<LPR>(vx2, vq);
-        if (live) {
-            const int64_t dst = new_row_offset<LAYOUT>(a, slot, kvh, len + r, D);
-            if (dst < 0) {
-                a.err[0] = 1;
-            } else {
-                *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.k) + dst + sg * 16) = kq;
-                *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.v) + dst + sg * 16) = vq;
-                if (sg == 0) {
-                    a.kv.ks[dst / D] = ksc;
-                    a.kv.vs[dst / D] = vsc;
-                }
-            }
-        }
-    }
-}
-// Fused int8 append, read side: the same rows quantised again into LDS by the
-// calling wave (row r: 16-byte units nrow_k / nrow_v[r * D/16 + unit], scales
-// nrow_s[r] (K) and nrow_s[NQ + r] (V)), for the decode's tile or pass that
-// attends over them.
-template <int D, int NQ>
-__device__ __forceinline__ void i8_new_rows_lds(const DecodeArgs &a, int item, int kvh, int hkv, int Qn, int lane,
-                                                uint4 *nrow_k, uint4 *nrow_v, float *nrow_s) {
+// Fused int8 append: the launch's Qn new rows of (item, kv head) quantised
+// exactly as the append kernel quantises them (D/16 lanes of 16 values per
+// row, quantize16_bf16) by the calling wave into LDS (row r: 16-byte units
+// nrow_k / nrow_v[r * D/16 + unit], scales nrow_s[r] (K) and nrow_s[NQ + r]
+// (V)), for the decode's pass or tile that attends over them; with store,
+// also into the cache with their scales (the one wave whose key range
+// starts at or before the first new row does that).
+template <int D, int NQ, int LAYOUT>
+__device__ __forceinline__ void i8_new_rows(const DecodeArgs &a, int item, int slot, int kvh, int hkv, int len,
+                                            int Qn, int lane, bool store, uint4 *nrow_k, uint4 *nrow_v,
+                                            float *nrow_s) {
     constexpr int LPR = D / 16, RPW = 64 / LPR;
     const int sub = lane / LPR, seg = lane % LPR;
     const int64_t base = (((int64_t)item * hkv + kvh) * Qn) * D + seg * 16;
@@ -233,6 +200,19 @@ __device__ __forceinline__ void i8_new_rows_lds(const DecodeArgs &a, int item, i
             if (seg == 0) {
                 nrow_s[r] = ks;
                 nrow_s[NQ + r] = vs;
+            }
+            if (store) {
+                const int64_t dst = new_row_offset<LAYOUT>(a, slot, kvh, len + r, D);
+                if (dst < 0) {
+                    a.err[0] = 1;
+                } else {
+                    *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.k) + dst + seg * 16) = kq;
+                    *reinterpret_cast<uint4 *>(static_cast<int8_t *>(a.kv.v) + dst + seg * 16) = vq;
+                    if (seg == 0) {
+                        a.kv.ks[dst / D] = ks;
+                        a.kv.vs[dst / D] = vs;
+                    }
+                }
             }
         }
     }
@@ -763,22 +743,22 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         }
     }
 
-    // Fused int8 append. Workgroup 0 of every (item, kv head) quantises the
-    // new rows (exactly as the append kernel does: LPR lanes of 16 values per
-    // row) and stores them with their scales; no workgroup of the launch reads
-    // those cache rows. A wave whose key range reaches them quantises them
-    // again into LDS before its main loop, where registers are free, for the
-    // pass that reaches them. Two waves of a workgroup may both fill the LDS
-    // copy: they write the same bytes, and each reads its own writes. (The
-    // rows are loaded here rather than next to the length load: holding them
-    // from there raised the kernel to 132 VGPRs, 3 waves per SIMD, and config
-    // 5 from 0.83 to 0.94 ms per step; one loop for both copies took 130.)
+    // Fused int8 append. A wave whose key range reaches the new rows
+    // quantises them (exactly as the append kernel does: LPR lanes of 16
+    // values per row) into LDS before its main loop, where registers are
+    // free, for the pass that reaches them; the one whose range starts at or
+    // before the first of them also stores them with their scales (no
+    // workgroup of the launch reads those cache rows). Two waves of a
+    // workgroup may both fill the LDS copy: they write the same bytes, and
+    // each reads its own writes. (The rows are loaded here rather than next
+    // to the length load: holding them from there raised the kernel to 132
+    // VGPRs, 3 waves per SIMD, and config 5 from 0.83 to 0.94 ms per step.)
     constexpr int NQ = KDT == KVRT_INT8 ? kMaxInt8Rows : 1;
     __shared__ uint4 nrow_k[NQ * LPR], nrow_v[NQ * LPR];
     __shared__ float nrow_s[2 * NQ];
     if constexpr (KDT == KVRT_INT8) {
-        if (fused && blockIdx.x == 0) i8_store_new_rows<D, LAYOUT>(a, item, slot, kvh, hkv, len, Qn);
-        if (fused && we > len) i8_new_rows_lds<D, NQ>(a, item, kvh, hkv, Qn, lane, nrow_k, nrow_v, nrow_s);
+        if (fused && we > len)
+            i8_new_rows<D, NQ, LAYOUT>(a, item, slot, kvh, hkv, len, Qn, lane, ws <= len, nrow_k, nrow_v, nrow_s);
     }
 
     // q rows of this kv head, packed bf16 pairs. Row r = j*Q + i of the tile
@@ -1782,8 +1762,8 @@ __device__ __forceinline__ uint4 i8x8_to_bf16(uint2 w) {
 // v_mfma_f32_16x16x32_bf16 over the tile's 32 keys, whose A operand V^T
 // (8 keys of one dim per lane) is one ds_read_b64_tr_b8 per 16 dims. P
 // carries the V scale and is split into two bf16 terms. A fused append's new
-// rows are quantised as in decode_kernel (workgroup 0 stores them, the waves
-// that reach them read them from LDS).
+// rows are quantised as in decode_kernel (by the waves that reach them, into
+// LDS; the first of those also stores them).
 template <int D>
 __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     constexpr int R = 8;                   // rows per tile and partial
@@ -1915,13 +1895,14 @@ __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     for (int b = 0; b < D / 16; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int pro = min(NSTG, ntiles);
     for (int j = 0; j < pro; ++j) dma_tile(j, j);
-    // A fused append's new rows, quantised while the first tiles stream in:
-    // workgroup 0 of each (item, kv head) stores them, the waves that reach
-    // them put them in LDS (their loads complete after the DMAs issued
-    // before them, so the wait for them also covers the first tiles, which
-    // the wave computes next)
-    if (fused && blockIdx.x == 0) i8_store_new_rows<D, KVRT_LAYOUT_PAGED>(a, item, slot, kvh, hkv, len, Qn);
-    if (fused && we > len) i8_new_rows_lds<D, NQ>(a, item, kvh, hkv, Qn, lane, nrow_k, nrow_v, nrow_s);
+    // A fused append's new rows, quantised while the first tiles stream in
+    // by the waves that reach them, into LDS (the one whose range starts at
+    // or before the first of them also stores them; their loads complete
+    // after the DMAs issued before them, so the wait for them also covers
+    // the first tiles, which the wave computes next)
+    if (fused && we > len)
+        i8_new_rows<D, NQ, KVRT_LAYOUT_PAGED>(a, item, slot, kvh, hkv, len, Qn, lane, ws <= len, nrow_k, nrow_v,
+                                              nrow_s);
     // this lane's K operand keys kperm(kb, col) (dims 32c + 8grp .. + 7 of
     // step c) and V^T source key and half unit
     const int kq0 = 8 * (col >> 2) + (col & 3), kq1 = kq0 + 4;

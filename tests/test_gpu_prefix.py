@@ -101,6 +101,45 @@ def test_prefix_mask_decode_parity(d, qn, layout, kernel):
     assert rt.health() == 0
 
 
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+@pytest.mark.parametrize("d,hq,qn", [(128, 8, 1), (128, 2, 1), (64, 4, 2)])
+def test_prefix_mask_int8_paged_decode_parity(d, hq, qn, kernel):
+    """int8 PAGED decodes under prefix masks: the VALU decode and (forced
+    MFMA, head_dim 64 / 128) the int8 MFMA ring kernel, whose 32-key tiles
+    test the mask per key; fused append + attend steps quantise the new rows
+    in the launch."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(d + hq * 7 + qn)
+    spec = LayerSpec(kv_heads=1, head_dim=d, layout="paged", dtype="int8")
+    rt = KVRuntime([spec], 4, 1400, max_q=qn, decode_kernel=kernel, block_size=16,
+                   pool_pages=4 * 1400 // 16 + 8, pool_seed=6, device="cuda")
+    orc = O.OracleCache([O.OracleLayer(1, d, 0, int8=True)], 4)
+    masks = [_mask("canonical", 34, gen), _mask("random", 512, gen), _mask("zeros", 200, gen), None]
+    lens = [600, 1200, 900, 700]
+    for s, (n, m) in enumerate(zip(lens, masks)):
+        k, v = randn_bf16(gen, (1, 1, n, d)), randn_bf16(gen, (1, 1, n, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+        if m is not None:
+            rt.set_prefix_attention(s, torch.from_numpy(m).cuda())
+            orc.set_prefix_attention(s, m)
+    slots = [0, 1, 2, 3]
+    worst = 0.0
+    for _ in range(3):
+        q = randn_bf16(gen, (4, hq, qn, d), 1.0 / math.sqrt(d))
+        k, v = randn_bf16(gen, (4, 1, qn, d)), randn_bf16(gen, (4, 1, qn, d))
+        c0 = rt.counters()
+        out = rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), slots, 1.0)
+        torch.cuda.synchronize()
+        assert rt.counters()["mfma_decodes"] - c0["mfma_decodes"] == (1 if kernel == "mfma" else 0)
+        for i, s in enumerate(slots):
+            orc.append(s, 0, to_np(k[i]), to_np(v[i]))
+            worst = max(worst, float(np.abs(to_np(out[i]) - orc.attend(s, 0, to_np(q[i]), 1.0)).max()))
+    assert worst <= ATOL
+    assert rt.health() == 0
+
+
 @pytest.mark.parametrize("d,layout,qn,plen", [(256, "ring", 291, 34), (512, "contig", 291, 34),
                                               (256, "contig", 64, 512), (512, "paged", 40, 300)])
 def test_prefix_mask_prefill_parity(d, layout, qn, plen):

@@ -1774,10 +1774,9 @@ __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     constexpr int DPT = 2 * (KB / 1024) + 1;  // DMA instructions per tile
     constexpr int WB = NSTG * SB;          // ring bytes per wave
     constexpr int NQ = kMaxInt8Rows;
-    constexpr int LPR = D / 16;
     constexpr int kPartBytes = kWaves * R * (D + 4) * 4;
     constexpr int kLdsBytes = kWaves * WB > kPartBytes ? kWaves * WB : kPartBytes;
-    constexpr int CPR = D / 16;   // 16-byte units per row
+    constexpr int CPR = D / 16;   // 16-byte units per int8 row
     constexpr int RPI = 64 / CPR;  // rows per DMA instruction
     constexpr int RPB = 256 / D;   // rows per 256 bytes (one pass over the banks)
     static_assert(T == 32 && (D == 64 || D == 128), "int8 MFMA decode tiles");
@@ -1787,7 +1786,7 @@ __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint8_t lds_raw[kLdsBytes];
     __shared__ float2 lds_ml[kWaves * R];
     __shared__ uint32_t lds_unm[kWaves * NSTG];  // per (wave, stage): bit k = key k on an unmapped page
-    __shared__ __align__(16) uint4 nrow_k[NQ * LPR], nrow_v[NQ * LPR];
+    __shared__ __align__(16) uint4 nrow_k[NQ * CPR], nrow_v[NQ * CPR];
     __shared__ float nrow_s[2 * NQ];
 
     const int lane = threadIdx.x & 63;

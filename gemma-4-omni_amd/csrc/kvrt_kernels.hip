@@ -2597,12 +2597,12 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     }
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     uint16_t *op = a.out + (((int64_t)item * hq + head) * Qn + qr) * D + 4 * grp;
+    // v_cvt_pk_bf16_f32: round to nearest even, as f32_to_bf16 for every
+    // non-NaN value, in one instruction per pair
 #pragma unroll
-    for (int b = 0; b < D / 16; ++b) {
-        const uint32_t w0 = (uint32_t)f32_to_bf16(o[b][0] * inv) | ((uint32_t)f32_to_bf16(o[b][1] * inv) << 16);
-        const uint32_t w1 = (uint32_t)f32_to_bf16(o[b][2] * inv) | ((uint32_t)f32_to_bf16(o[b][3] * inv) << 16);
-        *reinterpret_cast<uint2 *>(op + 16 * b) = make_uint2(w0, w1);
-    }
+    for (int b = 0; b < D / 16; ++b)
+        *reinterpret_cast<uint2 *>(op + 16 * b) =
+            make_uint2(pack_bf16x2(o[b][0] * inv, o[b][1] * inv), pack_bf16x2(o[b][2] * inv, o[b][3] * inv));
 }
 
 // Merge of a key-split prefill: one thread per (item, q head, query, dim),

@@ -2000,10 +2000,13 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     // to 29.6 us, talker Q 512 from 33.6 to 29.7 us and thinker Q 2048 from
     // 93.2 to 67.2 us; 4 parts (talker: 147 KB of LDS, one workgroup per CU)
     // 43.9 us for the talker. KVRT_PF_KEY_PARTS caps it.
-    static const int parts_env = env_int("KVRT_PF_KEY_PARTS", 2);
+    static const int parts_env = env_int("KVRT_PF_KEY_PARTS", 0);
     const int64_t wgs_grid = (int64_t)((qn + 15) / 16) * hkv * (group / hw) * n;
-    int parts = std::min({parts_env, prefill_max_parts(D), 8 / hw});
-    if (wgs_grid >= 512) parts = 1;  // a grid of two workgroups per CU needs no more waves per block
+    int parts = std::min({parts_env > 0 ? parts_env : 2, prefill_max_parts(D), 8 / hw});
+    // a grid of two workgroups per CU needs no more waves per block (talker
+    // Q 512: 23.3 us with one part, 24.4 us with two); KVRT_PF_KEY_PARTS
+    // sets the parts there too
+    if (wgs_grid >= 512 && parts_env == 0) parts = 1;
     parts = parts >= 4 ? 4 : parts >= 2 ? 2 : 1;
     while (parts > 1 && s.layout == KVRT_LAYOUT_RING && s.ring_rows < kPfKeys * parts) parts /= 2;
     a.key_parts = parts;

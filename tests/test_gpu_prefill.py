@@ -81,6 +81,10 @@ def _check(rt, orc, q, scale, prefill=True):
         (16, 8, 128, 0, "contig", [0, 0, 0, 0], 512),
         # LDS DMA ring over a wrapped ring layout, two waves per head
         (8, 2, 128, 200, "ring", [900, 64], 77),
+        # talker-sized grids (>= 512 workgroups, DMA ring): an odd block count
+        # over ragged prefixes, and a windowed ring layout
+        (16, 8, 128, 0, "contig", [0, 37, 300, 5], 481),
+        (16, 8, 128, 200, "ring", [0, 900, 64, 10], 300),
     ],
 )
 def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):

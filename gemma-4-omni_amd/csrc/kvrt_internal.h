@@ -301,6 +301,7 @@ struct PrefillArgs {
     int32_t heads_per_wg;   // q heads of the group served by one workgroup (divides group)
     int32_t key_parts;      // waves per head splitting every tile's keys (1, 2 or 4)
     int32_t ring_groups;    // > 0: LDS DMA ring of key_parts * ring_groups 32-key stages (prefill_ring_ok)
+    int32_t q_blocks;       // 16-query blocks per workgroup sharing its staged tiles (1; 2 on the ring)
     int32_t n_ksplit;       // key ranges per query block; > 1: partials to part_o / part_ml
     float *part_o;          // [n, Hq, Q, n_ksplit, D] unnormalised outputs
     float2 *part_ml;        // [n, Hq, Q, n_ksplit] (running max in log2 units, sum)
@@ -385,11 +386,13 @@ constexpr int prefill_max_parts(int head_dim) { return head_dim >= 512 ? 1 : hea
 // Shapes of the prefill's LDS DMA ring: bf16 CONTIG / RING rows of 128 or
 // 256 dims, key_parts (1 or 2) * kPfRingGroups unpadded 32-key stages (K and
 // V), one group of key_parts stages computed while the next is in flight
-// (deeper rings measured slower: their LDS costs workgroups per CU).
+// (deeper rings measured slower: their LDS costs workgroups per CU); at
+// head_dim 128 one or two 16-query blocks per workgroup.
 constexpr int kPfRingGroups = 2;
-constexpr bool prefill_ring_ok(int head_dim, int layout, int key_parts, int groups) {
+constexpr bool prefill_ring_ok(int head_dim, int layout, int key_parts, int groups, int q_blocks = 1) {
     return (head_dim == 128 || head_dim == 256) && layout != KVRT_LAYOUT_PAGED && groups == kPfRingGroups &&
-           (key_parts == 1 || key_parts == 2) && key_parts * groups * 32 * head_dim * 2 * 2 <= 128 * 1024;
+           (key_parts == 1 || key_parts == 2) && key_parts * groups * 32 * head_dim * 2 * 2 <= 128 * 1024 &&
+           (q_blocks == 1 || (q_blocks == 2 && head_dim == 128));
 }
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s);
 hipError_t launch_set_pages(int32_t *pt, int n, const int32_t *idx, const int32_t *val,

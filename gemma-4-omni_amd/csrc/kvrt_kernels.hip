@@ -2066,7 +2066,9 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // grid (ceil(Q / 16), kv_heads * g / hw, n_items), 64 * NW threads with NW =
 // 4 or 8 >= hw: workgroup (x, y) serves the hw q heads
-// kvh*g + (y % (g/hw))*hw + j (wave j < hw) over the 16 query rows of block x;
+// kvh*g + (y % (g/hw))*hw + j (wave j < hw) over the 16 query rows of block x
+// (on the DMA ring with QB = 2: x over ceil(Q / 32) pairs of blocks, waves
+// hw .. 2 hw - 1 on the second block of the pair);
 // all NW waves stage each 32-key K/V tile into LDS (K row-major, V
 // transposed) and the hw computing waves share it. With PF the next tile's
 // global loads are issued into registers before the current tile is
@@ -2190,7 +2192,7 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
     });
 }
 
-template <int D, int LAYOUT, int NW, bool PF, int KS, int G = 0>
+template <int D, int LAYOUT, int NW, bool PF, int KS, int G = 0, int QB = 1>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = pf_pitch<D>();  // K / V tile row pitch (bf16)
     constexpr int TK = kPfKeys * KS;   // keys per iteration: KS sub-tiles of 32
@@ -2204,6 +2206,9 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     // G > 0: the LDS DMA ring (bf16 CONTIG / RING, D 128 / 256): NS = KS * G
     // unpadded, swizzled 32-key stages (pf_rswz), G - 1 groups of KS in flight
     constexpr bool RG = G > 0;
+    // QB = 2: two consecutive 16-query blocks share the workgroup's staged
+    // tiles (half the tile traffic and DMA instructions per block)
+    static_assert(QB == 1 || (QB == 2 && RG && D == 128), "query-block pairs: DMA ring, head_dim 128");
     constexpr int NS = KS * (RG ? G : 1);
     constexpr int RSUB = kPfKeys * D;   // bf16 elements of one ring stage (K or V)
     constexpr int LDS_ELEMS = RG ? NS * RSUB : NBUF * TILE;
@@ -2212,18 +2217,21 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                           (D / 8) % NW == 0), "DMA ring: bf16 CONTIG / RING, D 128 / 256");
     // the KS - 1 upper parts' accumulators fit the tile buffers for the final combine
     static_assert((KS - 1) * (NW / KS) * 16 * D * 4 <= LDS_ELEMS * 2, "part combine fits LDS");
+    static_assert((KS - 1) * (NW / KS) * 16 * 8 <= LDS_ELEMS * 2, "part (m, l) fit LDS");
     __shared__ __align__(16) uint16_t sk[LDS_ELEMS];
     __shared__ __align__(16) uint16_t sv[LDS_ELEMS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int hw = a.heads_per_wg, nhb = a.group / hw;
-    // Wave w computes head w % hw over key part w / hw: within every tile,
-    // part p takes the 32-key sub-tile p, and the parts' accumulators are
-    // combined at the end (KS > 1 puts 2 or 4 waves on one head and query
-    // block without staging any tile twice).
-    const int hidx = wave % hw, part = wave / hw;
+    // Wave w computes head w % hw over key part (w / hw) % KS of the
+    // workgroup's query block w / (hw KS): within every tile, part p takes
+    // the 32-key sub-tile p, and the parts' accumulators are combined at the
+    // end (KS > 1 puts 2 or 4 waves on one head and query block without
+    // staging any tile twice; QB > 1 puts QB blocks on the same tiles).
+    const int hidx = wave % hw, part = (wave / hw) % KS;
+    const int qsub = QB > 1 ? wave / (hw * KS) : 0;  // this wave's block of the workgroup's QB
     // Dispatch order: workgroups start in linear id order, so the id maps to
-    // (query block, key range, head part, item) with the query block most
+    // (query blocks, key range, head part, item) with the query blocks most
     // significant and the last blocks first. Without a window the last blocks
     // see the most keys: the longest workgroups start first and the grid's
     // tail is short ones.
@@ -2237,7 +2245,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int item = (lin / (nks * gridDim.y)) % gridDim.z;
     const int kvh = by / nhb, hkv = gridDim.y / nhb;
     const int g = a.group, hq = hkv * g;
-    const bool computes = wave < hw * KS;
+    const bool computes = wave < hw * KS * QB;
     const int head = kvh * g + (by % nhb) * hw + (computes ? hidx : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
@@ -2245,16 +2253,21 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     uint32_t pw;
     load_prefix(a.pmask, slot, lane, plen, pw);
     const int Qn = a.qn;
-    const int qrow0 = qb * 16;
+    const int qrow0 = (qb * QB + qsub) * 16;   // this wave's block
     const int base_pos = L - Qn;               // position of query row 0
     const int qr = qrow0 + col;                // this lane's query row (S^T / O^T column)
     const bool qvalid = computes && qr < Qn;
     const int pq = base_pos + qr;
     const int lo_q = a.window > 0 ? pq - a.window + 1 : 0;
-    // the block's keys: up to its last query, from its first query's window;
-    // with a key split, part ks of them in whole tiles
-    int kend = base_pos + min(Qn, qrow0 + 16);
-    int kstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
+    // the workgroup's keys: up to its last block's last query, from its first
+    // block's first query's window; with a key split, part ks of them in
+    // whole tiles
+    int kend = base_pos + min(Qn, (qb + 1) * QB * 16);
+    int kstart = a.window > 0 ? max(0, base_pos + qb * QB * 16 - a.window + 1) : 0;
+    // this wave's own block's keys (QB > 1: a step outside them is skipped)
+    const int wkend = base_pos + min(Qn, qrow0 + 16);
+    const int wkstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
+    const bool wlive = computes && qrow0 < Qn;
     if (nks > 1) {
         const int span = (kend - kstart + nks - 1) / nks;
         const int part = (span + kPfKeys - 1) / kPfKeys * kPfKeys;
@@ -2446,10 +2459,11 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             for (int j = issued; j < next; ++j) issue_tile(j);  // into group it - 1's stages
             issued = next;
             const int j = it * KS + part;  // this wave's tile (wave-uniform)
-            if (computes && j < ntiles) {
+            const int tj = kstart + j * kPfKeys;
+            if (wlive && j < ntiles && (QB == 1 || (tj < wkend && tj + kPfKeys > wkstart))) {
                 const int sb = (j % NS) * RSUB;
                 tile_core(
-                    kstart + j * kPfKeys,
+                    tj,
                     [&](int b, int c) __attribute__((always_inline)) {
                         const int kr = b ? kr1 : kr0, ksw = b ? ksw1 : ksw0;
                         return *reinterpret_cast<const uint4 *>(&sk[sb + kr * D + 8 * ((4 * c) ^ ksw)]);
@@ -2548,9 +2562,9 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         // bank conflicts; a [query][D] layout put the 16 queries of a half-wave
         // D * 4 B apart, on the same banks)
         float4 *xo = reinterpret_cast<float4 *>(sk);
-        float2 *xml = reinterpret_cast<float2 *>(sv);  // [(part - 1) * hw + hidx][16 queries]
+        float2 *xml = reinterpret_cast<float2 *>(sv);  // [((part - 1) * hw + hidx) * QB + qsub][16 queries]
         if (computes && part > 0) {
-            const int e = (part - 1) * hw + hidx;
+            const int e = ((part - 1) * hw + hidx) * QB + qsub;
             float4 *dst = xo + (int64_t)e * (D / 16) * 64 + lane;
 #pragma unroll
             for (int b = 0; b < D / 16; ++b) dst[64 * b] = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
@@ -2560,14 +2574,14 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         if (!computes || part > 0) return;
         float M = m;
 #pragma unroll
-        for (int q = 1; q < KS; ++q) M = fmaxf(M, xml[((q - 1) * hw + hidx) * 16 + col].x);
+        for (int q = 1; q < KS; ++q) M = fmaxf(M, xml[(((q - 1) * hw + hidx) * QB + qsub) * 16 + col].x);
         const float w0 = __builtin_amdgcn_exp2f(m - M);
         l *= w0;
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) o[b] *= w0;
 #pragma unroll
         for (int q = 1; q < KS; ++q) {
-            const int e = (q - 1) * hw + hidx;
+            const int e = ((q - 1) * hw + hidx) * QB + qsub;
             const float2 ml = xml[e * 16 + col];
             const float w = __builtin_amdgcn_exp2f(ml.x - M);
             l = fmaf(ml.y, w, l);
@@ -3016,24 +3030,25 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     if (a.n_ksplit < 1 || (a.n_ksplit > 1 && (!a.part_o || !a.part_ml))) return hipErrorInvalidValue;
     const int ks = a.key_parts;
     if ((ks != 1 && ks != 2 && ks != 4) || ks > prefill_max_parts(head_dim) || hw * ks > 8) return hipErrorInvalidValue;
+    if (a.q_blocks != 1 && !(a.q_blocks == 2 && a.ring_groups)) return hipErrorInvalidValue;
     if (a.kv.layout == KVRT_LAYOUT_RING && a.kv.rows < kPfKeys * ks) return hipErrorInvalidValue;  // one wrap per tile
     if (a.ring_groups) {
-        // DMA ring: hw * ks waves (at least 2), every one computing
-        const int g = a.ring_groups;
-        if (!prefill_ring_ok(head_dim, a.kv.layout, ks, g) || hw * ks > 8) return hipErrorInvalidValue;
-        dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
-        const int nw = hw * ks < 2 ? 2 : hw * ks;
-        auto ring = [&](auto d_c, auto ks_c) -> hipError_t {
-            constexpr int HD = decltype(d_c)::value, KS = decltype(ks_c)::value;
+        // DMA ring: hw * ks * qb waves (at least 2), every one computing
+        const int g = a.ring_groups, qbk = a.q_blocks;
+        if (!prefill_ring_ok(head_dim, a.kv.layout, ks, g, qbk) || hw * ks * qbk > 8) return hipErrorInvalidValue;
+        dim3 grid((a.qn + 16 * qbk - 1) / (16 * qbk) * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
+        const int nw = hw * ks * qbk < 2 ? 2 : hw * ks * qbk;
+        auto ring = [&](auto d_c, auto ks_c, auto qb_c) -> hipError_t {
+            constexpr int HD = decltype(d_c)::value, KS = decltype(ks_c)::value, QB = decltype(qb_c)::value;
             constexpr int G = kPfRingGroups;
             auto go = [&](auto nw_c) {
                 constexpr int NW = decltype(nw_c)::value;
                 if (a.kv.layout == KVRT_LAYOUT_RING)
-                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_RING, NW, true, KS, G>), grid, dim3(64 * NW),
-                                       0, s, a);
+                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_RING, NW, true, KS, G, QB>), grid,
+                                       dim3(64 * NW), 0, s, a);
                 else
-                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_CONTIG, NW, true, KS, G>), grid, dim3(64 * NW),
-                                       0, s, a);
+                    hipLaunchKernelGGL((prefill_kernel<HD, KVRT_LAYOUT_CONTIG, NW, true, KS, G, QB>), grid,
+                                       dim3(64 * NW), 0, s, a);
             };
             if (nw == 2) go(std::integral_constant<int, 2>{});
             else if (nw == 4) go(std::integral_constant<int, 4>{});
@@ -3042,11 +3057,12 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
         };
         using C128 = std::integral_constant<int, 128>;
         using C256 = std::integral_constant<int, 256>;
-        using K1 = std::integral_constant<int, 1>;
-        using K2 = std::integral_constant<int, 2>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
         hipError_t e;
-        if (head_dim == 256) e = ks == 1 ? ring(C256{}, K1{}) : ring(C256{}, K2{});
-        else e = ks == 1 ? ring(C128{}, K1{}) : ring(C128{}, K2{});
+        if (qbk == 2) e = ks == 1 ? ring(C128{}, I1{}, I2{}) : ring(C128{}, I2{}, I2{});
+        else if (head_dim == 256) e = ks == 1 ? ring(C256{}, I1{}, I1{}) : ring(C256{}, I2{}, I1{});
+        else e = ks == 1 ? ring(C128{}, I1{}, I1{}) : ring(C128{}, I2{}, I1{});
         if (e != hipSuccess || a.n_ksplit == 1) return e;
         const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
         hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim,

@@ -2021,6 +2021,23 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     if ((ring_env > 0 || (ring_env < 0 && ring_default)) && prefill_ring_ok(D, s.layout, parts, kPfRingGroups) &&
         (s.layout != KVRT_LAYOUT_RING || s.ring_rows >= kPfKeys))
         a.ring_groups = kPfRingGroups;
+    // Talker-sized grids (>= 512 workgroups) on the ring at head_dim 128: two
+    // 16-query blocks per workgroup share its staged tiles, and with the LDS
+    // and waves this frees each block's keys go to two waves (talker Q 512:
+    // 22.1 -> 21.3 us; pairs with one key part 21.2 -> 22.2 us on another
+    // box, four key parts without pairs 40.0 us). KVRT_PF_QBLOCKS = 1 / 2
+    // forces single blocks / pairs; KVRT_PF_KEY_PARTS sets the parts.
+    static const int qblocks_env = env_int("KVRT_PF_QBLOCKS", 0);
+    a.q_blocks = 1;
+    if (a.ring_groups && (qblocks_env == 2 || (qblocks_env == 0 && wgs_grid >= 512))) {
+        int p2 = parts_env > 0 ? parts : 2;
+        while (p2 > 1 && (hw * p2 * 2 > 8 || (s.layout == KVRT_LAYOUT_RING && s.ring_rows < kPfKeys * p2))) p2 /= 2;
+        if (hw * p2 * 2 <= 8 && prefill_ring_ok(D, s.layout, p2, a.ring_groups, 2)) {
+            a.q_blocks = 2;
+            parts = p2;
+            a.key_parts = parts;
+        }
+    }
     // Key split: when the query blocks give fewer than 128 workgroups (a short
     // chunk over a long context: thinker full layers, Q 291 over 2048 keys,
     // 76 workgroups on 256 CUs), each block's keys are cut into n_ksplit

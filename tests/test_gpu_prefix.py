@@ -174,6 +174,37 @@ def test_prefix_mask_prefill_parity(d, layout, qn, plen):
     assert rt.health() == 0
 
 
+def test_prefix_mask_talker_sized_prefill_parity():
+    """Prefix masks on a talker-sized prefill grid (head_dim 128, >= 512
+    workgroups: pairs of 16-query blocks share a workgroup's tiles, each
+    block's keys over two waves): ragged prefixes around the mask lengths, one
+    stream without a mask."""
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(128)
+    hq, hkv, d, qn = 16, 8, 128, 300
+    rt = KVRuntime([LayerSpec(kv_heads=hkv, head_dim=d)], 4, 1200, max_q=qn, device="cuda")
+    orc = O.OracleCache([O.OracleLayer(hkv, d)], 4)
+    masks = [_mask("canonical", 34, gen), _mask("random", 512, gen), _mask("random", 120, gen), None]
+    for s, (n, m) in enumerate(zip((34, 600, 150, 90), masks)):
+        k, v = randn_bf16(gen, (1, hkv, n, d)), randn_bf16(gen, (1, hkv, n, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+        if m is not None:
+            rt.set_prefix_attention(s, torch.from_numpy(m).cuda())
+            orc.set_prefix_attention(s, m)
+    k, v = randn_bf16(gen, (4, hkv, qn, d)), randn_bf16(gen, (4, hkv, qn, d))
+    rt.append(0, k.cuda(), v.cuda(), [0, 1, 2, 3])
+    q = randn_bf16(gen, (4, hq, qn, d), 1.0 / math.sqrt(d))
+    out = rt.attend_prefill(0, q.cuda(), [0, 1, 2, 3], 1.0)
+    torch.cuda.synchronize()
+    for s in range(4):
+        orc.append(s, 0, to_np(k[s]), to_np(v[s]))
+        ref = orc.attend(s, 0, to_np(q[s]), 1.0)
+        assert float(np.abs(to_np(out[s]) - ref).max()) <= ATOL, s
+    assert rt.health() == 0
+
+
 def test_prefix_mask_on_the_padded_tensor_path():
     from kvrt import attend_padded, gather
     from kvrt import KVRTCache, KVRuntime, LayerSpec

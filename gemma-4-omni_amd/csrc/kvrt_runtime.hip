@@ -273,10 +273,11 @@ bool use_mfma_decode(int mode, int dtype, int rows_tile_, int head_dim, int64_t 
     if (mode == KVRT_DECODE_VALU) return false;
     // int8 (PAGED): AUTO keeps the VALU kernel. A forced MFMA decode runs
     // the int8 ring kernel at head_dim 64 / 128 (i8_mfma_dma), the register-
-    // staged MFMA tiles elsewhere. At config 5 the ring kernel matches the
-    // VALU kernel per launch (29.0 vs 28.0 us, fused 32.2 vs 31.7) with a
-    // third of its VALU instructions, and runs the step slower (0.838 vs
-    // 0.808 ms); KVRT_I8_MFMA=1 lets AUTO take it.
+    // staged MFMA tiles elsewhere. At config 5's layer the ring kernel runs
+    // about as long as the VALU kernel (fused append + attend 31.7 vs 29.2
+    // us) with a third of its VALU instructions, and the step slower (0.838
+    // vs 0.808 ms when both quantised the new rows twice); KVRT_I8_MFMA=1
+    // lets AUTO take it.
     if (dtype == KVRT_INT8) {
         static const char *env = std::getenv("KVRT_I8_MFMA");
         static const bool ring = env && std::atoi(env) != 0;
@@ -2024,9 +2025,9 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     // Talker-sized grids (>= 512 workgroups) on the ring at head_dim 128: two
     // 16-query blocks per workgroup share its staged tiles, and with the LDS
     // and waves this frees each block's keys go to two waves (talker Q 512:
-    // 22.1 -> 21.3 us; pairs with one key part 21.2 -> 22.2 us on another
-    // box, four key parts without pairs 40.0 us). KVRT_PF_QBLOCKS = 1 / 2
-    // forces single blocks / pairs; KVRT_PF_KEY_PARTS sets the parts.
+    // 22.1 -> 21.3 us; pairs with one key part were 2-5% faster than single
+    // blocks, four key parts without pairs took 40.0 us). KVRT_PF_QBLOCKS =
+    // 1 / 2 forces single blocks / pairs; KVRT_PF_KEY_PARTS sets the parts.
     static const int qblocks_env = env_int("KVRT_PF_QBLOCKS", 0);
     a.q_blocks = 1;
     if (a.ring_groups && (qblocks_env == 2 || (qblocks_env == 0 && wgs_grid >= 512))) {

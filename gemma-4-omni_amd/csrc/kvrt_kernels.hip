@@ -2064,11 +2064,12 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // chunked-prefill attention (MFMA)
 // ---------------------------------------------------------------------------
-// grid (ceil(Q / 16), kv_heads * g / hw, n_items), 64 * NW threads with NW =
-// 4 or 8 >= hw: workgroup (x, y) serves the hw q heads
-// kvh*g + (y % (g/hw))*hw + j (wave j < hw) over the 16 query rows of block x
-// (on the DMA ring with QB = 2: x over ceil(Q / 32) pairs of blocks, waves
-// hw .. 2 hw - 1 on the second block of the pair);
+// grid (n_ksplit * kv_heads * g / hw, n_items, ceil(Q / 16)), 64 * NW
+// threads with NW = 4 or 8 >= hw: workgroup (x, y, z) serves key range
+// x % n_ksplit of the hw q heads kvh*g + (b % (g/hw))*hw + j (wave j < hw,
+// b = x / n_ksplit, kvh = b / (g/hw)) of item y over the 16 query rows of
+// block ceil(Q / 16) - 1 - z (on the DMA ring with QB = 2: z over ceil(Q / 32)
+// pairs of blocks, waves hw .. 2 hw - 1 on the second block of the pair);
 // all NW waves stage each 32-key K/V tile into LDS (K row-major, V
 // transposed) and the hw computing waves share it. With PF the next tile's
 // global loads are issued into registers before the current tile is
@@ -2192,6 +2193,18 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
     });
 }
 
+// q = x / d and r = x % d for wave-uniform x >= 0 and d > 0: a shift and a
+// mask when d is a power of two (a uniform branch), else the division.
+__device__ __forceinline__ void udivmod_uniform(int x, int d, int &q, int &r) {
+    if ((d & (d - 1)) == 0) {
+        q = x >> __builtin_ctz((unsigned)d);
+        r = x & (d - 1);
+    } else {
+        q = x / d;
+        r = x - q * d;
+    }
+}
+
 template <int D, int LAYOUT, int NW, bool PF, int KS, int G = 0, int QB = 1>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     constexpr int KP = pf_pitch<D>();  // K / V tile row pitch (bf16)
@@ -2220,33 +2233,35 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     static_assert((KS - 1) * (NW / KS) * 16 * 8 <= LDS_ELEMS * 2, "part (m, l) fit LDS");
     __shared__ __align__(16) uint16_t sk[LDS_ELEMS];
     __shared__ __align__(16) uint16_t sv[LDS_ELEMS];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, grp = lane >> 4;
-    const int hw = a.heads_per_wg, nhb = a.group / hw;
+    const int hw = a.heads_per_wg;
+    int nhb, rem;
+    udivmod_uniform(a.group, hw, nhb, rem);
     // Wave w computes head w % hw over key part (w / hw) % KS of the
     // workgroup's query block w / (hw KS): within every tile, part p takes
     // the 32-key sub-tile p, and the parts' accumulators are combined at the
     // end (KS > 1 puts 2 or 4 waves on one head and query block without
     // staging any tile twice; QB > 1 puts QB blocks on the same tiles).
-    const int hidx = wave % hw, part = (wave / hw) % KS;
-    const int qsub = QB > 1 ? wave / (hw * KS) : 0;  // this wave's block of the workgroup's QB
-    // Dispatch order: workgroups start in linear id order, so the id maps to
-    // (query blocks, key range, head part, item) with the query blocks most
-    // significant and the last blocks first. Without a window the last blocks
-    // see the most keys: the longest workgroups start first and the grid's
-    // tail is short ones.
+    int hidx, wrest;
+    udivmod_uniform(wave, hw, wrest, hidx);
+    const int part = KS > 1 ? wrest % KS : 0;
+    const int qsub = QB > 1 ? wrest / KS : 0;  // this wave's block of the workgroup's QB
+    // Grid (head part x key range, item, query blocks): workgroups start in
+    // linear id order, so the query blocks are the most significant and run
+    // last blocks first. Without a window the last blocks see the most keys:
+    // the longest workgroups start first and the grid's tail is short ones.
     const int nks = a.n_ksplit;
-    const int nqb = gridDim.x / nks;
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int per_qb = nks * gridDim.y * gridDim.z;
-    const int qb = nqb - 1 - lin / per_qb;
-    const int ks = lin % nks;
-    const int by = (lin / nks) % gridDim.y;
-    const int item = (lin / (nks * gridDim.y)) % gridDim.z;
-    const int kvh = by / nhb, hkv = gridDim.y / nhb;
+    int by, ks;
+    udivmod_uniform(blockIdx.x, nks, by, ks);
+    const int item = blockIdx.y;
+    const int qb = gridDim.z - 1 - blockIdx.z;
+    int kvh, hb;
+    udivmod_uniform(by, nhb, kvh, hb);
+    const int hkv = a.kv.kv_heads;
     const int g = a.group, hq = hkv * g;
     const bool computes = wave < hw * KS * QB;
-    const int head = kvh * g + (by % nhb) * hw + (computes ? hidx : 0);
+    const int head = kvh * g + hb * hw + (computes ? hidx : 0);
     const int slot = a.slots[item];
     const int L = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     int plen;  // prefix-attention mask of the slot
@@ -3036,7 +3051,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
         // DMA ring: hw * ks * qb waves (at least 2), every one computing
         const int g = a.ring_groups, qbk = a.q_blocks;
         if (!prefill_ring_ok(head_dim, a.kv.layout, ks, g, qbk) || hw * ks * qbk > 8) return hipErrorInvalidValue;
-        dim3 grid((a.qn + 16 * qbk - 1) / (16 * qbk) * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
+        dim3 grid(a.n_ksplit * a.kv.kv_heads * (a.group / hw), a.n_items, (a.qn + 16 * qbk - 1) / (16 * qbk));
         const int nw = hw * ks * qbk < 2 ? 2 : hw * ks * qbk;
         auto ring = [&](auto d_c, auto ks_c, auto qb_c) -> hipError_t {
             constexpr int HD = decltype(d_c)::value, KS = decltype(ks_c)::value, QB = decltype(qb_c)::value;
@@ -3069,7 +3084,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
                            outs);
         return hipGetLastError();
     }
-    dim3 grid((a.qn + 15) / 16 * a.n_ksplit, a.kv.kv_heads * (a.group / hw), a.n_items);
+    dim3 grid(a.n_ksplit * a.kv.kv_heads * (a.group / hw), a.n_items, (a.qn + 15) / 16);
     // 4 or 8 waves (hw * ks compute); D = 512 keeps no tile in flight across
     // the MFMAs (registers)
     const bool w8 = hw * ks > 4;

@@ -2366,13 +2366,15 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                 tmax = fmaxf(tmax, sc[j]);
             }
         } else {
+            // bit j of vis8: key k0 + j lies in [klo, khi] and passes the
+            // prefix mask; one bit test per key
             const int k0 = t0 + 8 * grp;
-            const uint32_t pvis = t0 < plen ? prefix_bits8(pw, k0, plen) : 0xffu;  // bit j: key k0 + j
+            const uint32_t pvis = t0 < plen ? prefix_bits8(pw, k0, plen) : 0xffu;
+            const int nhi = min(max(khi - k0 + 1, 0), 8), nlo = min(max(klo - k0, 0), 8);
+            const uint32_t vis8 = ((1u << nhi) - 1u) & ~((1u << nlo) - 1u) & pvis;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int key = k0 + j;
-                const bool vis = (key <= khi) & (key >= klo) & (((pvis >> j) & 1u) != 0);
-                sc[j] = vis ? (j < 4 ? s[0][j] : s[1][j - 4]) * a.scale_log2 : -INFINITY;
+                sc[j] = (vis8 & (1u << j)) != 0 ? (j < 4 ? s[0][j] : s[1][j - 4]) * a.scale_log2 : -INFINITY;
                 tmax = fmaxf(tmax, sc[j]);
             }
         }

@@ -85,6 +85,11 @@ def _check(rt, orc, q, scale, prefill=True):
         # over ragged prefixes, and a windowed ring layout
         (16, 8, 128, 0, "contig", [0, 37, 300, 5], 481),
         (16, 8, 128, 200, "ring", [0, 900, 64, 10], 300),
+        # GQA groups of 6 and 3 (3 q heads per workgroup: the index splits
+        # by a divisor that is not a power of two)
+        (6, 1, 128, 0, "contig", [100, 37], 50),
+        (12, 2, 256, 512, "ring", [300], 40),
+        (3, 1, 64, 0, "paged", [70], 33),
     ],
 )
 def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):

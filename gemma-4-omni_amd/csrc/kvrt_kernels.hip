@@ -92,6 +92,23 @@ __device__ __forceinline__ uint32_t prefix_bits8(uint32_t pw, int k0, int plen) 
 }
 
 
+// q = x / d and r = x % d for x >= 0 and a wave-uniform d > 0: a shift and a
+// mask when d is a power of two (a uniform branch), else the division.
+__device__ __forceinline__ void udivmod_uniform(int x, int d, int &q, int &r) {
+    if ((d & (d - 1)) == 0) {
+        q = x >> __builtin_ctz((unsigned)d);
+        r = x & (d - 1);
+    } else {
+        q = x / d;
+        r = x - q * d;
+    }
+}
+__device__ __forceinline__ int umod_uniform(int x, int d) {
+    int q, r;
+    udivmod_uniform(x, d, q, r);
+    return r;
+}
+
 // A wave's window of page-table entries: lane i holds the entry of logical
 // page win0 + i of the slot (-1 past the table).
 __device__ __forceinline__ int load_page_window(const KVView &v, int slot, int win0, int lane) {
@@ -565,8 +582,8 @@ __device__ __forceinline__ void decode_merge_tail(const DecodeArgs &a, int item,
                 m = load_agent(ml + (int64_t)sp * R);
                 v = load_agent(acc + (int64_t)sp * R * D);
             }, M, L, O);
-            const int jh = r / Qn, i = r % Qn;
-            a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
+            // row r is q head kvh*g + r / Qn, query r % Qn
+            a.out[(((int64_t)item * hkv * a.group + kvh * a.group) * Qn + r) * D + d] =
                 f32_to_bf16(L > 0.f ? O / L : 0.f);
         }
     } else {
@@ -615,8 +632,8 @@ __device__ __forceinline__ void decode_merge_tail(const DecodeArgs &a, int item,
                     }
                 }
             }
-            const int jh = r / Qn, i = r % Qn;
-            const int64_t orow = (((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D;
+            // row r is q head kvh*g + r / Qn, query r % Qn
+            const int64_t orow = (((int64_t)item * hkv * a.group + kvh * a.group) * Qn + r) * D;
             uint32_t *dst = reinterpret_cast<uint32_t *>(a.out + orow) + j;
 #pragma unroll
             for (int h = 0; h < EPT / 2; ++h)
@@ -798,7 +815,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
         const int base_hi = max(t.prefix_pos, t.prefix_start - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const bool audio = (r % Qn) == Qn - 1;
+            const bool audio = umod_uniform(r, Qn) == Qn - 1;
             lo[r] = 0;
             hi[r] = r >= rows ? -1 : (audio && t.mode == 1 ? t.prefix_start - 1 : base_hi);
             alo[r] = r < rows && audio ? t.audio_start : 0x7fffffff;
@@ -808,7 +825,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int p = p0 + (r % Qn);
+            const int p = p0 + umod_uniform(r, Qn);
             hi[r] = r < rows ? p : -1;
             lo[r] = a.window > 0 ? p - a.window + 1 : 0;
             alo[r] = 0x7fffffff;
@@ -893,8 +910,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
             const int e = t * 64 + lane;
             int r = e / LPR;
             r = r < rows ? r : 0;
-            const int j = r / Qn, i = r % Qn;
-            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + j) * Qn + i) * D + (e % LPR) * VEC;
+            const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group) * Qn + r) * D + (e % LPR) * VEC;
             dma_load16(qp, __builtin_amdgcn_readfirstlane(ring + t * 1024));
         }
         const int pro = min(STG, npass);
@@ -1409,16 +1425,17 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     if constexpr (!DMA) {
         // every lane loads (rows past the tile's real rows read row 0), then
         // those lanes zero their operand: no branch around the loads
-        const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
-        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D;
+        // row col is q head kvh*g + col / Qn, query col % Qn
+        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group) * Qn + (rvalid ? col : 0)) * D;
 #pragma unroll
         for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + kdim(c));
 #pragma unroll
         for (int c = 0; c < D / 32; ++c)
             if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
     }
-    const int hi = rvalid ? p0 + col % Qn : -1;
-    const int lo = a.window > 0 ? p0 + col % Qn - a.window + 1 : 0;
+    const int cq = umod_uniform(col, Qn);  // this column's query
+    const int hi = rvalid ? p0 + cq : -1;
+    const int lo = a.window > 0 ? p0 + cq - a.window + 1 : 0;
     float m = kNegBig, l = 0.f;  // running max (uniform per column) and this lane's partial sum
     f32x4_t o[D / 16];
 #pragma unroll
@@ -1657,7 +1674,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
                 const int row = RPI * i + lane / CPR;
                 const int lc = (lane % CPR) ^ mfma_dswz(row);
                 const int rq = row < rows ? row : 0;
-                const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + rq / Qn) * Qn + rq % Qn) * D;
+                const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group) * Qn + rq) * D;
                 dma_load16(qp + 8 * lc, __builtin_amdgcn_readfirstlane(ring + i * 1024));
             }
         }
@@ -1822,16 +1839,17 @@ __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     const bool rvalid = col < rows;
     uint4 qop[D / 32];
     {
-        const int jh = rvalid ? col / Qn : 0, qi = rvalid ? col % Qn : 0;
-        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group + jh) * Qn + qi) * D + 8 * grp;
+        // row col is q head kvh*g + col / Qn, query col % Qn
+        const uint16_t *qp = a.q + (((int64_t)item * hq + kvh * a.group) * Qn + (rvalid ? col : 0)) * D + 8 * grp;
 #pragma unroll
         for (int c = 0; c < D / 32; ++c) qop[c] = *reinterpret_cast<const uint4 *>(qp + 32 * c);
 #pragma unroll
         for (int c = 0; c < D / 32; ++c)
             if (!rvalid) qop[c] = make_uint4(0, 0, 0, 0);
     }
-    const int hi = rvalid ? p0 + col % Qn : -1;
-    const int lo = a.window > 0 ? p0 + col % Qn - a.window + 1 : 0;
+    const int cq = umod_uniform(col, Qn);  // this column's query
+    const int hi = rvalid ? p0 + cq : -1;
+    const int lo = a.window > 0 ? p0 + cq - a.window + 1 : 0;
 
     // unit swizzles: K reads take units 2c + g2 of the 16 keys kperm(kb, i),
     // V^T reads unit b of 32 keys
@@ -2053,8 +2071,8 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
         O = group_sum<G>(O * w);
     }
     if (live && j == 0) {
-        const int jh = r / Qn, i = r % Qn;
-        a.out[(((int64_t)item * hkv * a.group + kvh * a.group + jh) * Qn + i) * D + d] =
+        // row r is q head kvh*g + r / Qn, query r % Qn
+        a.out[(((int64_t)item * hkv * a.group + kvh * a.group) * Qn + r) * D + d] =
             f32_to_bf16(L > 0.f ? O / L : 0.f);
     }
     if (a.advance && kvh == 0 && blockIdx.z == 0 && threadIdx.x == 0)
@@ -2191,18 +2209,6 @@ __device__ __forceinline__ void pf_stage(uint16_t *sk, uint16_t *sv, const u32x4
         constexpr int u = decltype(uc)::value;
         pf_stage_unit<D, TK, EXACT>(sk, sv, threadIdx.x + u * NT, kreg[u], vreg[u]);
     });
-}
-
-// q = x / d and r = x % d for wave-uniform x >= 0 and d > 0: a shift and a
-// mask when d is a power of two (a uniform branch), else the division.
-__device__ __forceinline__ void udivmod_uniform(int x, int d, int &q, int &r) {
-    if ((d & (d - 1)) == 0) {
-        q = x >> __builtin_ctz((unsigned)d);
-        r = x & (d - 1);
-    } else {
-        q = x / d;
-        r = x - q * d;
-    }
 }
 
 template <int D, int LAYOUT, int NW, bool PF, int KS, int G = 0, int QB = 1>

@@ -1367,6 +1367,12 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const int kvh = blockIdx.y, hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
+    // The scalar arguments of the set-up, loaded in one batch with the slot
+    // (one round trip) rather than each at its first use
+    asm volatile("" ::"s"(a.qn), "s"(a.group), "s"(a.window), "s"(a.n_split), "s"(a.k_new), "s"(a.v_new),
+                 "s"(a.kv.rows), "s"(a.pmask), "s"(a.q), "s"(a.kv.k), "s"(a.kv.v), "s"(a.kv.slot_stride),
+                 "s"(a.kv.head_stride), "s"(a.len.lens), "s"(a.len.stride), "s"(a.len.offset), "s"(a.err),
+                 "s"(a.n_upd), "s"(slot));
     const int len = a.len.lens[(int64_t)slot * a.len.stride + a.len.offset];
     // Prefix-attention mask of the slot. PAGED rows at D 512 use every
     // register: launches with masks run that shape on decode_kernel instead

@@ -92,6 +92,15 @@ __device__ __forceinline__ uint32_t prefix_bits8(uint32_t pw, int k0, int plen) 
 }
 
 
+// Item of grid z-index z of a PAGED decode: order[] read as aligned words
+// through the scalar cache (a byte read is a vector load: one more memory
+// round trip ahead of the slot and length loads).
+static_assert(offsetof(DecodeArgs, order) % 4 == 0 && kMaxItems % 4 == 0, "order[] in whole words");
+__device__ __forceinline__ int launch_item(const DecodeArgs &a, int z) {
+    const uint32_t w = reinterpret_cast<const uint32_t *>(a.order)[z >> 2];
+    return (int)((w >> (8 * (z & 3))) & 0xffu);
+}
+
 // q = x / d and r = x % d for x >= 0 and a wave-uniform d > 0: a shift and a
 // mask when d is a power of two (a uniform branch), else the division.
 __device__ __forceinline__ void udivmod_uniform(int x, int d, int &q, int &r) {
@@ -704,7 +713,7 @@ __global__ __launch_bounds__(256) void decode_kernel(Args a) {
     // grid ends on short ones; other layouts keep z (the indirection is a
     // dependent argument load ahead of every workgroup's first load: +1 % on
     // the north-star step, whose items are equally long)
-    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? a.order[blockIdx.z] : (int)blockIdx.z;
+    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? launch_item(a, blockIdx.z) : (int)blockIdx.z;
     const int kvh = blockIdx.y;
     const int hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
@@ -1363,7 +1372,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     uint16_t *sv_all = reinterpret_cast<uint16_t *>(lds_raw);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? a.order[blockIdx.z] : (int)blockIdx.z;
+    const int item = LAYOUT == KVRT_LAYOUT_PAGED ? launch_item(a, blockIdx.z) : (int)blockIdx.z;
     const int kvh = blockIdx.y, hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];
@@ -1815,7 +1824,7 @@ __global__ __launch_bounds__(256) void decode_i8_mfma_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, grp = lane >> 4;
-    const int item = a.order[blockIdx.z];
+    const int item = launch_item(a, blockIdx.z);
     const int kvh = blockIdx.y, hkv = gridDim.y;
     const int split = blockIdx.x * kWaves + wave;
     const int slot = a.slots[item];

@@ -97,7 +97,8 @@ __device__ __forceinline__ uint32_t prefix_bits8(uint32_t pw, int k0, int plen) 
 // round trip ahead of the slot and length loads).
 static_assert(offsetof(DecodeArgs, order) % 4 == 0 && kMaxItems % 4 == 0, "order[] in whole words");
 __device__ __forceinline__ int launch_item(const DecodeArgs &a, int z) {
-    const uint32_t w = reinterpret_cast<const uint32_t *>(a.order)[z >> 2];
+    uint32_t w;
+    __builtin_memcpy(&w, a.order + 4 * (z >> 2), 4);
     return (int)((w >> (8 * (z & 3))) & 0xffu);
 }
 

@@ -1,0 +1,86 @@
+"""GPU parity of fused append + decode attention against the fp64 oracle over
+seeded random layer shapes: head_dim 64 / 128 / 256, CONTIG / RING / PAGED,
+bf16 and (PAGED) int8, 1..8 KV heads, GQA groups 1..8, Q 1 / 2, 1..4 ragged
+streams of 1..4000 positions, with and without a window, on the AUTO, VALU and
+MFMA decode kernels. Max-abs 1e-2, as every attention test."""
+from __future__ import annotations
+
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from tests.helpers import randn_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+ATOL = 1e-2
+
+
+def _cases(n_cases: int, seed: int, max_len: int) -> list[tuple]:
+    r = random.Random(seed)
+    out = []
+    while len(out) < n_cases:
+        d = r.choice([64, 128, 256])
+        layout = r.choice(["contig", "ring", "paged"])
+        dtype = "int8" if layout == "paged" and r.random() < 0.5 else "bf16"
+        hkv, g, qn = r.choice([1, 2, 4, 8]), r.choice([1, 2, 4, 8]), r.choice([1, 2])
+        if g * qn > 16 or (dtype == "int8" and g * qn > 8):
+            continue
+        kernel = r.choice(["auto", "valu", "mfma"])
+        if layout == "ring":
+            window = r.choice([64, 200])
+        elif layout == "paged":
+            window = r.choice([0, 0, 300])
+        else:
+            window = r.choice([0, 0, 128])
+        lens = tuple(r.randint(1, max_len) for _ in range(r.choice([1, 2, 3, 4])))
+        out.append((d, layout, dtype, hkv, g, qn, kernel, window, lens))
+    return out
+
+
+# short streams, and streams long enough for many workgroups per (stream,
+# head) and the LDS DMA rings (>= 2048 keys)
+CASES = _cases(24, 2024, 700) + _cases(16, 7, 4000)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[
+    f"d{c[0]}-{c[1]}-{c[2]}-h{c[3]}g{c[4]}q{c[5]}-{c[6]}-w{c[7]}-n{len(c[8])}" for c in CASES])
+def test_random_shape_fused_decode_parity(case):
+    from kvrt import KVRuntime, LayerSpec
+
+    d, layout, dtype, hkv, g, qn, kernel, window, lens = case
+    gen = torch.Generator().manual_seed(d * 1000 + hkv * 100 + g * 10 + qn + sum(lens))
+    n = len(lens)
+    cap = max(lens) + 3 * qn + 8
+    kw = {}
+    if layout == "ring":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="ring", window=window, ring_rows=window + qn + 2)
+    elif layout == "paged":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="paged", window=window, dtype=dtype)
+        kw = dict(block_size=16, pool_pages=n * ((cap + 15) // 16) + 8, pool_seed=5)
+    else:
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, window=window)
+    rt = KVRuntime([spec], n, cap, max_q=qn, decode_kernel=kernel, device="cuda", **kw)
+    orc = O.OracleCache([O.OracleLayer(hkv, d, window, dtype == "int8")], n)
+    for s, length in enumerate(lens):
+        k, v = randn_bf16(gen, (1, hkv, length, d)), randn_bf16(gen, (1, hkv, length, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    slots = list(range(n))
+    scale = 1.0 / math.sqrt(d)
+    worst = 0.0
+    for _ in range(3):
+        q = randn_bf16(gen, (n, hkv * g, qn, d), 0.5)
+        k, v = randn_bf16(gen, (n, hkv, qn, d), 0.5), randn_bf16(gen, (n, hkv, qn, d), 0.5)
+        out = rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), slots, scale)
+        torch.cuda.synchronize()
+        for i in slots:
+            orc.append(i, 0, to_np(k[i]), to_np(v[i]))
+            ref = orc.attend(i, 0, to_np(q[i]), scale)
+            worst = max(worst, float(np.abs(to_np(out[i]) - ref).max()))
+    assert worst <= ATOL, worst
+    assert rt.health() == 0
+    rt.close()

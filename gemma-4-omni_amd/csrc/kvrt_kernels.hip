@@ -2136,40 +2136,40 @@ struct StaticFor {
 
 // Tile units: unit c = (row c / (D/8), 16 B segment c % (D/8)) of both the
 // K and the V tile, both staged row-major. Keys at or past kend read row
-// kstart (masked in the softmax).
+// kclamp (a key of the cache, masked in the softmax).
 // Element offset of row kr of the tile at t0 (key t0 + kr; keys at or past
-// kend read row kstart, masked in the softmax).
+// kend read row kclamp).
 template <int D, int LAYOUT>
-__device__ __forceinline__ int64_t pf_row_offset(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend,
+__device__ __forceinline__ int64_t pf_row_offset(const KVView &kv, int slot, int kvh, int t0, int kclamp, int kend,
                                                  int kr, bool &bad) {
     const int key = t0 + kr;
     if constexpr (LAYOUT == KVRT_LAYOUT_CONTIG) {
         // one multiply-add per row from the (slot, head) base
         const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
-        return base + (int64_t)(key < kend ? key : kstart) * D;
+        return base + (int64_t)(key < kend ? key : kclamp) * D;
     } else if constexpr (LAYOUT == KVRT_LAYOUT_RING) {
         // t0 % rows once per tile: rows of the tile wrap at most once
         const int64_t base = (int64_t)slot * kv.slot_stride + (int64_t)kvh * kv.head_stride;
-        const int r0 = t0 % kv.rows, rs = kstart % kv.rows;
+        const int r0 = t0 % kv.rows, rs = kclamp % kv.rows;
         int rk = r0 + kr;
         rk = rk >= kv.rows ? rk - kv.rows : rk;
         return base + (int64_t)(key < kend ? rk : rs) * D;
     } else {
-        const int64_t off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kstart, D);
+        const int64_t off = row_offset<LAYOUT>(kv, slot, kvh, key < kend ? key : kclamp, D);
         bad |= off < 0;
         return off < 0 ? 0 : off;
     }
 }
 
 template <int D, int LAYOUT, int TK>
-__device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend, int c,
+__device__ __forceinline__ void pf_fetch_unit(const KVView &kv, int slot, int kvh, int t0, int kclamp, int kend, int c,
                                               u32x4_t &kx, u32x4_t &vx, bool &bad) {
     constexpr int UNITS = TK * (D / 8);
     const uint16_t *kg = static_cast<const uint16_t *>(kv.k);
     const uint16_t *vg = static_cast<const uint16_t *>(kv.v);
     const int cc = c < UNITS ? c : 0;
     const int kr = cc / (D / 8), ks = cc % (D / 8);
-    const int64_t off = pf_row_offset<D, LAYOUT>(kv, slot, kvh, t0, kstart, kend, kr, bad);
+    const int64_t off = pf_row_offset<D, LAYOUT>(kv, slot, kvh, t0, kclamp, kend, kr, bad);
     kx = *reinterpret_cast<const u32x4_t *>(kg + off + 8 * ks);
     vx = *reinterpret_cast<const u32x4_t *>(vg + off + 8 * ks);
 }
@@ -2210,11 +2210,11 @@ __device__ __forceinline__ void pf_stage_unit(uint16_t *sk, uint16_t *sv, int c,
 // A whole tile of TK keys, KU units per thread: unit u of thread t is
 // c = t + u * blockDim (the rows of a tile of KS sub-tiles are consecutive).
 template <int D, int LAYOUT, int TK, int KU, int NT>
-__device__ __forceinline__ void pf_fetch(const KVView &kv, int slot, int kvh, int t0, int kstart, int kend,
+__device__ __forceinline__ void pf_fetch(const KVView &kv, int slot, int kvh, int t0, int kclamp, int kend,
                                          u32x4_t (&kreg)[KU], u32x4_t (&vreg)[KU], bool &bad) {
     StaticFor<0, KU>::run([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        pf_fetch_unit<D, LAYOUT, TK>(kv, slot, kvh, t0, kstart, kend, threadIdx.x + u * NT, kreg[u], vreg[u], bad);
+        pf_fetch_unit<D, LAYOUT, TK>(kv, slot, kvh, t0, kclamp, kend, threadIdx.x + u * NT, kreg[u], vreg[u], bad);
     });
 }
 
@@ -2305,6 +2305,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
     const int wkend = base_pos + min(Qn, qrow0 + 16);
     const int wkstart = a.window > 0 ? max(0, base_pos + qrow0 - a.window + 1) : 0;
     const bool wlive = computes && qrow0 < Qn;
+    const int kblock = kstart;  // the block's first key: a row of the cache
     if (nks > 1) {
         const int span = (kend - kstart + nks - 1) / nks;
         const int part = (span + kPfKeys - 1) / kPfKeys * kPfKeys;
@@ -2312,6 +2313,11 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         kend = min(kend, k0 + part);
         kstart = min(k0, kend);
     }
+    // Rows fetched past the range read row kclamp and are masked: the range's
+    // first key, or the block's first key when the split left this range
+    // empty (kstart == kend can be one past the slot's last row, on a page
+    // not mapped or, in CONTIG storage, past the layer's rows)
+    const int kclamp = kstart < kend ? kstart : kblock;
 
     // Q^T as the B operand: lane (col, grp) holds d = 32c + 8grp .. +7 of query qr.
     uint4 qop[D / 32];
@@ -2473,7 +2479,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                 const int q = wave + i * NW;      // < IPT: K instruction q, else V instruction q - IPT
                 const int ins = q % IPT;
                 const int r = ins * RPI + lrow;   // key row of this lane
-                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, r, bad);
+                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kclamp, kend, r, bad);
                 const uint16_t *gp = (q < IPT ? kg : vg) + off + 8 * (pchunk ^ pf_rswz(r));
                 const uint32_t dst = (q < IPT ? sk_a : sv_a) + stage + (uint32_t)ins * 1024u;
                 dma_load16_cached(gp, __builtin_amdgcn_readfirstlane(dst));
@@ -2521,7 +2527,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         }
     } else if constexpr (PF) {
         // PD tiles in flight in registers (ring slot s holds tiles s, s + PD,
-        // ...; keys past kend read row kstart: in bounds, never visible) and
+        // ...; keys past kend read row kclamp: in bounds, never visible) and
         // two tile buffers in LDS (tile i in buffer i % 2; PD is even). Per
         // tile one barrier: after it, tile i is staged and every wave is done
         // with tile i - 1, whose buffer then takes tile i + 1 while tile i is
@@ -2530,10 +2536,10 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         u32x4_t kreg[PD][KU], vreg[PD][KU];
         StaticFor<0, PD>::run([&](auto pc) {
             constexpr int p = decltype(pc)::value;
-            pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + p * TK, kstart, kend, kreg[p], vreg[p], bad);
+            pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + p * TK, kclamp, kend, kreg[p], vreg[p], bad);
         });
         pf_stage<D, TK, KU, 64 * NW>(sk, sv, kreg[0], vreg[0]);
-        pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + PD * TK, kstart, kend, kreg[0], vreg[0], bad);
+        pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, kstart + PD * TK, kclamp, kend, kreg[0], vreg[0], bad);
         for (int t0 = kstart; t0 < kend; t0 += PD * TK) {
             StaticFor<0, PD>::run([&](auto pc) {
                 constexpr int p = decltype(pc)::value;
@@ -2547,7 +2553,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
                     // still in flight, and it then waits for all of them
                     // (the next tiles' prefetches included) before staging.
                     pf_stage<D, TK, KU, 64 * NW>(sk + (pn % 2) * TILE, sv + (pn % 2) * TILE, kreg[pn], vreg[pn]);
-                    pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, tt + TK + PD * TK, kstart, kend, kreg[pn],
+                    pf_fetch<D, LAYOUT, TK, KU, 64 * NW>(a.kv, slot, kvh, tt + TK + PD * TK, kclamp, kend, kreg[pn],
                                                          vreg[pn], bad);
                     // this wave's 32 keys of the tile (wave-uniform)
                     const int st = tt + part * kPfKeys;
@@ -2569,7 +2575,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
         auto dma_tile = [&](int t0, int buf) __attribute__((always_inline)) {
             for (int rr = wave; rr < 2 * kPfKeys; rr += NW) {  // rr < 32: K row rr, else V row rr - 32
                 const int kr = rr % kPfKeys;
-                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kstart, kend, kr, bad);
+                const int64_t off = pf_row_offset<D, LAYOUT>(a.kv, slot, kvh, t0, kclamp, kend, kr, bad);
                 const uint16_t *g = (rr < kPfKeys ? kg : vg) + off + 8 * (lane ^ pf_swz<D>(kr));
                 const uint32_t dst = (rr < kPfKeys ? sk_a : sv_a) + (uint32_t)(buf * TILE + kr * KP) * 2;
                 dma_load16_cached(g, __builtin_amdgcn_readfirstlane(dst));

@@ -90,6 +90,11 @@ def _check(rt, orc, q, scale, prefill=True):
         (6, 1, 128, 0, "contig", [100, 37], 50),
         (12, 2, 256, 512, "ring", [300], 40),
         (3, 1, 64, 0, "paged", [70], 33),
+        # a key split (one long stream) leaves the short streams' later key
+        # ranges empty: their clamped fetches must stay on mapped pages (the
+        # health check below would report the device flag otherwise)
+        (12, 4, 128, 0, "paged", [31, 839, 241], 1),
+        (8, 2, 64, 0, "paged", [5, 1500], 3),
     ],
 )
 def test_prefill_matches_oracle(hq, hkv, d, window, layout, prefix, qn):

@@ -1,8 +1,10 @@
-"""GPU parity of fused append + decode attention against the fp64 oracle over
-seeded random layer shapes: head_dim 64 / 128 / 256, CONTIG / RING / PAGED,
-bf16 and (PAGED) int8, 1..8 KV heads, GQA groups 1..8, Q 1 / 2, 1..4 ragged
+"""GPU parity against the fp64 oracle over seeded random layer shapes: fused
+append + decode attention (head_dim 64 / 128 / 256, CONTIG / RING / PAGED,
+bf16 and PAGED int8, 1..8 KV heads, GQA groups 1..8, Q 1 / 2, 1..4 ragged
 streams of 1..4000 positions, with and without a window, on the AUTO, VALU and
-MFMA decode kernels. Max-abs 1e-2, as every attention test."""
+MFMA decode kernels) and chunked prefill (head_dim 64..512, GQA groups 1..8
+including 3 and 6, chunks of 1..300 queries over ragged prefixes). Max-abs
+1e-2, as every attention test."""
 from __future__ import annotations
 
 import math
@@ -83,4 +85,61 @@ def test_random_shape_fused_decode_parity(case):
             worst = max(worst, float(np.abs(to_np(out[i]) - ref).max()))
     assert worst <= ATOL, worst
     assert rt.health() == 0
+    rt.close()
+
+
+def _prefill_cases(n_cases: int, seed: int) -> list[tuple]:
+    r = random.Random(seed)
+    out = []
+    while len(out) < n_cases:
+        d = r.choice([64, 128, 256, 512])
+        layout = r.choice(["contig", "ring", "paged"] if d < 512 else ["contig", "paged"])
+        hkv, g = r.choice([1, 2, 4, 8]), r.choice([1, 2, 3, 4, 6, 8])
+        qn = r.choice([1, 5, 16, 33, 100, 300])
+        window = r.choice([64, 300]) if layout == "ring" else r.choice([0, 0, 200])
+        prefix = tuple(r.randint(0, 1500) for _ in range(r.choice([1, 2, 3, 4])))
+        out.append((d, layout, hkv, g, qn, window, prefix))
+    return out
+
+
+PREFILL_CASES = _prefill_cases(20, 11)
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=[
+    f"d{c[0]}-{c[1]}-h{c[2]}g{c[3]}-q{c[4]}-w{c[5]}-n{len(c[6])}" for c in PREFILL_CASES])
+def test_random_shape_prefill_parity(case):
+    """Chunked-prefill attention (kvrt_attend_prefill_async) over seeded random
+    shapes, GQA groups that are not powers of two included."""
+    from kvrt import KVRuntime, LayerSpec
+
+    d, layout, hkv, g, qn, window, prefix = case
+    gen = torch.Generator().manual_seed(d + hkv * 10 + g * 100 + qn * 1000 + sum(prefix))
+    n = len(prefix)
+    cap = max(prefix) + qn + 8
+    kw = {}
+    if layout == "ring":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="ring", window=window, ring_rows=window + qn - 1)
+    elif layout == "paged":
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, layout="paged", window=window)
+        kw = dict(block_size=16, pool_pages=n * ((cap + 15) // 16) + 8, pool_seed=3)
+    else:
+        spec = LayerSpec(kv_heads=hkv, head_dim=d, window=window)
+    rt = KVRuntime([spec], n, cap, max_q=qn, device="cuda", **kw)
+    orc = O.OracleCache([O.OracleLayer(hkv, d, window)], n)
+    for s, p in enumerate(prefix):
+        if p:
+            k, v = randn_bf16(gen, (1, hkv, p, d)), randn_bf16(gen, (1, hkv, p, d))
+            rt.import_(s, 0, k.cuda(), v.cuda())
+            orc.append(s, 0, to_np(k[0]), to_np(v[0]))
+    k, v = randn_bf16(gen, (n, hkv, qn, d)), randn_bf16(gen, (n, hkv, qn, d))
+    rt.append(0, k.cuda(), v.cuda(), list(range(n)))
+    for s in range(n):
+        orc.append(s, 0, to_np(k[s]), to_np(v[s]))
+    q = randn_bf16(gen, (n, hkv * g, qn, d), 0.5)
+    scale = 1.0 / math.sqrt(d)
+    out = rt.attend_prefill(0, q.cuda(), list(range(n)), scale)
+    torch.cuda.synchronize()
+    assert rt.health() == 0
+    worst = max(float(np.abs(to_np(out[s]) - orc.attend(s, 0, to_np(q[s]), scale)).max()) for s in range(n))
+    assert worst <= ATOL, worst
     rt.close()

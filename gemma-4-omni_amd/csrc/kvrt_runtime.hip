@@ -103,8 +103,24 @@ struct kvrt_ctx {
     LayerDesc *d_desc = nullptr;      // device [n_layers] layer descriptions
     kvrt_counters counters{};
 
+    // RING layers, host only [slot * n_layers + layer]: the lowest position
+    // whose row the ring still holds. An append raises it to length -
+    // ring_rows; a rollback leaves it where it is, so a second rollback (or
+    // one after a shorter re-append) cannot reach rows that positions past the
+    // first rollback point overwrote.
+    std::vector<int32_t> ring_lo;
+
     int len_at(int slot, int layer) const { return len[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
     int &len_ref(int slot, int layer) { return len[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
+    int ring_floor(int slot, int layer) const { return ring_lo[(size_t)slot * cfg.n_layers + layers[layer].owner]; }
+    // after the (slot, layer) length grew: rows below length - ring_rows are overwritten
+    void ring_advance(int slot, int layer) {
+        const Layer &o = layers[layers[layer].owner];
+        if (o.spec.layout != KVRT_LAYOUT_RING) return;
+        const size_t i = (size_t)slot * cfg.n_layers + layers[layer].owner;
+        ring_lo[i] = std::max(ring_lo[i], len[i] - o.spec.ring_rows);
+    }
+    void ring_set(int slot, int layer, int lo) { ring_lo[(size_t)slot * cfg.n_layers + layers[layer].owner] = lo; }
 };
 
 namespace {
@@ -585,6 +601,7 @@ int create_impl(const kvrt_config *cfg, const kvrt_layer_spec *specs, const kvrt
     }
     c->layers.resize(cfg->n_layers);
     c->len.assign((size_t)cfg->n_slots * cfg->n_layers, 0);
+    c->ring_lo.assign((size_t)cfg->n_slots * cfg->n_layers, 0);
     c->paged = any_paged;
     auto fail = [&](int code) {
         kvrt_destroy(c);
@@ -746,11 +763,11 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         from[i] = L;
         if (Lnew < qn) return KVRT_ESTATE;
         if (fused && Lnew > c->cfg.capacity) return KVRT_ESTATE;
-        if (s.layout == KVRT_LAYOUT_PAGED) {
-            // the oldest key any query of the call sees must be on a live page
-            const int oldest = s.window > 0 ? std::max(0, Lnew - (int)qn - s.window + 1) : 0;
-            if (oldest < c->first_live[slots[i]] * c->cfg.block_size) return KVRT_ESTATE;
-        }
+        // the oldest key any query of the call sees must be on a live page
+        // (PAGED) or still in the ring (RING, after a rollback)
+        const int oldest = s.window > 0 ? std::max(0, Lnew - (int)qn - s.window + 1) : 0;
+        if (s.layout == KVRT_LAYOUT_PAGED && oldest < c->first_live[slots[i]] * c->cfg.block_size) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING && oldest < c->ring_floor(slots[i], layer)) return KVRT_ESTATE;
         item_keys[i] = talker ? titems[i].audio_pos + 1 : visible_keys(s, Lnew, (int)qn);
         max_keys = std::max<int64_t>(max_keys, item_keys[i]);
     }
@@ -833,6 +850,7 @@ int decode_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
         int &L = c->len_ref(slots[i], layer);
         if (fused) {
             L += (int)qn;
+            c->ring_advance(slots[i], layer);
             c->counters.appended_rows += (uint64_t)qn * hkv;
             c->counters.appended_bytes += (uint64_t)qn * hkv * D * 2 * kb;
         }
@@ -916,6 +934,7 @@ int append_impl(kvrt_ctx *c, int layer, int n, const int32_t *slots, const kvrt_
     const int kb = s.dtype == KVRT_INT8 ? 1 : 2;
     for (int i = 0; i < n; ++i) {
         c->len_ref(slots[i], layer) += (int)qn;
+        c->ring_advance(slots[i], layer);
         c->counters.appended_rows += (uint64_t)qn * hkv;
         c->counters.appended_bytes += (uint64_t)qn * hkv * D * 2 * kb;
     }
@@ -1247,6 +1266,7 @@ int kvrt_grow_slots(kvrt_ctx *c, int32_t n_slots, const kvrt_storage *storage) {
         c->d_pt = d_pt;
     }
     c->len.resize((size_t)n_slots * c->cfg.n_layers, 0);
+    c->ring_lo.resize((size_t)n_slots * c->cfg.n_layers, 0);
     c->slot.resize(n_slots, SlotState{});
     for (int i = old_n; i < n_slots; ++i) renew_generation(c, i);
     c->cfg.n_slots = n_slots;
@@ -1321,6 +1341,7 @@ int kvrt_import_async(kvrt_ctx *c, int32_t slot, int32_t layer, const kvrt_tenso
         if (rc) return rc;
     }
     c->len_ref(slot, layer) = (int)S;
+    c->ring_set(slot, layer, s.layout == KVRT_LAYOUT_RING ? keep_from : 0);  // rows below keep_from are not written
     c->counters.appended_rows += (uint64_t)S * s.kv_heads;
     c->counters.appended_bytes += (uint64_t)S * s.kv_heads * s.head_dim * 2 * (s.dtype == KVRT_INT8 ? 1 : 2);
     // new contents: holders of the slot's previous generation are stale
@@ -1406,6 +1427,7 @@ int kvrt_reset_slot_async(kvrt_ctx *c, int32_t slot) {
             }
         }
         c->len_ref(slot, l) = 0;
+        c->ring_set(slot, l, 0);
         idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
     }
     if (c->paged) {
@@ -1508,7 +1530,8 @@ static int gather_impl(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slo
         else if (s.layout == KVRT_LAYOUT_PAGED) st = std::min(L, c->first_live[slots[i]] * c->cfg.block_size);
         else st = 0;
         if (st < 0 || st > L || L - st > lmax) return KVRT_EINVAL;
-        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && st < L - s.ring_rows) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING && st < std::max(L - s.ring_rows, c->ring_floor(slots[i], layer)))
+            return KVRT_ESTATE;
         if (s.layout == KVRT_LAYOUT_PAGED) {
             for (int p = st / c->cfg.block_size; p * c->cfg.block_size < L; ++p)
                 if (c->pt[(size_t)slots[i] * c->pt_stride + p] < 0) return KVRT_ESTATE;
@@ -1547,6 +1570,7 @@ static int gather_impl(kvrt_ctx *c, int32_t layer, int32_t n, const int32_t *slo
     c->counters.gathered_bytes += (uint64_t)n * s.kv_heads * lmax * s.head_dim * 2 * elem_size(out_dtype);
     for (int i = 0; k && i < n; ++i) {
         c->len_ref(slots[i], layer) += qn;
+        c->ring_advance(slots[i], layer);
         c->counters.appended_rows += (uint64_t)qn * s.kv_heads;
         c->counters.appended_bytes += (uint64_t)qn * s.kv_heads * s.head_dim * 2 * 2;
     }
@@ -1603,7 +1627,11 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
         // the caller's position must be the slot's (rewind_session_async's
         // current_position == valid_kv_len)
         if (new_len > L || (expected_len >= 0 && L != expected_len)) return KVRT_ESTATE;
-        if (s.layout == KVRT_LAYOUT_RING && L > s.ring_rows && new_len - s.window + 1 < L - s.ring_rows)
+        // RING: the keys the next query (position new_len) sees must still be
+        // in the ring; PAGED: no rollback into released pages. A rollback to 0
+        // keeps no rows (a release) and is always possible.
+        if (new_len == 0) continue;
+        if (s.layout == KVRT_LAYOUT_RING && std::max(0, new_len - s.window + 1) < c->ring_floor(slot, l))
             return KVRT_ESTATE;
         if (s.layout == KVRT_LAYOUT_PAGED && new_len < c->first_live[slot] * c->cfg.block_size && new_len < L)
             return KVRT_ESTATE;
@@ -1615,6 +1643,7 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
         c->counters.truncated_rows += (uint64_t)(L - new_len);
         before.push_back(L);
         L = new_len;
+        if (new_len == 0) c->ring_set(slot, l, 0);
         idx.push_back((int32_t)((size_t)slot * c->cfg.n_layers + l));
     }
     if (c->paged) {
@@ -1682,9 +1711,10 @@ int copy_range(const kvrt_ctx *c, int slot, int l, int n, int &lo) {
     const kvrt_layer_spec &s = c->layers[l].spec;
     const int L = c->len_at(slot, l);
     if (n > L) return KVRT_ESTATE;
-    const int need = s.window > 0 ? std::max(0, n - s.window + 1) : 0;
     lo = 0;
-    if (s.layout == KVRT_LAYOUT_RING) lo = std::max(0, std::max(n - s.ring_rows, L - s.ring_rows));
+    if (n == 0) return KVRT_OK;  // nothing to carry
+    const int need = s.window > 0 ? std::max(0, n - s.window + 1) : 0;
+    if (s.layout == KVRT_LAYOUT_RING) lo = std::max({0, n - s.ring_rows, L - s.ring_rows, c->ring_floor(slot, l)});
     else if (s.layout == KVRT_LAYOUT_PAGED) lo = std::min(n, c->first_live[slot] * c->cfg.block_size);
     return lo > need ? KVRT_ESTATE : KVRT_OK;
 }
@@ -1775,6 +1805,7 @@ int copy_slot_impl(kvrt_ctx *dst, int dst_slot, kvrt_ctx *src, int src_slot, int
             if (a.n_entries == kMaxMoveLayers && (rc = flush()) != KVRT_OK) return rc;
         }
         dst->len_ref(dst_slot, l) = n;
+        dst->ring_set(dst_slot, l, s.layout == KVRT_LAYOUT_RING ? lo[l] : 0);
         idx.push_back((int32_t)((size_t)dst_slot * nl + l));
     }
     if ((rc = flush()) != KVRT_OK) return rc;
@@ -1962,7 +1993,8 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
         if (L < qn) return KVRT_ESTATE;
         // the oldest key any query of the chunk can see
         const int oldest = s.window > 0 ? std::max<int64_t>(0, L - qn - s.window + 1) : 0;
-        if (s.layout == KVRT_LAYOUT_RING && L - oldest > s.ring_rows) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_RING && (L - oldest > s.ring_rows || oldest < c->ring_floor(slots[i], layer)))
+            return KVRT_ESTATE;
         if (s.layout == KVRT_LAYOUT_PAGED && oldest < c->first_live[slots[i]] * c->cfg.block_size) return KVRT_ESTATE;
         for (int64_t q0 = 0; q0 < qn; q0 += 16) {
             const int64_t kend = L - qn + std::min<int64_t>(qn, q0 + 16);
@@ -2194,6 +2226,9 @@ int kvrt_sync_lengths(kvrt_ctx *c) {
         if (dev[i] < 0 || dev[i] > c->cfg.capacity) return KVRT_EFAULT;
     }
     c->len = dev;
+    for (int slot = 0; slot < c->cfg.n_slots; ++slot)
+        for (int l = 0; l < c->cfg.n_layers; ++l)
+            if (c->layers[l].owner == l) c->ring_advance(slot, l);
     c->lens_stale = false;
     return KVRT_OK;
 }

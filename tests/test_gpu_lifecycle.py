@@ -177,6 +177,72 @@ def test_copy_prefix_refusals_leave_state_unchanged():
     assert paged.seq_length(1) == 160 and paged.health() == 0
 
 
+def _ring_step(rt, orc, gen, slot=0):
+    """One fused Q1 step on the ring layer, checked against the oracle."""
+    q = randn_bf16(gen, (1, 2, 1, 128), 0.5)
+    k, v = randn_bf16(gen, (1, 1, 1, 128)), randn_bf16(gen, (1, 1, 1, 128))
+    out = rt.append_attend(0, q.cuda(), k.cuda(), v.cuda(), [slot], 0.1)
+    orc.append(slot, 0, to_np(k[0]), to_np(v[0]))
+    torch.cuda.synchronize()
+    return float(np.abs(to_np(out[0]) - orc.attend(slot, 0, to_np(q[0]), 0.1)).max())
+
+
+def test_ring_rollbacks_stop_at_rows_later_positions_overwrote():
+    """A ring of 70 rows under a 64-key window. After 500 positions it holds
+    [430, 500); a rollback to 495 leaves those rows in place, so a second
+    rollback (or one after a shorter re-append) may only go as far as the
+    window of its next query still starts at 430 or later: position 427's row
+    now holds position 497. Rollbacks to 0 (a release) always succeed."""
+    from kvrt import KVRTError, KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(31)
+    rt = KVRuntime([LayerSpec(kv_heads=1, head_dim=128, layout="ring", window=64, ring_rows=70)], 2, 1024,
+                   max_q=2, device="cuda")
+    orc = O.OracleCache([O.OracleLayer(1, 128, 64)], 2)
+    _fill(rt, orc, 0, 0, 500, gen, 1, 128)
+    rt.truncate(0, 495)
+    orc.truncate(0, 0, 495)
+    for bad in (490, 492):  # windows from 427 / 429: overwritten by 497 / 499
+        with pytest.raises(KVRTError) as e:
+            rt.truncate(0, bad)
+        assert e.value.code == -2 and rt.seq_length(0) == 495
+    assert _ring_step(rt, orc, gen) <= ATOL
+    assert _ring_step(rt, orc, gen) <= ATOL       # 497: the ring still remembers 500
+    with pytest.raises(KVRTError):
+        rt.truncate(0, 492)
+    with pytest.raises(KVRTError):                # a clone's next query needs [429, 492]
+        rt.copy_prefix(0, 1, 492)
+    rt.truncate(0, 493)                           # window [430, 493): all resident
+    orc.truncate(0, 0, 493)
+    assert _ring_step(rt, orc, gen) <= ATOL
+    rt.copy_prefix(0, 1, 494)                     # the clone inherits the ring's floor
+    orc.copy_prefix(0, 1, 0, 494)
+    with pytest.raises(KVRTError):
+        rt.truncate(1, 492)
+    assert _ring_step(rt, orc, gen, slot=1) <= ATOL
+    _check_rows(rt, orc, 1, 0, start=495 - 63)
+    # an empty clone and releases of long slots
+    rt.copy_prefix(0, 1, 0)
+    assert rt.seq_length(1) == 0
+    orc.copy_prefix(0, 1, 0, 0)
+    rt.truncate(0, 0)
+    orc.truncate(0, 0, 0)
+    for slot in (0, 1):
+        for _ in range(3):
+            assert _ring_step(rt, orc, gen, slot) <= ATOL
+    assert rt.health() == 0
+    paged = KVRuntime([LayerSpec(kv_heads=1, head_dim=128, layout="paged", window=32)], 1, 1024, max_q=2,
+                      device="cuda", block_size=16, pool_pages=40)
+    x = torch.ones((1, 1, 300, 128), dtype=torch.bfloat16, device="cuda")
+    slot = paged.acquire_slot()
+    paged.import_(slot, 0, x, x)
+    paged.evict(slot, 240)
+    with pytest.raises(KVRTError):               # below the released pages
+        paged.truncate(slot, 200)
+    paged.release_slot(slot)
+    assert paged.seq_length(slot) == 0 and paged.counters()["pages_in_use"] == 0 and paged.health() == 0
+
+
 def test_copy_session_between_contexts():
     from kvrt import KVRTError, KVRuntime, LayerSpec
 

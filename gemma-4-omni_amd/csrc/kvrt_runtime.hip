@@ -1627,14 +1627,14 @@ int kvrt_truncate(kvrt_ctx *c, int32_t slot, int32_t layer, int32_t new_len, uin
         // the caller's position must be the slot's (rewind_session_async's
         // current_position == valid_kv_len)
         if (new_len > L || (expected_len >= 0 && L != expected_len)) return KVRT_ESTATE;
-        // RING: the keys the next query (position new_len) sees must still be
-        // in the ring; PAGED: no rollback into released pages. A rollback to 0
+        // The keys the next query (position new_len) sees must still be
+        // stored: in the ring (RING), on live pages (PAGED with a window;
+        // without one, no rollback into released pages). A rollback to 0
         // keeps no rows (a release) and is always possible.
-        if (new_len == 0) continue;
-        if (s.layout == KVRT_LAYOUT_RING && std::max(0, new_len - s.window + 1) < c->ring_floor(slot, l))
-            return KVRT_ESTATE;
-        if (s.layout == KVRT_LAYOUT_PAGED && new_len < c->first_live[slot] * c->cfg.block_size && new_len < L)
-            return KVRT_ESTATE;
+        if (new_len == 0 || new_len == L) continue;
+        const int need = s.window > 0 ? std::max(0, new_len - s.window + 1) : new_len;
+        if (s.layout == KVRT_LAYOUT_RING && need < c->ring_floor(slot, l)) return KVRT_ESTATE;
+        if (s.layout == KVRT_LAYOUT_PAGED && need < c->first_live[slot] * c->cfg.block_size) return KVRT_ESTATE;
     }
     std::vector<int32_t> idx, before;
     for (int l : targets) {

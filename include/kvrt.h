@@ -377,10 +377,15 @@ int kvrt_append_gather_async(kvrt_ctx *ctx, int32_t layer, int32_t n, const int3
  * check), when new_len exceeds the current length or lies below the slot's
  * prefix-attention mask (the rewind floor), while the host lengths are
  * unverified (work of this context was captured into a graph since the
- * last kvrt_sync_lengths), or when a RING layer would need rows already
- * overwritten (L > ring_rows and new_len - window + 1 < L - ring_rows, i.e.
- * a rollback deeper than ring_rows - window + 1 positions). Nothing changes
- * when it fails. The device applies the edit only where it still holds the
+ * last kvrt_sync_lengths), or when the keys the next query (position
+ * new_len) sees are no longer stored: a RING layer keeps positions from
+ * (its longest length since the slot was last empty) - ring_rows on, a
+ * rollback leaving that floor in place; a PAGED layer with a window keeps
+ * the pages kvrt_evict did not release (without a window, new_len may not
+ * fall below them). new_len == 0 (a release) is always possible; a RING
+ * layer's floor then restarts at 0, and a slot's released pages are
+ * forgotten once all its PAGED layers are empty. Nothing changes when it
+ * fails. The device applies the edit only where it still holds the
  * lengths the host validated against; where a graph replay has advanced
  * them since (replays after a kvrt_sync_lengths), the edit is dropped whole
  * and kvrt_health reports KVRT_EFAULT (kvrt_sync_lengths then reloads the

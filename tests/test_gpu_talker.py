@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import random
 
 import numpy as np
 import pytest
@@ -26,12 +27,13 @@ SCALE = 1.0 / math.sqrt(D)
 class _Talker:
     """A kvrt runtime and its host mirror, filled slot by slot."""
 
-    def __init__(self, n, capacity, seed):
+    def __init__(self, n, capacity, seed, hq=HQ, hkv=HKV, d=D, **kw):
         from kvrt import KVRuntime, LayerSpec
 
-        self.rt = KVRuntime([LayerSpec(kv_heads=HKV, head_dim=D)], n, capacity, max_q=2, device="cuda")
-        self.k = np.zeros((n, HKV, capacity, D), np.float32)
-        self.v = np.zeros((n, HKV, capacity, D), np.float32)
+        self.hq, self.hkv, self.d, self.scale = hq, hkv, d, 1.0 / math.sqrt(d)
+        self.rt = KVRuntime([LayerSpec(kv_heads=hkv, head_dim=d)], n, capacity, max_q=2, device="cuda", **kw)
+        self.k = np.zeros((n, hkv, capacity, d), np.float32)
+        self.v = np.zeros((n, hkv, capacity, d), np.float32)
         self.len = [0] * n
         self.gen = torch.Generator().manual_seed(seed)
 
@@ -39,8 +41,8 @@ class _Talker:
         positions = list(positions)
         for c in range(0, len(positions), 128):
             pos = positions[c:c + 128]
-            k = randn_bf16(self.gen, (1, HKV, len(pos), D), scale)
-            v = randn_bf16(self.gen, (1, HKV, len(pos), D), scale)
+            k = randn_bf16(self.gen, (1, self.hkv, len(pos), self.d), scale)
+            v = randn_bf16(self.gen, (1, self.hkv, len(pos), self.d), scale)
             self.rt.write_positions(0, k.cuda(), v.cuda(), [slot], [pos])
             self.k[slot][:, pos] = to_np(k[0])
             self.v[slot][:, pos] = to_np(v[0])
@@ -64,15 +66,15 @@ class _Talker:
         """Write the step's K/V rows, then attend; returns (out, reference)."""
         pos = [[m.prefix_position, m.audio_position] if q_rows == 2 else [m.audio_position] for m in masks]
         n = len(slots)
-        k = randn_bf16(self.gen, (n, HKV, q_rows, D))
-        v = randn_bf16(self.gen, (n, HKV, q_rows, D))
+        k = randn_bf16(self.gen, (n, self.hkv, q_rows, self.d))
+        v = randn_bf16(self.gen, (n, self.hkv, q_rows, self.d))
         self.rt.write_positions(0, k.cuda(), v.cuda(), slots, pos)
         for i, s in enumerate(slots):
             self.k[s][:, pos[i]] = to_np(k[i])
             self.v[s][:, pos[i]] = to_np(v[i])
             self.len[s] = max(self.len[s], max(pos[i]) + 1)
-        q = randn_bf16(self.gen, (n, HQ, q_rows, D), 0.5)
-        out = self.rt.attend_talker(0, q.cuda(), slots, SCALE, masks)
+        q = randn_bf16(self.gen, (n, self.hq, q_rows, self.d), 0.5)
+        out = self.rt.attend_talker(0, q.cuda(), slots, self.scale, masks)
         torch.cuda.synchronize()
         assert self.rt.health() == 0
         refs = []
@@ -80,7 +82,7 @@ class _Talker:
             L = self.len[s]
             mask = O.talker_mask(q_rows, L, m.prefix_start, m.audio_start, m.prefix_position, m.audio_position,
                                  m.prefix_attention_mode, m.visible_prefix_count, m.prefix_log_gate)
-            refs.append(O.attend_masked(to_np(q[i]), self.k[s][:, :L], self.v[s][:, :L], mask, SCALE))
+            refs.append(O.attend_masked(to_np(q[i]), self.k[s][:, :L], self.v[s][:, :L], mask, self.scale))
         return out, refs
 
 
@@ -214,3 +216,49 @@ def test_invalid_talker_calls_are_refused_before_any_launch():
         ring.attend_talker(0, q, [0], SCALE, [TalkerMask(2, 8, 4, 10)])
     assert e.value.code == L.KVRT_EINVAL
     assert t.rt.health() == 0 and ring.health() == 0
+
+
+def _talker_cases(n_cases: int, seed: int) -> list[tuple]:
+    r = random.Random(seed)
+    out = []
+    while len(out) < n_cases:
+        d, hkv, g, q_rows = r.choice([64, 128, 256, 512]), r.choice([1, 2, 4, 8]), r.choice([1, 2, 4, 8]), r.choice([1, 2])
+        if g * q_rows > 16:
+            continue
+        masks = []
+        for _ in range(r.choice([1, 2, 3, 4])):
+            ps = r.choice([0, r.randint(1, 200)])
+            pp = ps + r.randint(0, 40)
+            as_ = pp + 1 + r.choice([0, r.randint(1, 60)])
+            ap = as_ + r.choice([0, r.randint(1, 60), r.randint(100, 3000)])
+            mode = r.choice([0, 1, 2])
+            count = r.randint(1, 50) if mode == 2 else 0
+            masks.append((ps, as_, pp, ap, mode, count, r.choice([-8.0, -2.0, 0.5])))
+        out.append((d, hkv, g, q_rows, tuple(masks), r.choice([0, 64, 512]), r.randrange(1 << 30)))
+    return out
+
+
+TALKER_CASES = _talker_cases(16, 2718)
+
+
+@pytest.mark.parametrize("case", TALKER_CASES, ids=[
+    f"d{c[0]}-h{c[1]}g{c[2]}-q{c[3]}-n{len(c[4])}-wg{c[5]}" for c in TALKER_CASES])
+def test_random_talker_shapes_and_masks(case):
+    """Seeded random talker steps: head_dim 64..512, 1..8 KV heads, GQA groups
+    1..8, JOINT (Q 2) and audio-only (Q 1) rows, 1..4 sessions each with its
+    own stable text, prefix, reserved and audio ranges (audio tails up to
+    3000 positions), modes 0 / 1 / 2 with random counts and gates, and
+    several workgroup budgets."""
+    from kvrt import TalkerMask
+
+    d, hkv, g, q_rows, ms, wgs, seed = case
+    masks = [TalkerMask(ps, as_, pp, ap, prefix_attention_mode=mode, visible_prefix_count=count,
+                        prefix_log_gate=gate) for ps, as_, pp, ap, mode, count, gate in ms]
+    cap = max(m.audio_position for m in masks) + 8
+    t = _Talker(len(masks), cap, seed, hq=hkv * g, hkv=hkv, d=d, decode_wgs=wgs)
+    for s, m in enumerate(masks):
+        t.fill(s, m, q_rows)
+    slots = list(range(len(masks)))
+    random.Random(seed).shuffle(slots)
+    out, refs = t.step(slots, [masks[s] for s in slots], q_rows)
+    assert _worst(out, refs) <= ATOL

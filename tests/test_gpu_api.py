@@ -333,3 +333,61 @@ def test_golden_attention_vectors_through_the_hip_kernel(name, case):
     out = rt.attend(0, q[None].cuda(), [0], float(case["scale"][0]))
     err = np.abs(to_np(out[0]) - case["out"]).max()
     assert err <= ATOL, err
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_update_crop_and_copy_sequences_match_hf_caches(seed):
+    """Seeded random sequences on a KVRTCache with two global layers and a
+    sliding one, mirrored on transformers' DynamicLayer /
+    DynamicSlidingWindowLayer: appends of 1..4 rows (the returned states and
+    the stored layers bit for bit), crops of the global layers by a negative
+    count, to an absolute length or by 0, and deep copies that must keep their
+    contents while the original moves on."""
+    import random
+
+    from kvrt import KVRTCache, LayerSpec
+    from transformers.cache_utils import DynamicLayer, DynamicSlidingWindowLayer
+
+    r = random.Random(seed)
+    gen = torch.Generator().manual_seed(seed)
+    d, hkv, w = r.choice([64, 128]), r.choice([1, 2]), r.choice([5, 16])
+    rt = _runtime([LayerSpec(kv_heads=hkv, head_dim=d)] * 2
+                  + [LayerSpec(kv_heads=hkv, head_dim=d, layout="ring", window=w, ring_rows=w + 3 + r.choice([0, 6]))],
+                  n_slots=8, capacity=400, max_q=4)
+    cache = KVRTCache(rt)
+    hf = [DynamicLayer(), DynamicLayer(), DynamicSlidingWindowLayer(sliding_window=w)]
+    snaps = []
+    for _ in range(30):
+        op = r.choice(["update"] * 3 + ["crop", "copy"])
+        if op == "update" and cache.get_seq_length(0) + 4 <= 400:
+            q = r.randint(1, 4)
+            for layer in (0, 1):
+                k, v = randn_bf16(gen, (1, hkv, q, d)).cuda(), randn_bf16(gen, (1, hkv, q, d)).cuda()
+                got, want = cache.update(k, v, layer), hf[layer].update(k, v)
+                for a, b in zip(got, want):
+                    np.testing.assert_array_equal(bits(a), bits(b))
+            k, v = randn_bf16(gen, (1, hkv, q, d)), randn_bf16(gen, (1, hkv, q, d))
+            got, want = cache.update(k.cuda(), v.cuda(), 2), hf[2].update(k, v)
+            for a, b in zip(got, want):
+                np.testing.assert_array_equal(bits(a), bits(b))
+        elif op == "crop" and hf[0].is_initialized:
+            L = cache.get_seq_length(0)
+            tokens = r.choice([0, -r.randint(1, 6), r.randint(0, L + 3)])
+            for layer in (0, 1):
+                cache._crop_layer(layer, tokens)
+                hf[layer].crop(tokens)
+                assert cache.get_seq_length(layer) == hf[layer].get_seq_length()
+        elif op == "copy" and hf[0].is_initialized and cache.get_seq_length(0) == cache.get_seq_length(2) \
+                and len(snaps) < 4:
+            snaps.append((copy.deepcopy(cache), [copy.deepcopy(h) for h in hf[:2]]))
+        for layer in (0, 1):
+            if hf[layer].is_initialized:
+                np.testing.assert_array_equal(bits(cache.layers[layer].keys), bits(hf[layer].keys))
+                np.testing.assert_array_equal(bits(cache.layers[layer].values), bits(hf[layer].values))
+    for snap, hfs in snaps:
+        for layer in (0, 1):
+            assert snap.get_seq_length(layer) == hfs[layer].get_seq_length()
+            np.testing.assert_array_equal(bits(snap.layers[layer].keys), bits(hfs[layer].keys))
+        snap.release()
+    cache.release()
+    assert rt.health() == 0 and len(rt._free_slots) == 8

@@ -2664,22 +2664,58 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(PrefillArgs a) {
             make_uint2(pack_bf16x2(o[b][0] * inv, o[b][1] * inv), pack_bf16x2(o[b][2] * inv, o[b][3] * inv));
 }
 
-// Merge of a key-split prefill: one thread per (item, q head, query, dim),
-// the n_ksplit partials in key order (merge_partials), bf16 out.
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int D, int64_t outs) {
+// Merge of a key-split prefill: one thread per (item, q head, query) row and
+// 4 consecutive dims (16-byte partial loads; D is a power of two, dshift =
+// log2(D / 4)), the n_ksplit partials in key order, bf16 out. Per dim the
+// arithmetic is merge_partials<1>'s (batches of 16 in partial order).
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int D, int dshift, int64_t outs4) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= outs) return;
-    const int64_t row = t / D;  // (item, q head, query)
-    const int d = (int)(t % D);
+    if (t >= outs4) return;
+    const int64_t row = t >> dshift;  // (item, q head, query)
+    const int d = (int)(t & ((1 << dshift) - 1)) * 4;
     const int nks = a.n_ksplit;
     const float2 *ml = a.part_ml + row * nks;
     const float *po = a.part_o + row * nks * D + d;
-    float M = kNegBig, L = 0.f, O = 0.f;
-    merge_partials<1>(0, nks, [&](int sp, float2 &m, float &v) {
-        m = ml[sp];
-        v = po[(int64_t)sp * D];
-    }, M, L, O);
-    a.out[t] = f32_to_bf16(L > 0.f ? O / L : 0.f);
+    constexpr int B = 16;
+    float M = kNegBig, L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nks; s0 += B) {
+        float2 m[B];
+        float4 v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int sp = s0 + u;
+            m[u] = make_float2(kNegBig, 0.f);
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (sp < nks) {
+                m[u] = ml[sp];
+                v[u] = *reinterpret_cast<const float4 *>(po + (int64_t)sp * D);
+            }
+        }
+        float bm = M;
+#pragma unroll
+        for (int u = 0; u < B; ++u) bm = fmaxf(bm, m[u].x);
+        const float c = __builtin_amdgcn_exp2f(M - bm);
+        L *= c;
+        O.x *= c;
+        O.y *= c;
+        O.z *= c;
+        O.w *= c;
+        M = bm;
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const float w = __builtin_amdgcn_exp2f(m[u].x - M);
+            L = fmaf(m[u].y, w, L);
+            O.x = fmaf(v[u].x, w, O.x);
+            O.y = fmaf(v[u].y, w, O.y);
+            O.z = fmaf(v[u].z, w, O.z);
+            O.w = fmaf(v[u].w, w, O.w);
+        }
+    }
+    const bool any = L > 0.f;
+    const uint2 packed = make_uint2(pack_bf16x2(any ? O.x / L : 0.f, any ? O.y / L : 0.f),
+                                    pack_bf16x2(any ? O.z / L : 0.f, any ? O.w / L : 0.f));
+    *reinterpret_cast<uint2 *>(a.out + row * D + d) = packed;
 }
 
 // ---------------------------------------------------------------------------
@@ -3069,6 +3105,17 @@ hipError_t launch_decode_talker(const TalkerArgs &a, int head_dim, int rows_per_
     return hipErrorInvalidValue;
 }
 
+// The key-split merge: (item, q head, query) rows x D / 4 threads.
+hipError_t launch_prefill_merge(const PrefillArgs &a, int head_dim, hipStream_t s) {
+    if (head_dim < 4 || (head_dim & (head_dim - 1)) != 0) return hipErrorInvalidValue;
+    int dshift = 0;
+    while ((1 << dshift) < head_dim / 4) ++dshift;
+    const int64_t outs4 = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * (head_dim / 4);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs4 + 255) / 256)), dim3(256), 0, s, a, head_dim,
+                       dshift, outs4);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int hw = a.heads_per_wg;
     if (hw <= 0 || a.group % hw != 0 || hw > kPfMaxHeads) return hipErrorInvalidValue;
@@ -3109,10 +3156,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
         else if (head_dim == 256) e = ks == 1 ? ring(C256{}, I1{}, I1{}) : ring(C256{}, I2{}, I1{});
         else e = ks == 1 ? ring(C128{}, I1{}, I1{}) : ring(C128{}, I2{}, I1{});
         if (e != hipSuccess || a.n_ksplit == 1) return e;
-        const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
-        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim,
-                           outs);
-        return hipGetLastError();
+        return launch_prefill_merge(a, head_dim, s);
     }
     dim3 grid(a.n_ksplit * a.kv.kv_heads * (a.group / hw), a.n_items, (a.qn + 15) / 16);
     // 4 or 8 waves (hw * ks compute); D = 512 keeps no tile in flight across
@@ -3140,9 +3184,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     else if (ks == 2) e = w8 ? go(I8{}, I2{}) : go(I4{}, I2{});
     else e = w8 ? go(I8{}, I4{}) : go(I4{}, I4{});
     if (e != hipSuccess || a.n_ksplit == 1) return e;
-    const int64_t outs = (int64_t)a.n_items * a.kv.kv_heads * a.group * a.qn * head_dim;
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, a, head_dim, outs);
-    return hipGetLastError();
+    return launch_prefill_merge(a, head_dim, s);
 }
 
 hipError_t launch_set_lens(const SetLenArgs &a, hipStream_t s) {

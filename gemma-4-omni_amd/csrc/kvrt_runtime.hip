@@ -2076,8 +2076,9 @@ int kvrt_attend_prefill_async(kvrt_ctx *c, int32_t layer, int32_t n, const int32
     // 76 workgroups on 256 CUs), each block's keys are cut into n_ksplit
     // ranges of >= 256 keys, as many as keep the grid within 256 workgroups
     // (one round: a D 512 workgroup holds 135 KB of LDS, one per CU); a merge
-    // kernel then combines the ranges' partials. Q 291 at D 512: 253.6 us
-    // unsplit, 168.9 / 133.9 / 171.7 / 148.6 us with 2 / 3 / 4 / 6 ranges.
+    // kernel then combines the ranges' partials. Q 291 at D 512: 213.8 us
+    // unsplit, 134.8 / 106.1 / 142.4 / 125.7 us with 2 / 3 / 4 / 6 ranges
+    // (4 ranges: 304 workgroups, a second round).
     // Not inside a capture that would need a larger workspace.
     // KVRT_PF_KSPLIT=1 turns it off, n >= 2 forces n ranges.
     static const int ksplit_env = env_int("KVRT_PF_KSPLIT", 0);

@@ -613,9 +613,12 @@ class KVRuntime:
         Refused (``KVRTError`` code -2, nothing changes) below the slot's prefix
         mask; with a nonzero ``generation``, when the slot has been replaced
         since; with ``expected_len`` >= 0, when a layer's length is not that
-        position; and after a graph capture until :meth:`sync_lengths`
+        position; after a graph capture until :meth:`sync_lengths`
         (rewind_session_async's identity and position checks,
-        impl.inc:3588-3618). A rollback the host accepted against lengths that
+        impl.inc:3588-3618); and when the next query's window would need a row
+        the layer no longer stores (a RING row a later position overwrote, a
+        page :meth:`evict` released). ``new_len`` 0 always succeeds (a
+        release). A rollback the host accepted against lengths that
         graph replays have since advanced is dropped on the device and
         reported by :meth:`health` (code -6)."""
         self._bind()

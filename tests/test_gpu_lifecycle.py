@@ -215,6 +215,19 @@ def test_ring_rollbacks_stop_at_rows_later_positions_overwrote():
     rt.truncate(0, 493)                           # window [430, 493): all resident
     orc.truncate(0, 0, 493)
     assert _ring_step(rt, orc, gen) <= ATOL
+    # a copy into another context of the same topology carries the floor too
+    other = KVRuntime([LayerSpec(kv_heads=1, head_dim=128, layout="ring", window=64, ring_rows=70)], 1, 1024,
+                      max_q=2, device="cuda")
+    with pytest.raises(KVRTError):
+        other.copy_session(0, rt, 0, 492)
+    other.copy_session(0, rt, 0, 494)
+    with pytest.raises(KVRTError):
+        other.truncate(0, 492)
+    orc_other = O.OracleCache([O.OracleLayer(1, 128, 64)], 1)
+    orc_other.append(0, 0, *orc.values(0, 0))
+    orc_other.truncate(0, 0, 494)
+    assert _ring_step(other, orc_other, gen) <= ATOL
+    assert other.health() == 0
     rt.copy_prefix(0, 1, 494)                     # the clone inherits the ring's floor
     orc.copy_prefix(0, 1, 0, 494)
     with pytest.raises(KVRTError):

@@ -169,3 +169,49 @@ def test_even_physical_q_with_pad_row_truncation_equals_the_logical_q(logical_q)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert rts[0].health() == 0 and rts[1].health() == 0
+
+
+# the prefill benchmark's cases: name, streams, Hq, Hkv, D, Q, prefix, window
+BENCH_SHAPES = [
+    ("thinker_sliding_q291", 4, 8, 1, 256, 291, 2048, 512),
+    ("thinker_full_d512_q291", 4, 8, 1, 512, 291, 2048, 0),
+    ("talker_prefill_q512", 4, 16, 8, 128, 512, 0, 0),
+    ("thinker_prefill_q2048", 1, 8, 1, 256, 2048, 0, 0),
+    ("thinker_full_d512_q2048", 4, 8, 1, 512, 2048, 2048, 0),
+]
+
+
+@pytest.mark.parametrize("name,n,hq,hkv,d,qn,prefix,window", BENCH_SHAPES, ids=[c[0] for c in BENCH_SHAPES])
+def test_prefill_at_the_benchmark_shapes_on_sampled_rows(name, n, hq, hkv, d, qn, prefix, window):
+    """The full-size chunks the prefill benchmark times (key-split grids,
+    query-block pairs, the D 512 path, a wrapped ring): every q head of 12
+    query rows per stream (the first, the last and 10 seeded others) against
+    the oracle, which attends those rows only."""
+    import random
+
+    from kvrt import KVRuntime, LayerSpec
+
+    gen = torch.Generator().manual_seed(qn + d + prefix)
+    layout = "ring" if window else "contig"
+    spec = LayerSpec(kv_heads=hkv, head_dim=d, layout=layout, window=window,
+                     ring_rows=window + qn - 1 if window else 0)
+    L = prefix + qn
+    rt = KVRuntime([spec], n, L + 8, max_q=qn, device="cuda")
+    ks, vs = [], []
+    for s in range(n):
+        k, v = randn_bf16(gen, (1, hkv, L, d)), randn_bf16(gen, (1, hkv, L, d))
+        rt.import_(s, 0, k.cuda(), v.cuda())
+        ks.append(to_np(k[0]))
+        vs.append(to_np(v[0]))
+    q = randn_bf16(gen, (n, hq, qn, d), 0.5)
+    scale = 1.0 / math.sqrt(d)
+    out = rt.attend_prefill(0, q.cuda(), list(range(n)), scale)
+    torch.cuda.synchronize()
+    assert rt.health() == 0
+    r = random.Random(qn * 7 + d)
+    worst = 0.0
+    for s in range(n):
+        rows = sorted({0, qn - 1, *r.sample(range(qn), min(qn, 10))})
+        ref = O.attend(to_np(q[s])[:, rows], ks[s], vs[s], np.array([L - qn + i for i in rows]), scale, window)
+        worst = max(worst, float(np.abs(to_np(out[s])[:, rows] - ref).max()))
+    assert worst <= ATOL, worst
